@@ -1,0 +1,160 @@
+// A1: per-row fp8-e4m3fn quantisation with an fp32 (optionally UE8M0) scale.
+//
+// Semantics follow the reference device kernel
+// operators/deepseek_v32/indexer/quantization.py:34-60: NaN-propagating row
+// amax, clamp_min(1e-4), scale = amax * fl32(1/448), UE8M0 = round the scale
+// bits up to a power of two, y = clamp(x / scale, +-448) cast with RNE.
+// NaN follows the reference GPU's canonical NaN (scale 0x7FFFFFFF, code 0x7F).
+//
+// Layout: rows of `dim` elements with a row stride; the D=128 bf16 path is
+// the model's shape (index K [tokens,128], index Q [tokens*64,128]) and uses
+// 16 lanes per row, 8 bf16 (one 16-byte load) per lane. Other shapes and
+// dtypes use one wave per row.
+#include "dsa_common.h"
+#include "../../include/dsa_gfx950.h"
+
+namespace dsa {
+namespace {
+
+template <int kWidth>
+__device__ __forceinline__ uint32_t max_abs_bits_reduce(uint32_t v) {
+  // |x| as fp32 bits orders like the magnitude; any NaN (bits > 0x7F800000)
+  // wins, which is the NaN-propagating max the reference uses.
+#pragma unroll
+  for (int offset = kWidth / 2; offset > 0; offset >>= 1) {
+    uint32_t o = __shfl_xor(v, offset, kWidth);
+    v = v > o ? v : o;
+  }
+  return v;
+}
+
+__device__ __forceinline__ float scale_from_amax_bits(uint32_t amax_bits, bool ue8m0) {
+  uint32_t bits;
+  if (amax_bits > 0x7F800000u) {
+    bits = kCanonicalNan;
+  } else {
+    float amax = fmaxf(__uint_as_float(amax_bits), 1e-4f);
+    bits = __float_as_uint(amax * kReciprocal448);
+    if (ue8m0) bits = (bits + 0x7FFFFFu) & 0x7F800000u;
+  }
+  return __uint_as_float(bits);
+}
+
+__device__ __forceinline__ uint32_t quantize_one(float v, float scale, float inverse, bool ue8m0) {
+  float y = ue8m0 ? v * inverse : __fdiv_rn(v, scale);
+  if (y != y) return 0x7Fu;
+  y = fminf(fmaxf(y, -448.0f), 448.0f);
+  return f32_to_e4m3fn(y);
+}
+
+// 16 lanes per 128-wide bf16 row; each lane owns 8 consecutive values.
+__global__ __launch_bounds__(256) void quantize_bf16_d128(const uint16_t* __restrict__ x,
+                                                          int64_t rows, int64_t row_stride,
+                                                          uint8_t* __restrict__ y,
+                                                          float* __restrict__ scales, int ue8m0) {
+  const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;
+  const int part = threadIdx.x & 15;
+  const bool live = row < rows;
+  uint4 raw = make_uint4(0, 0, 0, 0);
+  if (live) raw = *reinterpret_cast<const uint4*>(x + row * row_stride + part * 8);
+  uint32_t words[4] = {raw.x, raw.y, raw.z, raw.w};
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = bf16_to_f32(words[i] & 0xFFFFu);
+    v[2 * i + 1] = bf16_to_f32(words[i] >> 16);
+  }
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    uint32_t a = __float_as_uint(v[i]) & 0x7FFFFFFFu;
+    m = m > a ? m : a;
+  }
+  m = max_abs_bits_reduce<16>(m);
+  if (!live) return;
+  const float scale = scale_from_amax_bits(m, ue8m0 != 0);
+  const float inverse = 1.0f / scale;
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) lo |= quantize_one(v[i], scale, inverse, ue8m0 != 0) << (8 * i);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) hi |= quantize_one(v[4 + i], scale, inverse, ue8m0 != 0) << (8 * i);
+  *reinterpret_cast<uint2*>(y + row * 128 + part * 8) = make_uint2(lo, hi);
+  if (part == 0) scales[row] = scale;
+}
+
+template <typename T>
+__device__ __forceinline__ float load_as_f32(const T* p);
+template <>
+__device__ __forceinline__ float load_as_f32<uint16_t>(const uint16_t* p) {
+  return bf16_to_f32(*p);
+}
+template <>
+__device__ __forceinline__ float load_as_f32<_Float16>(const _Float16* p) {
+  return (float)*p;
+}
+template <>
+__device__ __forceinline__ float load_as_f32<float>(const float* p) {
+  return *p;
+}
+
+// One wave per row, any width and dtype (bf16 bits, fp16, fp32).
+template <typename T>
+__global__ __launch_bounds__(256) void quantize_generic(const T* __restrict__ x, int64_t rows,
+                                                        int64_t dim, int64_t row_stride,
+                                                        uint8_t* __restrict__ y,
+                                                        float* __restrict__ scales, int ue8m0) {
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const T* src = x + row * row_stride;
+  uint32_t m = 0;
+  for (int64_t i = lane; i < dim; i += 64) {
+    uint32_t a = __float_as_uint(load_as_f32<T>(src + i)) & 0x7FFFFFFFu;
+    m = m > a ? m : a;
+  }
+  m = max_abs_bits_reduce<64>(m);
+  const float scale = scale_from_amax_bits(m, ue8m0 != 0);
+  const float inverse = 1.0f / scale;
+  for (int64_t i = lane; i < dim; i += 64)
+    y[row * dim + i] = (uint8_t)quantize_one(load_as_f32<T>(src + i), scale, inverse, ue8m0 != 0);
+  if (lane == 0) scales[row] = scale;
+}
+
+}  // namespace
+}  // namespace dsa
+
+extern "C" int dsa_quantize_fp8_rows(const void* x, int dtype, int64_t rows, int64_t dim,
+                                     int64_t row_stride, void* out_codes, float* out_scales,
+                                     int ue8m0, hipStream_t stream) {
+  using namespace dsa;
+  DSA_CHECK_ARG(rows >= 0 && dim >= 1 && row_stride >= dim, "invalid quantize shape");
+  DSA_CHECK_ARG(dtype == DSA_DTYPE_BF16 || dtype == DSA_DTYPE_F16 || dtype == DSA_DTYPE_F32,
+                "quantize supports bf16, fp16 and fp32 inputs");
+  if (rows == 0) return kOk;
+  DSA_CHECK_ARG(x && out_codes && out_scales, "null pointer");
+  uint8_t* y = static_cast<uint8_t*>(out_codes);
+  const bool vector_path = dtype == DSA_DTYPE_BF16 && dim == 128 && row_stride % 8 == 0 &&
+                           (reinterpret_cast<uintptr_t>(x) % 16) == 0;
+  if (vector_path) {
+    const int64_t threads = rows * 16;
+    const int64_t blocks = (threads + 255) / 256;
+    hipLaunchKernelGGL(quantize_bf16_d128, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       static_cast<const uint16_t*>(x), rows, row_stride, y, out_scales, ue8m0);
+  } else {
+    const int64_t blocks = (rows + 3) / 4;
+    if (dtype == DSA_DTYPE_BF16)
+      hipLaunchKernelGGL(quantize_generic<uint16_t>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                         static_cast<const uint16_t*>(x), rows, dim, row_stride, y, out_scales,
+                         ue8m0);
+    else if (dtype == DSA_DTYPE_F16)
+      hipLaunchKernelGGL(quantize_generic<_Float16>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                         static_cast<const _Float16*>(x), rows, dim, row_stride, y, out_scales,
+                         ue8m0);
+    else
+      hipLaunchKernelGGL(quantize_generic<float>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                         static_cast<const float*>(x), rows, dim, row_stride, y, out_scales, ue8m0);
+  }
+  DSA_CHECK_LAUNCH("quantize");
+  return kOk;
+}

@@ -1,0 +1,193 @@
+"""DSA indexer operators on MI355X: fp8 quantisation, fp8 MQA logits, exact top-k.
+
+Drop-in for the reference's indexer operators (same names, argument order,
+validation messages and output layouts):
+
+* ``quantize_index``  - ``operators/deepseek_v32/indexer/quantization.py:63-88``
+* ``logits``          - ``operators/deepseek_v32/indexer/echo.py:299-410``
+  (resident branch; the fused ECHO prefetch branch ``:412-483`` is replaced by
+  the top-k-driven gather in ``cxldsagr_amd.token_pool``)
+* ``exact_topk``      - ``operators/deepseek_v32/indexer/selection.py:62-113``
+
+All work runs in hand-written gfx950 kernels (``csrc/quantize.hip``,
+``csrc/logits.hip``, ``csrc/topk.hip``) on the caller's current stream, with
+no host synchronisation.
+"""
+
+import torch
+
+from cxldsagr_amd import _native
+
+SCORE_ALIGNMENT = 256
+
+
+def _check_tensor(tensor, shape, dtype, device, name):
+    """Mirror of ``echo.py:86-95``."""
+    if (
+        not isinstance(tensor, torch.Tensor)
+        or tuple(tensor.shape) != tuple(shape)
+        or tensor.dtype != dtype
+        or tensor.device != device
+        or not tensor.is_contiguous()
+        or tensor.requires_grad
+    ):
+        raise ValueError(f"{name} must be contiguous {dtype} {tuple(shape)} on {device}")
+
+
+def quantize_index(x, scale_fmt="ue8m0"):
+    """Quantize each last-dimension row, returning contiguous FP8 and FP32 ``[..., 1]``.
+
+    Same arithmetic as the reference device kernel (``quantization.py:34-60``):
+    NaN-propagating amax, ``clamp_min(1e-4)``, ``scale = amax * fl32(1/448)``,
+    UE8M0 rounds the scale up to a power of two, RNE e4m3fn cast of
+    ``clamp(x / scale, -448, 448)``. Accepts bf16, fp16 and fp32 in any layout
+    (non-unit last-dim strides are copied first).
+    """
+    if scale_fmt not in ("ue8m0", None):
+        raise ValueError("Unsupported indexer quantization scale format")
+    if not isinstance(x, torch.Tensor) or x.ndim == 0:
+        raise ValueError("quantize_index expects a tensor with a last dimension")
+    if x.dtype not in _native.DTYPE_CODES:
+        raise ValueError("quantize_index supports bf16, fp16 and fp32 inputs")
+    _native.require_gfx950(x.device, "indexer quantization")
+    dim = x.shape[-1]
+    if dim == 0:
+        raise ValueError("quantize_index needs a nonempty last dimension")
+    data = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=x.device)
+    scales = torch.empty((*x.shape[:-1], 1), dtype=torch.float32, device=x.device)
+    rows = x.numel() // dim
+    if rows == 0:
+        return data, scales
+    # Rows must sit at a uniform stride with unit element stride; other
+    # layouts are copied on the device first.
+    if x.is_contiguous():
+        source, row_stride = x, dim
+    elif x.ndim == 2 and x.stride(1) == 1:
+        source, row_stride = x, x.stride(0)
+    else:
+        source, row_stride = x.contiguous(), dim
+    with torch.cuda.device(x.device):
+        _native.call(
+            "dsa_quantize_fp8_rows",
+            _native.ptr(source),
+            _native.DTYPE_CODES[x.dtype],
+            rows,
+            dim,
+            row_stride,
+            _native.ptr(data),
+            _native.ptr(scales),
+            1 if scale_fmt == "ue8m0" else 0,
+            _native.stream_of(x.device),
+        )
+    return data, scales
+
+
+def padded_columns(columns):
+    return (columns + SCORE_ALIGNMENT - 1) // SCORE_ALIGNMENT * SCORE_ALIGNMENT
+
+
+def logits(q, k, weights, kscale, query_start, prefetch=None, *, _bounds=None,
+           _pad_to_stride=False):
+    """Return causal FP32 ``[Q,N]`` logits with a padded physical row stride.
+
+    ``out[i, j] = kscale[j] * sum_h weights[i, h] * relu(q[i, h] . k[j])`` for
+    ``starts[i] <= j < ends[i]`` and ``-inf`` elsewhere; the default bounds are
+    ``[0, query_start + i + 1)``. Storage is ``[Q, ceil(N/256)*256]`` with every
+    padded column ``-inf``; ``_pad_to_stride`` returns that whole contiguous
+    matrix, otherwise the logical ``[Q, N]`` view of it (``echo.py:318-322``).
+
+    ``prefetch`` must be ``None``: the reference's fused ECHO prefetch is
+    replaced in this build by the top-k-driven gather (``token_pool``).
+    """
+    if q.ndim != 3 or q.shape[1:] != (64, 128) or not q.is_cuda or len(q) < 1:
+        raise ValueError("ECHO requires nonempty CUDA Q[query,64,128]")
+    if k.ndim != 2 or k.shape[1] != 128 or len(k) < 1:
+        raise ValueError("ECHO requires nonempty K[token,128]")
+    rows, columns, device = len(q), len(k), q.device
+    if type(_pad_to_stride) is not bool:
+        raise ValueError("_pad_to_stride must be boolean")
+    if type(query_start) is not int or not 0 <= query_start <= columns - rows:
+        raise ValueError("query_start must place all query rows inside the visible KV sequence")
+    if prefetch is not None:
+        raise NotImplementedError(
+            "fused ECHO prefetch is replaced by the top-k-driven gather (token_pool)"
+        )
+    _native.require_gfx950(device, "fp8 MQA logits")
+    for tensor, shape, dtype, name in (
+        (q, (rows, 64, 128), torch.float8_e4m3fn, "q"),
+        (k, (columns, 128), torch.float8_e4m3fn, "k"),
+        (weights, (rows, 64), torch.float32, "weights"),
+        (kscale, (columns,), torch.float32, "kscale"),
+    ):
+        _check_tensor(tensor, shape, dtype, device, name)
+    starts = ends = None
+    if _bounds is not None:
+        starts, ends = _bounds
+        _check_tensor(starts, (rows,), torch.int32, device, "starts")
+        _check_tensor(ends, (rows,), torch.int32, device, "ends")
+    width = padded_columns(columns)
+    output = torch.empty((rows, width), dtype=torch.float32, device=device)
+    with torch.cuda.device(device):
+        _native.call(
+            "dsa_indexer_logits_fp8",
+            _native.ptr(q),
+            _native.ptr(k),
+            _native.ptr(weights),
+            _native.ptr(kscale),
+            _native.ptr(starts),
+            _native.ptr(ends),
+            query_start,
+            rows,
+            columns,
+            width,
+            _native.ptr(output),
+            _native.stream_of(device),
+        )
+    return output if _pad_to_stride else output[:, :columns]
+
+
+def exact_topk(scores, k):
+    """Return descending values and int32 token IDs; nonfinite slots use -1.
+
+    ``scores`` is FP32 ``[query, visible_tokens]`` (any row stride, unit column
+    stride preferred). Order is descending by the fp32 radix key (``-0.0`` below
+    ``+0.0``), ties to the smaller index (SMALL), matching FlashInfer's
+    deterministic radix top-k with the reference's mask (``selection.py:62-113``).
+    Capacity is ``min(k, visible_tokens)``.
+    """
+    if (
+        not isinstance(scores, torch.Tensor)
+        or scores.ndim != 2
+        or scores.shape[1] < 1
+        or scores.dtype != torch.float32
+        or scores.requires_grad
+    ):
+        raise ValueError("scores must be inference FP32 [query, nonempty visible_tokens]")
+    if type(k) is not int or not 1 <= k <= 2048:
+        raise ValueError("k must be an integer in [1, 2048]")
+    if not scores.is_cuda:
+        raise NotImplementedError("DSA exact selection requires an MI355X (gfx950) HIP device")
+    _native.require_gfx950(scores.device, "DSA exact selection")
+    rows, columns = scores.shape
+    count = min(k, columns)
+    device = scores.device
+    values = torch.empty((rows, count), dtype=torch.float32, device=device)
+    indices = torch.empty((rows, count), dtype=torch.int32, device=device)
+    if rows == 0:
+        return values, indices
+    if scores.stride(1) != 1 or scores.stride(0) < columns:
+        scores = scores.contiguous()
+    with torch.cuda.device(device):
+        _native.call(
+            "dsa_topk_radix",
+            _native.ptr(scores),
+            rows,
+            columns,
+            scores.stride(0),
+            k,
+            _native.ptr(values),
+            _native.ptr(indices),
+            count,
+            _native.stream_of(device),
+        )
+    return values, indices
