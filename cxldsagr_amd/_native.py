@@ -27,6 +27,10 @@ SIGNATURES = {
     "dsa_indexer_logits_fp8": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _ptr,
                                _ptr],
     "dsa_topk_radix": [_ptr, _i64, _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr],
+    "dsa_kv_pack_fp8": [_ptr, _i64, _i64, _ptr, _i64, _ptr, _ptr, _ptr],
+    "dsa_sparse_mla_bf16": [_ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _f32, _ptr, _ptr],
+    "dsa_sparse_mla_fp8_paged": [_ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i64, _f32,
+                                 _ptr, _ptr],
 }
 
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}

@@ -158,3 +158,78 @@ extern "C" int dsa_quantize_fp8_rows(const void* x, int dtype, int64_t rows, int
   DSA_CHECK_LAUNCH("quantize");
   return kOk;
 }
+
+namespace dsa {
+namespace {
+
+// A8 producer: pack bf16 latent+RoPE tokens (576 values) into the 656-byte
+// fp8 paged record. One wave per token: lane l quantises 8 values of latent
+// tile l/16 (the A1 rule, UE8M0 scale per 128-value tile); lanes 0-7 copy the
+// 64 RoPE bf16 values.
+__global__ __launch_bounds__(256) void kv_pack_fp8(const uint16_t* __restrict__ kv,
+                                                   int64_t tokens, int64_t token_offset,
+                                                   const int32_t* __restrict__ page_table,
+                                                   int64_t pages, uint8_t* __restrict__ cache,
+                                                   int32_t* __restrict__ status) {
+  const int64_t token = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (token >= tokens) return;
+  const int64_t logical = token_offset + token;
+  const int64_t page = page_table[logical / 64];
+  if (page < 0 || page >= pages) {
+    if (lane == 0 && status) atomicOr(status, 1);
+    return;
+  }
+  uint8_t* rec = cache + (page * 64 + logical % 64) * 656;
+  const uint16_t* src = kv + token * 576;
+  const int tile = lane >> 4;
+  const int part = lane & 15;
+  const uint4 raw = *reinterpret_cast<const uint4*>(src + tile * 128 + part * 8);
+  const uint32_t words[4] = {raw.x, raw.y, raw.z, raw.w};
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = bf16_to_f32(words[i] & 0xFFFFu);
+    v[2 * i + 1] = bf16_to_f32(words[i] >> 16);
+  }
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    uint32_t a = __float_as_uint(v[i]) & 0x7FFFFFFFu;
+    m = m > a ? m : a;
+  }
+  m = max_abs_bits_reduce<16>(m);
+  const float scale = scale_from_amax_bits(m, true);
+  const float inverse = 1.0f / scale;
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) lo |= quantize_one(v[i], scale, inverse, true) << (8 * i);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) hi |= quantize_one(v[4 + i], scale, inverse, true) << (8 * i);
+  *reinterpret_cast<uint2*>(rec + tile * 128 + part * 8) = make_uint2(lo, hi);
+  if (part == 0) *reinterpret_cast<float*>(rec + 512 + 4 * tile) = scale;
+  if (lane < 8)
+    *reinterpret_cast<uint4*>(rec + 528 + lane * 16) =
+        *reinterpret_cast<const uint4*>(src + 512 + lane * 8);
+}
+
+}  // namespace
+}  // namespace dsa
+
+extern "C" int dsa_kv_pack_fp8(const void* kv, int64_t tokens, int64_t token_offset,
+                               const int32_t* page_table, int64_t pages, void* cache,
+                               int32_t* status, hipStream_t stream) {
+  using namespace dsa;
+  DSA_CHECK_ARG(tokens >= 0 && token_offset >= 0 && pages >= 0, "invalid pack shape");
+  DSA_CHECK_ARG(token_offset + tokens <= pages * 64, "tokens exceed the paged cache");
+  if (tokens == 0) return kOk;
+  DSA_CHECK_ARG(kv && page_table && cache, "null pointer");
+  DSA_CHECK_ARG(reinterpret_cast<uintptr_t>(kv) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(cache) % 16 == 0,
+                "kv and cache must be 16-byte aligned");
+  hipLaunchKernelGGL(kv_pack_fp8, dim3((unsigned)((tokens + 3) / 4)), dim3(256), 0, stream,
+                     static_cast<const uint16_t*>(kv), tokens, token_offset, page_table, pages,
+                     static_cast<uint8_t*>(cache), status);
+  DSA_CHECK_LAUNCH("fp8 KV pack");
+  return kOk;
+}

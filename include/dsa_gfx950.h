@@ -78,6 +78,44 @@ int dsa_indexer_logits_fp8(const void* q, const void* k, const float* weights,
 int dsa_topk_radix(const float* scores, int64_t rows, int64_t columns, int64_t ld, int64_t k,
                    float* values, int32_t* indices, int64_t out_ld, hipStream_t stream);
 
+
+/*
+ * A8 producer - pack bf16 [tokens, 576] (512 latent + 64 RoPE) into the
+ * 656-byte fp8 paged record: 4 e4m3 tiles of 128 (A1 rule, UE8M0), 4 fp32
+ * tile scales, 64 raw bf16 RoPE values. Token i goes to logical position
+ * token_offset + i, physical row page_table[pos / 64] * 64 + pos % 64 of
+ * cache uint8 [pages * 64, 656]. A page number outside [0, pages) skips the
+ * token and ORs 1 into *status (may be NULL). No reference counterpart: the
+ * reference appends bf16 records (models/deepseek_v32/attention.py:400-401).
+ */
+int dsa_kv_pack_fp8(const void* kv, int64_t tokens, int64_t token_offset,
+                    const int32_t* page_table, int64_t pages, void* cache, int32_t* status,
+                    hipStream_t stream);
+
+/*
+ * A7 - sparse MLA over flat bf16 records. Replaces sparse_mla /
+ * sparse_mla_from_pool (FlashMLA flash_mla_sparse_fwd),
+ * operators/deepseek_v32/attention/device_only/mla.py:156-181 and
+ * operators/deepseek_v32/attention/offload/mla.py:12-20.
+ * q: bf16 [rows, heads, 576] (heads a multiple of 64); kv: bf16
+ * [kv_rows, 576]; indices: int32 [rows, topk], ids outside [0, kv_rows) are
+ * padding; out: bf16 [rows, heads, 512]. softmax scale `scale`.
+ */
+int dsa_sparse_mla_bf16(const void* q, int64_t rows, int64_t heads, const void* kv,
+                        int64_t kv_rows, const int32_t* indices, int64_t topk, float scale,
+                        void* out, hipStream_t stream);
+
+/*
+ * A7 over the A8 fp8 paged cache (no reference counterpart; same semantics
+ * as dsa_sparse_mla_bf16 on the dequantised records). cache: uint8
+ * [pages * 64, 656]; page_table: int32 logical page -> physical page; ids
+ * outside [0, n_tokens) (or mapped outside the cache) are padding.
+ */
+int dsa_sparse_mla_fp8_paged(const void* q, int64_t rows, int64_t heads, const void* cache,
+                             int64_t pages, const int32_t* page_table, int64_t n_tokens,
+                             const int32_t* indices, int64_t topk, float scale, void* out,
+                             hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

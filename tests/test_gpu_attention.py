@@ -1,0 +1,237 @@
+"""GPU parity of sparse MLA (A7) and the fp8 paged record (A8) with the oracle.
+
+Cases follow operators/deepseek_v32/attention/device_only/tests/
+test_deepseek_mla.py, offload/tests/test_deepseek_offload_mla.py and the
+reference oracle's known answers. Tolerances: the reference test's
+atol 4e-3 / rtol 2e-2, plus the north-star bar cosine >= 0.9999 and
+max-abs <= 2e-2 against the fp32 oracle.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fp8 as ofp8
+from oracle import kv_fp8 as okv
+from oracle import sparse_mla as omla
+
+pytestmark = pytest.mark.gpu
+
+SCALE = 576**-0.5
+
+
+def _oracle(q, kv, ids, scale, value_dim=512):
+    _, ref = omla.sparse_mla(q.float().cpu().numpy(), kv.float().cpu().numpy(),
+                             ids.cpu().numpy(), scale, value_dim)
+    return ref
+
+
+def _assert_attention_close(actual, ref):
+    a = actual.float().cpu().numpy()
+    np.testing.assert_allclose(a, ref, atol=4e-3, rtol=2e-2)
+    assert np.abs(a - ref).max() <= 2e-2
+    flat_a, flat_r = a.ravel().astype(np.float64), ref.ravel().astype(np.float64)
+    denom = np.linalg.norm(flat_a) * np.linalg.norm(flat_r)
+    if denom > 0:
+        assert flat_a @ flat_r / denom >= 0.9999
+
+
+@pytest.mark.parametrize(
+    ("heads", "queries", "selected"),
+    [(64, 3, 1), (64, 3, 127), (128, 3, 129), (128, 3, 2048), (128, 65, 137)],
+)
+def test_matches_fp32_oracle_with_strides_masks_and_duplicates(gpu, heads, queries, selected):
+    from cxldsagr_amd.attention import sparse_mla
+
+    torch.manual_seed(427)
+    q = torch.randn(queries, heads * 2, 1152, device=gpu, dtype=torch.bfloat16)[:, ::2, ::2]
+    kv = torch.randn(846, 1152, device=gpu, dtype=torch.bfloat16)[::2, ::2]
+    ids = torch.randint(1, len(kv), (queries, selected * 2), device=gpu, dtype=torch.int32)[:, ::2]
+    kv[0] = float("nan")
+    ids[0] = -1
+    ids[1, ::7] = len(kv) + 10
+    if selected >= 3:
+        ids[2, :3] = torch.tensor([1, 1, 2], device=gpu, dtype=torch.int32)
+    actual = sparse_mla(q, kv, ids, SCALE)
+    _assert_attention_close(actual, _oracle(q, kv, ids, SCALE))
+    assert torch.equal(actual[0], torch.zeros_like(actual[0]))
+    split = torch.cat([sparse_mla(q[s:s + 16], kv, ids[s:s + 16], SCALE)
+                       for s in range(0, len(q), 16)])
+    assert torch.equal(actual.view(torch.int16), split.view(torch.int16))
+
+
+def test_int64_invalid_ids_cannot_wrap_into_valid_records(gpu):
+    from cxldsagr_amd.attention import sparse_mla
+
+    q = torch.zeros(2, 64, 576, device=gpu, dtype=torch.bfloat16)
+    kv = torch.full((4, 576), 7, device=gpu, dtype=torch.bfloat16)
+    kv[0] = float("nan")
+    kv[1, :512] = 2
+    ids = torch.full((2, 129), 2**32 + 1, device=gpu, dtype=torch.int64)
+    ids[0, 1] = -(2**32) + 1
+    ids[1, 0] = 1
+    actual = sparse_mla(q, kv, ids, 1)
+    assert torch.equal(actual[0], torch.zeros_like(actual[0]))
+    assert torch.equal(actual[1], torch.full_like(actual[1], 2))
+
+
+def test_contiguous_storage_offsets_are_realigned(gpu):
+    from cxldsagr_amd.attention import sparse_mla
+
+    torch.manual_seed(294)
+    q = torch.randn(3 * 128 * 576 + 1, device=gpu, dtype=torch.bfloat16)[1:].view(3, 128, 576)
+    kv = torch.randn(17 * 576 + 1, device=gpu, dtype=torch.bfloat16)[1:].view(17, 576)
+    assert q.data_ptr() % 16 and kv.data_ptr() % 16
+    ids = torch.randint(0, len(kv), (3, 129), device=gpu, dtype=torch.int32)
+    _assert_attention_close(sparse_mla(q, kv, ids, SCALE), _oracle(q, kv, ids, SCALE))
+
+
+def test_empty_tiles_and_large_logits_keep_online_softmax_stable(gpu):
+    from cxldsagr_amd.attention import sparse_mla
+
+    q = torch.zeros(1, 64, 576, device=gpu, dtype=torch.bfloat16)
+    q[..., 575] = 100
+    kv = torch.zeros(3, 576, device=gpu, dtype=torch.bfloat16)
+    kv[0] = float("nan")
+    kv[1, :512], kv[1, 575] = 2, 100
+    kv[2, :512], kv[2, 575] = 5, -100
+    for order in ([1, 2], [2, 1]):
+        ids = torch.full((1, 193), -1, device=gpu, dtype=torch.int32)
+        ids[0, 65:67] = torch.tensor(order, device=gpu, dtype=torch.int32)
+        actual = sparse_mla(q, kv, ids, 1)
+        assert torch.equal(actual, torch.full_like(actual, 2))
+    # The large score arrives in the second key half after a small one.
+    ids = torch.full((1, 2048), -1, device=gpu, dtype=torch.int32)
+    ids[0, 5] = 2
+    ids[0, 2000] = 1
+    actual = sparse_mla(q, kv, ids, 1)
+    assert torch.equal(actual, torch.full_like(actual, 2))
+
+
+def test_known_answers_duplicates_padding_and_rope(gpu):
+    from cxldsagr_amd.attention import sparse_mla
+
+    q = torch.zeros(3, 64, 576, device=gpu, dtype=torch.bfloat16)
+    kv = torch.zeros(3, 576, device=gpu, dtype=torch.bfloat16)
+    kv[0] = float("nan")
+    kv[1, :512] = 2
+    kv[2, :512] = 5
+    ids = torch.tensor([[1, 2, 2, -1], [-1, -1, 10, -1], [1, -1, -1, -1]], device=gpu,
+                       dtype=torch.int32)
+    out = sparse_mla(q, kv, ids, 1.0)
+    assert torch.equal(out[0], torch.full_like(out[0], 4.0))
+    assert torch.equal(out[1], torch.zeros_like(out[1]))
+    assert torch.equal(out[2], torch.full_like(out[2], 2.0))
+    # RoPE dimensions steer scores but are not values: softmax(0, ln 3) -> 0.75.
+    q = torch.zeros(1, 64, 576, device=gpu, dtype=torch.bfloat16)
+    q[..., 575] = 1
+    kv = torch.zeros(2, 576, device=gpu, dtype=torch.bfloat16)
+    kv[1, :512] = 1
+    kv[1, 575] = float(np.log(3))
+    out = sparse_mla(q, kv, torch.tensor([[0, 1]], device=gpu), 1.0)
+    torch.testing.assert_close(out.float(), torch.full((1, 64, 512), 0.75, device=gpu),
+                               atol=4e-3, rtol=0)
+
+
+@pytest.mark.parametrize(("queries", "tokens", "selected"), [(0, 5, 3), (2, 0, 3), (2, 5, 0)])
+def test_empty_inputs(gpu, queries, tokens, selected):
+    from cxldsagr_amd.attention import sparse_mla
+
+    q = torch.empty(queries, 128, 576, device=gpu, dtype=torch.bfloat16)
+    kv = torch.empty(tokens, 576, device=gpu, dtype=torch.bfloat16)
+    indices = torch.full((queries, selected), -1, device=gpu, dtype=torch.int32)
+    actual = sparse_mla(q, kv, indices, 0.2)
+    assert actual.shape == (queries, 128, 512) and not actual.any()
+
+
+@pytest.mark.parametrize(
+    ("heads", "dimension", "value_dim", "dtype", "message"),
+    [(128, 576, 512, torch.float16, "BF16"), (96, 576, 512, torch.bfloat16, "multiple of 64"),
+     (128, 512, 512, torch.bfloat16, "576"), (128, 576, 448, torch.bfloat16, "V=512")],
+)
+def test_unsupported_layouts_fail_explicitly(gpu, heads, dimension, value_dim, dtype, message):
+    from cxldsagr_amd.attention import sparse_mla
+
+    q = torch.zeros(1, heads, dimension, device=gpu, dtype=dtype)
+    kv = torch.zeros(5, dimension, device=gpu, dtype=dtype)
+    ids = torch.zeros(1, 4, device=gpu, dtype=torch.int32)
+    with pytest.raises(ValueError, match=message):
+        sparse_mla(q, kv, ids, 1, value_dim)
+
+
+@pytest.mark.parametrize("heads", [64, 128])
+def test_physical_remapping_preserves_attention_bit_exactly(gpu, heads):
+    from cxldsagr_amd.attention import sparse_mla, sparse_mla_from_pool
+
+    torch.manual_seed(734)
+    q = torch.randn(65, heads, 576, device=gpu, dtype=torch.bfloat16)
+    resident = torch.randn(1031, 576, device=gpu, dtype=torch.bfloat16)
+    logical = torch.randint(0, len(resident), (65, 129), device=gpu, dtype=torch.int32)
+    logical[:, -4:] = -1
+    logical[0] = -1
+    unique = torch.unique(logical[logical >= 0]).long()
+    physical = torch.searchsorted(unique, logical).int().masked_fill(logical < 0, -1)
+    compact = resident[unique]
+    a = sparse_mla(q, resident, logical, 0.07)
+    b = sparse_mla_from_pool(q, compact, physical, 0.07)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+# ----------------------------------------------------------------------------- A8
+
+
+def _paged_setup(gpu, tokens, seed=947):
+    from cxldsagr_amd.attention import pack_kv_fp8
+
+    gen = torch.Generator().manual_seed(seed)
+    kv = torch.randn(tokens, 576, generator=gen).bfloat16()
+    pages = (tokens + 63) // 64 + 3
+    table = torch.randperm(pages, generator=gen)[: (tokens + 63) // 64].int()
+    cache = torch.zeros(pages, 64, 656, dtype=torch.uint8, device=gpu)
+    status = torch.zeros(1, dtype=torch.int32, device=gpu)
+    pack_kv_fp8(kv.to(gpu), cache, table.to(gpu), status=status)
+    assert status.item() == 0
+    return kv, table, cache, pages
+
+
+def test_kv_pack_fp8_bytes_match_oracle(gpu):
+    kv, table, cache, pages = _paged_setup(gpu, 1000)
+    bits = kv.view(torch.int16).numpy().view(np.uint16)
+    expected = okv.build_cache(bits, table.numpy(), pages)
+    rows = okv.physical_rows(table.numpy(), 1000)
+    got = cache.cpu().numpy().reshape(-1, 656)
+    np.testing.assert_array_equal(got[rows], expected.reshape(-1, 656)[rows])
+
+
+@pytest.mark.parametrize(("queries", "selected"), [(3, 1), (5, 129), (17, 2048)])
+def test_fp8_paged_equals_bf16_path_on_dequantised_records(gpu, queries, selected):
+    from cxldsagr_amd.attention import sparse_mla, sparse_mla_fp8_paged
+
+    tokens = 3000
+    kv, table, cache, pages = _paged_setup(gpu, tokens)
+    deq = okv.logical_records(cache.cpu().numpy(), table.numpy(), tokens)
+    deq_bf16 = torch.from_numpy(deq).bfloat16()
+    assert torch.equal(deq_bf16.float(), torch.from_numpy(deq))  # exact in bf16
+    torch.manual_seed(5)
+    q = torch.randn(queries, 128, 576, dtype=torch.bfloat16).to(gpu)
+    ids = torch.randint(-5, tokens + 5, (queries, selected), dtype=torch.int32).to(gpu)
+    paged = sparse_mla_fp8_paged(q, cache, table.to(gpu), ids, SCALE, n_tokens=tokens)
+    flat = sparse_mla(q, deq_bf16.to(gpu), ids, SCALE)
+    assert torch.equal(paged.view(torch.int16), flat.view(torch.int16))
+    _assert_attention_close(paged, _oracle(q, deq_bf16, ids, SCALE))
+
+
+def test_sparse_mla_config2_shape(gpu):
+    """Config 2 shape: 128 queries x 128 heads x 2048 selected of 65664 fp8 paged tokens."""
+    from cxldsagr_amd.attention import sparse_mla_fp8_paged
+
+    tokens = 65664
+    kv, table, cache, pages = _paged_setup(gpu, tokens, seed=11)
+    gen = torch.Generator().manual_seed(12)
+    q = torch.randn(128, 128, 576, generator=gen).bfloat16()
+    ids = torch.stack([torch.randperm(tokens, generator=gen)[:2048] for _ in range(128)]).int()
+    out = sparse_mla_fp8_paged(q.to(gpu), cache, table.to(gpu), ids.to(gpu), SCALE)
+    deq = okv.logical_records(cache.cpu().numpy(), table.numpy(), tokens)
+    rows = [0, 1, 63, 127]
+    _, ref = omla.sparse_mla(q[rows].float().numpy(), deq, ids[rows].numpy(), SCALE)
+    _assert_attention_close(out[rows], ref)
