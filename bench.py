@@ -1,0 +1,250 @@
+#!/usr/bin/env python3
+"""Benchmark: one DSA prefill layer at 64K history + 128 query tokens on one MI355X.
+
+A step is one full layer through the HIP kernels, with every input already
+resident in HBM: quantise the indexer Q, fold its scales into the head
+weights, quantise the 128 new index keys into the resident index cache, fp8
+logits over 65,664 keys with the causal tail, exact top-2048, pack the 128
+new KV records into the fp8 paged cache, sparse MLA (128 heads, 2048
+selected, 656-byte fp8 records). Workload = BASELINE configs 1 and 2 (same
+seed, seeded synthetic inputs of the DeepSeek-V3.2 shapes).
+
+Prints one JSON line. ``value`` is microseconds per layer (lower is better).
+``roofline`` is for the kernel with the largest share of the step, timed with
+HIP events on the stream it is launched on; ``kernels`` lists every stage.
+``cpu_baseline`` times the numpy oracle of the same layer on a bounded sample
+of query rows on this machine's cores, scaled to 128 rows.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAKS = {  # MI355X published dense peaks
+    "hbm_GBps": 8000.0,
+    "fp8_TFLOPs": 5000.0,
+    "bf16_TFLOPs": 2500.0,
+}
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--history", type=int, default=65536)
+    p.add_argument("--queries", type=int, default=128)
+    p.add_argument("--seed", type=int, default=947)
+    p.add_argument("--cpu-rows", type=int, default=8,
+                   help="query rows of the CPU baseline sample (scaled to all rows)")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--only", choices=["layer", "logits", "topk", "mla"], default=None,
+                   help="time only one stage (for profiler runs)")
+    return p.parse_args()
+
+
+def event_time_us(torch, fn, iters):
+    """Average duration of fn() over iters launches, HIP events on the current stream."""
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(iters):
+        fn()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) * 1e3 / iters
+
+
+def cpu_baseline(inputs, rows_sample, topk):
+    import numpy as np
+
+    from oracle import layer as olayer
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max([info.get("num_threads", 1) for info in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover - reporting only
+        threads = os.cpu_count() or 1
+    history, queries = inputs.history, inputs.queries
+    index_q = inputs.index_q.float().cpu().numpy()
+    index_k = inputs.index_k.float().cpu().numpy()
+    weights = inputs.weights.cpu().numpy()
+    mla_q = inputs.mla_q.float().cpu().numpy()
+    kv_bits = inputs.kv.cpu().view(__import__("torch").int16).numpy().view(np.uint16)
+    cache = olayer.HistoryCache(index_k, kv_bits, fp8_records=True)
+    rows = np.linspace(0, queries - 1, rows_sample).round().astype(np.int64)
+    olayer.dsa_layer(index_q, weights, mla_q, cache, history, rows[:1], k=topk)  # warm-up
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter_ns()
+        olayer.dsa_layer(index_q, weights, mla_q, cache, history, rows, k=topk)
+        times.append((time.perf_counter_ns() - t0) / 1e3)
+    per_layer = sorted(times)[1] * queries / len(rows)
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(per_layer, 1),
+        "unit": "us/layer",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"numpy oracle layer (A1 Q quantise, A4 logits, A6 top-k, A7 MLA over "
+                  f"dequantised fp8 records) on {len(rows)} of {queries} query rows, median of 3, "
+                  f"scaled x{queries / len(rows):g}; resident K/KV caches prebuilt as on the GPU",
+        "cpu": cpu_model,
+        "affinity": len(os.sched_getaffinity(0)),
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported here "
+              "(the DSA layer is single-GPU; see DESIGN.md for how it would shard)",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from cxldsagr_amd import attention, indexer
+    from cxldsagr_amd.layer import DSALayer
+    from cxldsagr_amd.workloads import make_layer_inputs
+
+    device = torch.device("cuda", 0)
+    history, queries, topk = args.history, args.queries, 2048
+    tokens = history + queries
+    inputs = make_layer_inputs(history, queries, seed=args.seed)
+    layer = DSALayer(tokens, device=device, kv_format="fp8_paged", page_table=inputs.page_table)
+    layer.write_history(inputs.index_k[:history].to(device), inputs.kv[:history].to(device))
+    index_q = inputs.index_q.to(device)
+    index_k_new = inputs.index_k[history:].to(device).contiguous()
+    weights = inputs.weights.to(device)
+    mla_q = inputs.mla_q.to(device)
+    kv_new = inputs.kv[history:].to(device).contiguous()
+
+    def step():
+        layer.written = history
+        return layer.forward(index_q, index_k_new, weights, mla_q, kv_new)
+
+    # Intermediates for per-stage timing (same values the step produces).
+    out, selection = step()
+    q8, q_scale = indexer.quantize_index(index_q)
+    w_eff = (weights * q_scale[..., 0]).contiguous()
+    keys, kscale = layer.index_keys[:tokens], layer.index_scales[:tokens]
+    scores = indexer.logits(q8, keys, w_eff, kscale, history, _pad_to_stride=True)
+    _, ids = indexer.exact_topk(scores, topk)
+    torch.cuda.synchronize()
+
+    stages = {
+        "quantize_q": lambda: indexer.quantize_index(index_q),
+        "logits": lambda: indexer.logits(q8, keys, w_eff, kscale, history, _pad_to_stride=True),
+        "topk": lambda: indexer.exact_topk(scores, topk),
+        "pack_kv": lambda: attention.pack_kv_fp8(kv_new, layer.kv_cache, layer.page_table,
+                                                 token_offset=history),
+        "sparse_mla": lambda: attention.sparse_mla_fp8_paged(
+            mla_q, layer.kv_cache, layer.page_table, ids, layer.scale, n_tokens=tokens),
+    }
+    if args.only is not None:
+        fn = step if args.only == "layer" else stages[{"mla": "sparse_mla"}.get(args.only, args.only)]
+        for _ in range(args.warmup):
+            fn()
+        us = event_time_us(torch, fn, args.steps)
+        print(json.dumps({"only": args.only, "us": round(us, 2), "steps": args.steps}))
+        return
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    layer_us = event_time_us(torch, step, args.steps)
+
+    kernel_us = {name: event_time_us(torch, fn, args.steps) for name, fn in stages.items()}
+    pairs = queries * history + queries * (queries + 1) // 2
+    logits_flop = 2 * 64 * 128 * pairs
+    mla_flop = 2 * queries * topk * 128 * (576 + 512)
+    gather_bytes = queries * topk * 656
+    topk_bytes = queries * scores.stride(0) * 4 + queries * topk * 8
+    kernels = {
+        "logits": {
+            "us": round(kernel_us["logits"], 2),
+            "TFLOPs": round(logits_flop / kernel_us["logits"] / 1e6, 1),
+            "frac_fp8_peak": round(logits_flop / kernel_us["logits"] / 1e6 / PEAKS["fp8_TFLOPs"], 4),
+        },
+        "topk": {
+            "us": round(kernel_us["topk"], 2),
+            "GBps": round(topk_bytes / kernel_us["topk"] / 1e3, 1),
+        },
+        "sparse_mla": {
+            "us": round(kernel_us["sparse_mla"], 2),
+            "TFLOPs": round(mla_flop / kernel_us["sparse_mla"] / 1e6, 1),
+            "frac_bf16_peak": round(mla_flop / kernel_us["sparse_mla"] / 1e6 / PEAKS["bf16_TFLOPs"], 4),
+            "gather_GBps": round(gather_bytes / kernel_us["sparse_mla"] / 1e3, 1),
+            "gather_frac_hbm": round(gather_bytes / kernel_us["sparse_mla"] / 1e3 / PEAKS["hbm_GBps"], 4),
+        },
+        "quantize_q": {"us": round(kernel_us["quantize_q"], 2)},
+        "pack_kv": {"us": round(kernel_us["pack_kv"], 2)},
+    }
+    dominant = max(("logits", "topk", "sparse_mla"), key=lambda k: kernel_us[k])
+    traffic = None
+    traffic_file = ROOT / "profiles" / "traffic.json"
+    if traffic_file.exists():
+        traffic = json.loads(traffic_file.read_text()).get(dominant)
+    if dominant == "logits":
+        achieved = logits_flop / kernel_us["logits"] / 1e6
+        roofline = {"kernel": "dsa_indexer_logits_fp8", "bound": "mfma", "achieved": achieved,
+                    "peak": PEAKS["fp8_TFLOPs"], "unit": "TFLOP/s"}
+    elif dominant == "sparse_mla":
+        achieved = mla_flop / kernel_us["sparse_mla"] / 1e6
+        roofline = {"kernel": "dsa_sparse_mla_fp8_paged", "bound": "mfma", "achieved": achieved,
+                    "peak": PEAKS["bf16_TFLOPs"], "unit": "TFLOP/s"}
+    else:
+        achieved = topk_bytes / kernel_us["topk"] / 1e3
+        roofline = {"kernel": "dsa_topk_radix", "bound": "hbm", "achieved": achieved,
+                    "peak": PEAKS["hbm_GBps"], "unit": "GB/s"}
+    roofline["achieved"] = round(roofline["achieved"], 1)
+    roofline["frac"] = round(achieved / roofline["peak"], 4)
+    roofline["traffic"] = traffic
+
+    result = {
+        "metric": "DSA layer us @64K+128 tokens; fp8 logits TFLOPS & sparse-MLA GB/s as % peak",
+        "value": round(layer_us, 2),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(layer_us / 1e3, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8 (indexer) + bf16 (sparse MLA)",
+        "data": "synthetic (seeded, DeepSeek-V3.2 DSA shapes)",
+        "config": {
+            "workload": "DSA layer, BASELINE configs 1+2: 65536 history + 128 queries, "
+                        "64x128 fp8 indexer, top-2048, 128-head sparse MLA over 656-B fp8 paged KV",
+            "history": history,
+            "queries": queries,
+            "topk": topk,
+            "seed": args.seed,
+        },
+        "roofline": roofline,
+        "kernels": kernels,
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(inputs, args.cpu_rows, topk)
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

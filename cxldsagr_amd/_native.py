@@ -31,6 +31,13 @@ SIGNATURES = {
     "dsa_sparse_mla_bf16": [_ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _f32, _ptr, _ptr],
     "dsa_sparse_mla_fp8_paged": [_ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i64, _f32,
                                  _ptr, _ptr],
+    "dsa_gather_records": [_ptr, _i64, _ptr, _i64, _i64, _ptr, _ptr, _i64, _ptr, _int, _i64, _ptr,
+                           _ptr],
+    "dsa_copy_records_h2d": [_ptr, _ptr, _i64, _ptr],
+    "dsa_pool_workspace_bytes": [_i64, _i64, ctypes.POINTER(ctypes.c_int64)],
+    "dsa_pool_recall": [_ptr, _i64, _ptr, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64,
+                        _ptr, _ptr, _ptr, _i64, _i64, _ptr, _i64, _i64, _int, _ptr, _ptr, _ptr,
+                        _ptr],
 }
 
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}

@@ -83,9 +83,10 @@ def sparse_mla(q, kv, indices, scale, value_dim=512):
     _check_layout(q, value_dim, "DSA sparse MLA")
     if kv.shape[0] > torch.iinfo(torch.int32).max:
         raise ValueError("sparse MLA requires the KV row count to fit int32")
-    out = torch.zeros((*q.shape[:2], value_dim), dtype=q.dtype, device=q.device)
     if not q.shape[0] or not kv.shape[0] or not indices.shape[1]:
-        return out
+        return torch.zeros((*q.shape[:2], value_dim), dtype=q.dtype, device=q.device)
+    # The kernel writes every output element (all-padding rows as zeros).
+    out = torch.empty((*q.shape[:2], value_dim), dtype=q.dtype, device=q.device)
     q, kv = _aligned(q), _aligned(kv)
     ids = _narrow_ids(indices, kv.shape[0])
     with torch.cuda.device(q.device):
@@ -149,9 +150,9 @@ def sparse_mla_fp8_paged(q, kv_cache, page_table, indices, scale, value_dim=512,
         n_tokens = page_table.numel() * PAGE_TOKENS
     if type(n_tokens) is not int or not 0 <= n_tokens <= page_table.numel() * PAGE_TOKENS:
         raise ValueError("n_tokens must be covered by the page table")
-    out = torch.zeros((*q.shape[:2], value_dim), dtype=q.dtype, device=q.device)
     if not q.shape[0] or not n_tokens or not indices.shape[1]:
-        return out
+        return torch.zeros((*q.shape[:2], value_dim), dtype=q.dtype, device=q.device)
+    out = torch.empty((*q.shape[:2], value_dim), dtype=q.dtype, device=q.device)
     q = _aligned(q)
     cache = _aligned(kv_cache)
     table = page_table.contiguous()

@@ -1,0 +1,339 @@
+// A10: exact recall of a top-k selection into a bounded HBM token pool.
+//
+// Semantics: cache/sparse_token_cache.py:502-569 (ensure) with its victim
+// choice _available_slots/_evict (:465-500) and the pool's FIFO events
+// (cache/sparse_token_pool.py:648-676):
+//   union of selected history ids -> global host ids through the page table
+//   -> hits get priority = protect_stamp; misses (ascending logical order)
+//   -> victims = first m available slots by (rank, slot), rank = -1 for an
+//   empty slot else its priority; the sentinel slot 0 and this selection's
+//   hits are never victims -> evict old owners, publish h2d/d2h, stamp the
+//   chosen slots -> gather the missing records from pinned host memory
+//   -> map every selected id to its physical slot.
+//
+// Everything runs on the stream with the miss count kept on the device, so
+// there is no host read when the history fits the pool (then every union
+// fits too). The (rank, slot) order is one rocPRIM radix sort of 64-bit keys
+// over the pool's slots, the role CUB's radix sort plays in the reference
+// (operators/deepseek_v32/indexer/csrc/echo_sparse_recall.cuh:191).
+#include <cstring>
+#include <rocprim/device/device_radix_sort.hpp>
+
+#include "dsa_common.h"
+#include "../../include/dsa_gfx950.h"
+
+namespace dsa {
+namespace {
+
+constexpr int32_t kMissing = 0x7FFFFFFF;
+constexpr int kPage = 64;
+constexpr int kClassifyThreads = 1024;
+
+enum Counter { kUnion = 0, kMisses = 1, kEvicted = 2, kCounters = 4 };
+enum StatusBits { kUnwritten = 4, kShortPool = 8 };
+
+__global__ void recall_clear(uint32_t* __restrict__ sel_bits, int64_t sel_words,
+                             uint32_t* __restrict__ kept_bits, int64_t kept_words,
+                             int64_t* __restrict__ counters) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < sel_words) sel_bits[i] = 0;
+  if (i < kept_words) kept_bits[i] = 0;
+  if (i < kCounters) counters[i] = 0;
+}
+
+__global__ void recall_mark(const int32_t* __restrict__ indices, int64_t n, int64_t history_end,
+                            int64_t written, uint32_t* __restrict__ sel_bits,
+                            int32_t* __restrict__ status) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int64_t id = indices[i];
+  if (id >= written) {
+    if (status) atomicOr(status, kUnwritten);
+    return;
+  }
+  if (id >= 0 && id < history_end) atomicOr(&sel_bits[id >> 5], 1u << (id & 31));
+}
+
+__device__ __forceinline__ int64_t to_global(const int32_t* page_table, int64_t t) {
+  return (int64_t)page_table[t / kPage] * kPage + t % kPage;
+}
+
+// One work-group walks the selection bitmap in order. Thread t of a round
+// owns one 32-id word; hits are protected, misses are counted, and a block
+// scan places each thread's misses so the list is in ascending logical order.
+__global__ __launch_bounds__(kClassifyThreads) void recall_classify(
+    const uint32_t* __restrict__ sel_bits, int64_t history_end,
+    const int32_t* __restrict__ page_table, const int32_t* __restrict__ h2d,
+    int64_t* __restrict__ priority, uint32_t* __restrict__ kept_bits, int64_t protect_stamp,
+    int64_t* __restrict__ misses, int64_t* __restrict__ counters, int64_t* __restrict__ stats) {
+  __shared__ uint32_t wave_sums[kClassifyThreads / 64];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t words = (history_end + 31) >> 5;
+  int64_t running = 0, union_total = 0;
+  for (int64_t base = 0; base < words; base += kClassifyThreads) {
+    const int64_t w = base + tid;
+    const uint32_t bits = w < words ? sel_bits[w] : 0u;
+    uint32_t miss_mask = 0;
+    for (uint32_t rest = bits; rest; rest &= rest - 1) {
+      const int b = __builtin_ctz(rest);
+      const int64_t t = w * 32 + b;
+      const int32_t d = h2d[to_global(page_table, t)];
+      if (d != kMissing) {
+        priority[d] = protect_stamp;
+        atomicOr(&kept_bits[d >> 5], 1u << (d & 31));
+      } else {
+        miss_mask |= 1u << b;
+      }
+    }
+    const uint32_t mine = __builtin_popcount(miss_mask);
+    uint32_t incl = mine;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const uint32_t o = __shfl_up(incl, d);
+      if (lane >= d) incl += o;
+    }
+    if (lane == 63) wave_sums[wave] = incl;
+    uint32_t union_here = __builtin_popcount(bits);
+    __syncthreads();
+    uint32_t before = 0, total = 0;
+    for (int i = 0; i < kClassifyThreads / 64; ++i) {
+      const uint32_t s = wave_sums[i];
+      if (i < wave) before += s;
+      total += s;
+    }
+    int64_t slot = running + before + incl - mine;
+    for (uint32_t rest = miss_mask; rest; rest &= rest - 1) {
+      const int b = __builtin_ctz(rest);
+      misses[slot++] = to_global(page_table, w * 32 + b);
+    }
+    running += total;
+    // union count: reduce popcounts through the same scratch after a barrier
+    __syncthreads();
+    uint32_t u = union_here;
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) u += __shfl_xor(u, d);
+    if (lane == 0) wave_sums[wave] = u;
+    __syncthreads();
+    for (int i = 0; i < kClassifyThreads / 64; ++i) union_total += wave_sums[i];
+    __syncthreads();
+  }
+  if (tid == 0) {
+    counters[kUnion] = union_total;
+    counters[kMisses] = running;
+    atomicAdd(reinterpret_cast<unsigned long long*>(&stats[0]), (unsigned long long)union_total);
+    atomicAdd(reinterpret_cast<unsigned long long*>(&stats[1]), (unsigned long long)running);
+  }
+}
+
+__global__ void recall_victim_keys(const int64_t* __restrict__ d2h,
+                                   const int64_t* __restrict__ priority,
+                                   const uint32_t* __restrict__ kept_bits, int64_t slots,
+                                   uint64_t* __restrict__ keys) {
+  const int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (s > slots) return;
+  const bool kept = s == 0 || ((kept_bits[s >> 5] >> (s & 31)) & 1u);
+  if (kept) {
+    keys[s] = ~0ull;
+    return;
+  }
+  const int64_t rank = d2h[s] == kMissing ? -1 : priority[s];
+  keys[s] = ((uint64_t)(rank + 1) << 32) | (uint64_t)s;
+}
+
+__global__ void recall_assign(const uint64_t* __restrict__ sorted,
+                              const int64_t* __restrict__ misses,
+                              int64_t* __restrict__ counters, int32_t* __restrict__ h2d,
+                              int64_t* __restrict__ d2h, int64_t* __restrict__ priority,
+                              int64_t stamp, int64_t* __restrict__ chosen,
+                              int64_t* __restrict__ stats, int32_t* __restrict__ status) {
+  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t m = counters[kMisses];
+  if (j >= m) return;
+  const uint64_t key = sorted[j];
+  if (key == ~0ull) {
+    if (status) atomicOr(status, kShortPool);
+    chosen[j] = -1;
+    return;
+  }
+  const int64_t s = (int64_t)(key & 0xFFFFFFFFull);
+  const int64_t old = d2h[s];
+  if (old != kMissing) {
+    h2d[old] = kMissing;
+    atomicAdd(reinterpret_cast<unsigned long long*>(&counters[kEvicted]), 1ull);
+    atomicAdd(reinterpret_cast<unsigned long long*>(&stats[2]), 1ull);
+  }
+  const int64_t g = misses[j];
+  d2h[s] = g;
+  h2d[g] = (int32_t)s;
+  priority[s] = stamp;
+  chosen[j] = s;
+}
+
+// records[chosen[j]] = host[misses[j]] for j < m; one wave per record.
+__global__ __launch_bounds__(256) void recall_gather(const uint8_t* __restrict__ host,
+                                                     uint8_t* __restrict__ records,
+                                                     const int64_t* __restrict__ misses,
+                                                     const int64_t* __restrict__ chosen,
+                                                     const int64_t* __restrict__ counters,
+                                                     int64_t row_bytes) {
+  const int64_t m = counters[kMisses];
+  const int lane = threadIdx.x & 63;
+  const int64_t stride = (int64_t)gridDim.x * 4;
+  for (int64_t j = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); j < m; j += stride) {
+    const int64_t s = chosen[j];
+    if (s < 0) continue;
+    const uint4* src = reinterpret_cast<const uint4*>(host + misses[j] * row_bytes);
+    uint4* dst = reinterpret_cast<uint4*>(records + s * row_bytes);
+    for (int64_t i = lane; i < (row_bytes >> 4); i += 64) dst[i] = src[i];
+  }
+}
+
+__global__ void recall_map(const int32_t* __restrict__ indices, int64_t n, int64_t history_end,
+                           int64_t transient_start, int64_t slots,
+                           const int32_t* __restrict__ page_table, const int32_t* __restrict__ h2d,
+                           int32_t* __restrict__ physical) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int64_t id = indices[i];
+  int32_t out = -1;
+  if (id >= 0 && id < history_end) {
+    out = h2d[to_global(page_table, id)];
+  } else if (transient_start >= 0 && id >= transient_start) {
+    out = (int32_t)(slots + 1 + id - transient_start);
+  }
+  physical[i] = out;
+}
+
+struct Workspace {
+  uint32_t* sel_bits;
+  uint32_t* kept_bits;
+  int64_t* misses;
+  int64_t* chosen;
+  uint64_t* keys;
+  uint64_t* sorted;
+  int64_t* counters;
+  void* sort_temp;
+  size_t sort_bytes;
+  size_t total;
+};
+
+size_t align_up(size_t x) { return (x + 255) & ~size_t(255); }
+
+int plan(int64_t slots, int64_t history_capacity, uint8_t* base, Workspace* ws) {
+  size_t sort_bytes = 0;
+  hipError_t err = rocprim::radix_sort_keys(nullptr, sort_bytes, (const uint64_t*)nullptr,
+                                            (uint64_t*)nullptr, (size_t)(slots + 1), 0, 64,
+                                            (hipStream_t)0, false);
+  if (err != hipSuccess) {
+    set_error("rocprim radix sort sizing failed: %s", hipGetErrorString(err));
+    return kLaunchFailed;
+  }
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    size_t at = off;
+    off = align_up(off + bytes);
+    return base ? base + at : nullptr;
+  };
+  ws->sel_bits = reinterpret_cast<uint32_t*>(take(((history_capacity + 31) / 32) * 4));
+  ws->kept_bits = reinterpret_cast<uint32_t*>(take(((slots + 1 + 31) / 32) * 4));
+  ws->misses = reinterpret_cast<int64_t*>(take(history_capacity * 8));
+  ws->chosen = reinterpret_cast<int64_t*>(take(history_capacity * 8));
+  ws->keys = reinterpret_cast<uint64_t*>(take((slots + 1) * 8));
+  ws->sorted = reinterpret_cast<uint64_t*>(take((slots + 1) * 8));
+  ws->counters = reinterpret_cast<int64_t*>(take(kCounters * 8));
+  ws->sort_temp = take(sort_bytes);
+  ws->sort_bytes = sort_bytes;
+  ws->total = off;
+  return kOk;
+}
+
+}  // namespace
+}  // namespace dsa
+
+extern "C" int dsa_pool_workspace_bytes(int64_t slots, int64_t history_capacity, int64_t* bytes) {
+  using namespace dsa;
+  DSA_CHECK_ARG(slots >= 1 && history_capacity >= 0 && bytes, "invalid pool workspace query");
+  Workspace ws{};
+  int status = plan(slots, history_capacity, nullptr, &ws);
+  if (status != kOk) return status;
+  *bytes = (int64_t)ws.total;
+  return kOk;
+}
+
+extern "C" int dsa_pool_recall(const int32_t* indices, int64_t n, const int32_t* page_table,
+                               int64_t history_end, int64_t written, int64_t transient_start,
+                               int64_t slots, const void* host, int64_t host_rows, void* records,
+                               int64_t record_rows, int64_t record_bytes, int32_t* h2d,
+                               int64_t* d2h, int64_t* priority, int64_t protect_stamp,
+                               int64_t chosen_stamp, void* workspace, int64_t workspace_bytes,
+                               int64_t history_capacity, int union_checked, int64_t* stats,
+                               int32_t* status, int32_t* physical, hipStream_t stream) {
+  using namespace dsa;
+  DSA_CHECK_ARG(n >= 0 && slots >= 1 && history_end >= 0 && written >= history_end,
+                "invalid recall shape");
+  DSA_CHECK_ARG(history_end <= history_capacity, "history exceeds the planned workspace");
+  DSA_CHECK_ARG(history_end <= slots || union_checked,
+                "recall without a host check needs history <= slots; otherwise the caller "
+                "must have checked that the selection's union fits the pool");
+  DSA_CHECK_ARG(record_rows >= slots + 1 && record_bytes > 0 && record_bytes % 16 == 0,
+                "records must hold slots + 1 rows of a 16-byte multiple width");
+  DSA_CHECK_ARG(transient_start < 0 || transient_start >= history_end,
+                "the transient suffix starts after the host-backed history");
+  DSA_CHECK_ARG(protect_stamp >= 0 && chosen_stamp > protect_stamp && chosen_stamp < 0x7FFFFFFF,
+                "invalid FIFO timestamps");
+  DSA_CHECK_ARG(indices && page_table && h2d && d2h && priority && stats && physical && records &&
+                    workspace,
+                "null pointer");
+  Workspace ws{};
+  int rc = plan(slots, history_capacity, static_cast<uint8_t*>(workspace), &ws);
+  if (rc != kOk) return rc;
+  DSA_CHECK_ARG((int64_t)ws.total <= workspace_bytes, "workspace too small");
+  void* mapped = nullptr;
+  if (host_rows > 0) {
+    hipError_t err = hipHostGetDevicePointer(&mapped, const_cast<void*>(host), 0);
+    if (err != hipSuccess) {
+      set_error("host records are not device-accessible pinned memory: %s",
+                hipGetErrorString(err));
+      return kInvalidArgument;
+    }
+  }
+  const int64_t sel_words = (history_end + 31) / 32;
+  const int64_t kept_words = (slots + 1 + 31) / 32;
+  const int64_t clear_n = sel_words > kept_words ? sel_words : kept_words;
+  hipLaunchKernelGGL(recall_clear, dim3((unsigned)((clear_n + 255) / 256 + 1)), dim3(256), 0,
+                     stream, ws.sel_bits, sel_words, ws.kept_bits, kept_words, ws.counters);
+  if (n > 0)
+    hipLaunchKernelGGL(recall_mark, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                       indices, n, history_end, written, ws.sel_bits, status);
+  hipLaunchKernelGGL(recall_classify, dim3(1), dim3(kClassifyThreads), 0, stream, ws.sel_bits,
+                     history_end, page_table, h2d, priority, ws.kept_bits, protect_stamp,
+                     ws.misses, ws.counters, stats);
+  hipLaunchKernelGGL(recall_victim_keys, dim3((unsigned)((slots + 1 + 255) / 256)), dim3(256), 0,
+                     stream, d2h, priority, ws.kept_bits, slots, ws.keys);
+  size_t sort_bytes = ws.sort_bytes;
+  hipError_t err = rocprim::radix_sort_keys(ws.sort_temp, sort_bytes, ws.keys, ws.sorted,
+                                            (size_t)(slots + 1), 0, 64, stream, false);
+  if (err != hipSuccess) {
+    set_error("rocprim radix sort failed: %s", hipGetErrorString(err));
+    return kLaunchFailed;
+  }
+  const int64_t assign_n = history_end > 0 ? history_end : 1;
+  hipLaunchKernelGGL(recall_assign, dim3((unsigned)((assign_n + 255) / 256)), dim3(256), 0,
+                     stream, ws.sorted, ws.misses, ws.counters, h2d, d2h, priority, chosen_stamp,
+                     ws.chosen, stats, status);
+  if (host_rows > 0) {
+    int64_t blocks = (history_end + 3) / 4;
+    if (blocks > 2048) blocks = 2048;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(recall_gather, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       static_cast<const uint8_t*>(mapped), static_cast<uint8_t*>(records),
+                       ws.misses, ws.chosen, ws.counters, record_bytes);
+  }
+  if (n > 0)
+    hipLaunchKernelGGL(recall_map, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                       indices, n, history_end, transient_start, slots, page_table, h2d, physical);
+  DSA_CHECK_LAUNCH("exact recall");
+  return kOk;
+}

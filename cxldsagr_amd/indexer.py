@@ -82,6 +82,33 @@ def quantize_index(x, scale_fmt="ue8m0"):
     return data, scales
 
 
+def quantize_into(x, codes, scales, scale_fmt="ue8m0"):
+    """Quantise bf16/fp16/fp32 rows ``x [R, D]`` straight into preallocated
+    storage: ``codes`` e4m3 ``[R, D]`` and ``scales`` fp32 ``[R]`` (both
+    contiguous), e.g. a slice of the resident index-K cache
+    (``models/deepseek_v32/attention.py:323-326``)."""
+    if scale_fmt not in ("ue8m0", None):
+        raise ValueError("Unsupported indexer quantization scale format")
+    if x.ndim != 2 or x.dtype not in _native.DTYPE_CODES or x.stride(-1) != 1:
+        raise ValueError("x must be [rows, dim] with a unit last-dim stride")
+    rows, dim = x.shape
+    if (codes.dtype != torch.float8_e4m3fn or tuple(codes.shape) != (rows, dim)
+            or not codes.is_contiguous() or codes.device != x.device):
+        raise ValueError("codes must be contiguous float8_e4m3fn [rows, dim] on the input device")
+    if (scales.dtype != torch.float32 or scales.numel() != rows or not scales.is_contiguous()
+            or scales.device != x.device):
+        raise ValueError("scales must be contiguous float32 with one entry per row")
+    _native.require_gfx950(x.device, "indexer quantization")
+    if rows == 0:
+        return codes, scales
+    with torch.cuda.device(x.device):
+        _native.call(
+            "dsa_quantize_fp8_rows", _native.ptr(x), _native.DTYPE_CODES[x.dtype], rows, dim,
+            x.stride(0), _native.ptr(codes), _native.ptr(scales),
+            1 if scale_fmt == "ue8m0" else 0, _native.stream_of(x.device))
+    return codes, scales
+
+
 def padded_columns(columns):
     return (columns + SCORE_ALIGNMENT - 1) // SCORE_ALIGNMENT * SCORE_ALIGNMENT
 

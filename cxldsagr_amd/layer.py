@@ -1,0 +1,159 @@
+"""One DSA prefill layer on MI355X: indexer -> exact top-k -> sparse MLA.
+
+Follows the stage order of the reference's ``EchoAttentionRunner._forward``
+(``models/deepseek_v32/attention.py:276-425``) for the hot path:
+
+1. quantise the indexer Q (A1) and fold ``q_scale`` into the head weights
+   (``models/deepseek_v32/projections.py:241-244``; A2);
+2. quantise the new tokens' index K straight into the resident index cache
+   (``attention.py:323-326``; A3);
+3. fp8 logits with the causal ``-inf`` tail over the aligned score storage
+   (``attention.py:338-353``; A4);
+4. exact top-k (``attention.py:358-370``; A6);
+5. append the new tokens' KV records (quantise-on-append into the fp8 paged
+   cache, or a bf16 copy) (``attention.py:400-401``);
+6. sparse MLA over the selection (``attention.py:201-235``; A7).
+
+Projections and the output projection stay outside this layer (the
+reference's ``project``/``output`` callbacks). All stages run on the current
+stream without host synchronisation.
+"""
+
+import torch
+
+from cxldsagr_amd import attention, indexer
+from cxldsagr_amd.contracts import AttentionContext, TokenSelection
+
+PAGE_TOKENS = 64
+
+
+class DSALayer:
+    """Resident HBM caches for one layer of one sequence.
+
+    ``kv_format`` is ``"fp8_paged"`` (656-byte records in 64-token pages behind
+    ``page_table``) or ``"bf16"`` (flat 1152-byte records, the reference's
+    format). Implements the ``CacheAccess`` protocol for its own sequence.
+    """
+
+    def __init__(self, capacity, *, device, heads=128, topk=2048, scale=576**-0.5,
+                 kv_format="fp8_paged", page_table=None, pages=None, layer_idx=0):
+        if kv_format not in ("fp8_paged", "bf16"):
+            raise ValueError("kv_format must be 'fp8_paged' or 'bf16'")
+        if type(capacity) is not int or capacity < 1:
+            raise ValueError("capacity must be a positive integer")
+        self.device = torch.device(device)
+        self.capacity, self.heads, self.topk, self.scale = capacity, heads, topk, scale
+        self.kv_format, self.layer_idx = kv_format, layer_idx
+        self.index_keys = torch.zeros((capacity, 128), dtype=torch.float8_e4m3fn, device=self.device)
+        self.index_scales = torch.zeros(capacity, dtype=torch.float32, device=self.device)
+        logical_pages = (capacity + PAGE_TOKENS - 1) // PAGE_TOKENS
+        if kv_format == "fp8_paged":
+            if page_table is None:
+                page_table = torch.arange(logical_pages, dtype=torch.int32)
+            self.page_table = page_table.to(device=self.device, dtype=torch.int32).contiguous()
+            if self.page_table.numel() < logical_pages:
+                raise ValueError("page_table must cover the layer capacity")
+            pages = logical_pages if pages is None else pages
+            self.kv_cache = torch.zeros((pages, PAGE_TOKENS, attention.RECORD_BYTES),
+                                        dtype=torch.uint8, device=self.device)
+            self.records = None
+        else:
+            self.page_table = None
+            self.kv_cache = None
+            self.records = torch.zeros((capacity, attention.QK_DIM), dtype=torch.bfloat16,
+                                       device=self.device)
+        self.written = 0
+        self._state = {}
+
+    # ------------------------------------------------------------ CacheAccess
+    @property
+    def length(self):
+        return self.written
+
+    @property
+    def max_seq_len(self):
+        return self.capacity
+
+    def get_layer_state(self, layer_idx):
+        return self._state.get(layer_idx)
+
+    def set_layer_state(self, layer_idx, state):
+        self._state[layer_idx] = state
+
+    # ---------------------------------------------------------------- writes
+    def _append_kv(self, kv, start):
+        if self.kv_format == "fp8_paged":
+            attention.pack_kv_fp8(kv, self.kv_cache, self.page_table, token_offset=start)
+        else:
+            self.records[start:start + len(kv)].copy_(kv)
+
+    def write_history(self, index_k, kv):
+        """Bulk-append already projected history tokens (bf16 index K and KV)."""
+        start, end = self.written, self.written + len(index_k)
+        if len(kv) != len(index_k) or end > self.capacity:
+            raise ValueError("history exceeds the layer capacity or K/KV lengths differ")
+        indexer.quantize_into(index_k, self.index_keys[start:end], self.index_scales[start:end])
+        self._append_kv(kv, start)
+        self.written = end
+        return start
+
+    # ---------------------------------------------------------------- stages
+    def index(self, index_q, index_k, weights, position):
+        """Indexer: A1 -> A2 -> A3 -> A4 -> A6. Returns the TokenSelection."""
+        rows = len(index_q)
+        end = position + rows
+        if end > self.capacity:
+            raise ValueError("query batch exceeds the layer capacity")
+        q8, q_scale = indexer.quantize_index(index_q)
+        weights = (weights * q_scale[..., 0]).contiguous()
+        indexer.quantize_into(index_k, self.index_keys[position:end],
+                              self.index_scales[position:end])
+        scores = indexer.logits(q8, self.index_keys[:end], weights, self.index_scales[:end],
+                                position, _pad_to_stride=end >= self.topk)
+        _, ids = indexer.exact_topk(scores, self.topk)
+        return TokenSelection(ids)
+
+    def consume(self, q, selection, kv, position):
+        """Main attention: append the new KV, then sparse MLA over the selection."""
+        end = position + len(q)
+        self._append_kv(kv, position)
+        ids = selection.token_ids
+        if self.kv_format == "fp8_paged":
+            return attention.sparse_mla_fp8_paged(q, self.kv_cache, self.page_table, ids,
+                                                  self.scale, n_tokens=end)
+        return attention.sparse_mla(q, self.records[:end], ids, self.scale)
+
+    def forward(self, index_q, index_k, weights, q, kv):
+        """Run one query batch at ``position = self.written``; returns (out, selection)."""
+        position = self.written
+        selection = self.index(index_q, index_k, weights, position)
+        out = self.consume(q, selection, kv, position)
+        self.written = position + len(q)
+        return out, selection
+
+
+class LayerIndexer:
+    """``Indexer`` protocol adapter: ``context.auxiliary_state`` carries the new
+    tokens' bf16 index K (``"index_k"``) and head weights (``"weights"``)."""
+
+    def __init__(self, layer):
+        self.layer = layer
+
+    def __call__(self, q, cache_access, context: AttentionContext):
+        aux = context.auxiliary_state
+        return self.layer.index(q, aux["index_k"], aux["weights"], context.query_start)
+
+
+class LayerAttention:
+    """``MainAttention`` protocol adapter: ``context.auxiliary_state["kv"]`` holds
+    the new tokens' bf16 KV records."""
+
+    def __init__(self, layer):
+        self.layer = layer
+
+    def __call__(self, q, selection, cache_access, context: AttentionContext):
+        if not isinstance(selection, TokenSelection):
+            raise ValueError("DSA main attention consumes a TokenSelection")
+        out = self.layer.consume(q, selection, context.auxiliary_state["kv"], context.query_start)
+        self.layer.written = max(self.layer.written, context.query_start + len(q))
+        return out

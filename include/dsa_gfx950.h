@@ -33,6 +33,10 @@ extern "C" {
 #define DSA_DTYPE_F16 1
 #define DSA_DTYPE_F32 2
 
+/* Element types of the optional device valid_count of dsa_gather_records. */
+#define DSA_COUNT_I64 0
+#define DSA_COUNT_U32 1
+
 /* Copy the last error message of this host thread into `buffer` (always
  * NUL-terminated when size > 0). Returns the message length. */
 int dsa_last_error(char* buffer, size_t size);
@@ -115,6 +119,63 @@ int dsa_sparse_mla_fp8_paged(const void* q, int64_t rows, int64_t heads, const v
                              int64_t pages, const int32_t* page_table, int64_t n_tokens,
                              const int32_t* indices, int64_t topk, float scale, void* out,
                              hipStream_t stream);
+
+/*
+ * A11 - gather whole records from pinned host memory into device memory,
+ * device[device_ids[r]] = host[host_ids[r]] for r < count, or for
+ * r < *valid_count when valid_count (a device int64 or uint32 scalar, kind
+ * DSA_COUNT_*) is given. Replaces gather_host_records,
+ * operators/common/kv_transfer.py:21-68 (kernel gather_records,
+ * operators/common/csrc/kv_transfer.cu:14-64).
+ * host: pinned host allocation (hipHostMalloc / torch pin_memory) of
+ * host_rows x row_bytes; device: device_rows x row_bytes; ids int64 on the
+ * device. max_blocks bounds the grid (0 = automatic). An id out of range
+ * skips its row and ORs 1 into *status, a valid_count outside [0, count]
+ * copies nothing and ORs 2 (status may be NULL): the reference traps instead.
+ */
+int dsa_gather_records(const void* host, int64_t host_rows, void* device, int64_t device_rows,
+                       int64_t row_bytes, const int64_t* host_ids, const int64_t* device_ids,
+                       int64_t count, const void* valid_count, int count_kind, int64_t max_blocks,
+                       int32_t* status, hipStream_t stream);
+
+/*
+ * A11 - contiguous host-to-device record copy on `stream` (hipMemcpyAsync).
+ * Replaces copy_host_records_async, operators/common/kv_transfer.py:71-103
+ * (copy_contiguous, kv_transfer.cu:83-99); spans are checked by the caller.
+ */
+int dsa_copy_records_h2d(const void* host, void* device, int64_t bytes, hipStream_t stream);
+
+/*
+ * A10 - workspace size in bytes for dsa_pool_recall on a pool of `slots`
+ * slots and sequences of at most `history_capacity` host-backed tokens.
+ */
+int dsa_pool_workspace_bytes(int64_t slots, int64_t history_capacity, int64_t* bytes);
+
+/*
+ * A10 - exact recall of a top-k selection into the HBM token pool, then the
+ * logical -> physical map. Replaces SparseTokenCache.ensure /
+ * _ensure_sparse_from_topk, cache/sparse_token_cache.py:502-569 and :616-739
+ * (native stages sparse_selection_classify / allocate / gather_records /
+ * publish / map, operators/deepseek_v32/indexer/cache_ops.py:303-1016).
+ * indices: int32 [n] logical ids (-1 padding); page_table: int32 logical page
+ * -> global host page; ids in [0, history_end) are host-backed, ids at or
+ * past transient_start (>= 0) are candidate rows slots + 1 + id -
+ * transient_start. Pool state: h2d int32 [host_rows] (MISSING = INT32_MAX),
+ * d2h / priority int64 [slots + 1] (slot 0 is the sentinel), records
+ * [record_rows, record_bytes] on the device, host records pinned
+ * [host_rows, record_bytes]. Hits are stamped protect_stamp, recalled slots
+ * chosen_stamp. stats int64 [4] accumulates union, recalled, evicted.
+ * status bits: 4 = an id at or past `written`, 8 = the union did not fit.
+ * With history_end > slots the caller must pass union_checked != 0 after
+ * checking the union size. physical: int32 [n].
+ */
+int dsa_pool_recall(const int32_t* indices, int64_t n, const int32_t* page_table,
+                    int64_t history_end, int64_t written, int64_t transient_start, int64_t slots,
+                    const void* host, int64_t host_rows, void* records, int64_t record_rows,
+                    int64_t record_bytes, int32_t* h2d, int64_t* d2h, int64_t* priority,
+                    int64_t protect_stamp, int64_t chosen_stamp, void* workspace,
+                    int64_t workspace_bytes, int64_t history_capacity, int union_checked,
+                    int64_t* stats, int32_t* status, int32_t* physical, hipStream_t stream);
 
 #ifdef __cplusplus
 }
