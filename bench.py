@@ -46,6 +46,9 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--only", choices=["layer", "logits", "topk", "mla"], default=None,
                    help="time only one stage (for profiler runs)")
+    p.add_argument("--copy-calibration-mib", type=int, default=0,
+                   help="first run one plain device copy of this many MiB (scales PMC byte "
+                        "counters in profiler runs)")
     return p.parse_args()
 
 
@@ -157,6 +160,12 @@ def main():
         "sparse_mla": lambda: attention.sparse_mla_fp8_paged(
             mla_q, layer.kv_cache, layer.page_table, ids, layer.scale, n_tokens=tokens),
     }
+    if args.copy_calibration_mib:
+        src = torch.ones(args.copy_calibration_mib << 18, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     if args.only is not None:
         fn = step if args.only == "layer" else stages[{"mla": "sparse_mla"}.get(args.only, args.only)]
         for _ in range(args.warmup):
