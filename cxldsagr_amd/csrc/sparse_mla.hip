@@ -9,27 +9,34 @@
 // rounded to bf16; a row with no valid id is zero.
 //
 // Mapping (gfx950, wave64, v_mfma_f32_16x16x32_bf16):
-// * Work-group = (query row, 64 heads), 8 waves, two per SIMD. Wave w owns
-//   heads 16*(w&3) .. +16 of the group and half (w>>2) of the selected keys,
-//   so Q=128, H=128 gives 2048 waves, two per SIMD. Each wave keeps its 16
-//   heads of Q (72 VGPRs) and its O accumulators (16 heads x 512 dims, 128
-//   VGPRs) resident. (32 heads per wave would halve LDS traffic per flop but
-//   needs 400 live registers, and the online-softmax rescale of O keeps the
-//   accumulators out of AGPRs.)
+// * Work-group = (query row, 64 heads), 4 waves, one per SIMD (each wave has
+//   the whole register file: 256 VGPRs plus AGPRs as spill space). Wave w
+//   owns heads 16w .. 16w+16 and walks every selected key, keeping its 16
+//   heads of Q (72 VGPRs) and O (16 heads x 512 dims, 128 VGPRs) resident.
+//   (32 heads per wave would halve LDS bytes per flop but needs ~400 live
+//   registers; the online-softmax rescale keeps O out of AGPRs.)
 // * Scores are computed transposed, S^T = K Q^T (keys x heads): the C layout
-//   of S^T puts head l%16 and keys 4(l/16)+r in lane l, which is exactly the
-//   B-operand layout of O^T += V^T P^T when the 32 keys of a block are
-//   ordered (l/16, j) -> key 16(j/4) + 4(l/16) + j%4. The probabilities
-//   therefore never leave their lane; V^T is staged in LDS in that key order.
-// * Each iteration gathers 64 records (32 per key half) into LDS: K row-major
-//   [64][576+8] bf16 (padded stride, conflict-free 16-byte reads) and V^T
-//   [2][512][32+8]. fp8 records are dequantised on the way in (e4m3 x
-//   power-of-two scale is exact in bf16).
-// * Online softmax in log2 units with lazy rescaling: the running max only
-//   moves (and O is only rescaled) when a block raises it by more than 8,
-//   so p <= 2^8 and the common case skips 256 multiplies per lane.
-// * The two key halves are merged with their (max, sum) at the end through
-//   LDS, then O / l is rounded to bf16.
+//   of S^T puts head l%16 and keys 4(l/16)+r in lane l, which is the B-operand
+//   layout of O^T += V^T P^T when the 32 keys of a block are ordered
+//   (l/16, j) -> key 16(j/4) + 4(l/16) + j%4. The probabilities never leave
+//   their lane.
+// * The records of a block live once in LDS as bf16 rows of 1152 bytes whose
+//   16-byte chunks are XOR-swizzled by the row (chunk ^ (row & 15) for the
+//   latent, ^ (row & 7) within the RoPE chunks), so the 16 rows read by a
+//   16-lane group hit 16 different bank groups. The V^T operand (8 keys of
+//   one dim per lane) is read straight from these rows with
+//   ds_read_b64_tr_b16: lane 4j+q of a 16-lane group addresses row key_j,
+//   dims d0+4q..+3, and lane i receives dim d0+i of key_0..key_3.
+// * Gather: the selected records are copied by LDS DMA (global_load_lds,
+//   16 bytes per lane, no registers) into a ring of raw stages kRing blocks
+//   ahead, with the wait counts managed explicitly, so the random record
+//   reads stay in flight while earlier blocks compute. Each iteration then
+//   converts one raw stage into the bf16 block (fp8: one
+//   v_cvt_scalef32_pk_bf16_fp8 per two values; e4m3 x power-of-two scale is
+//   exact in bf16). Physical rows of the whole selection are resolved once
+//   into an LDS table.
+// * Online softmax in log2 units with lazy rescaling (only when a block
+//   raises the running max by more than 8, so p <= 2^8).
 #include "dsa_common.h"
 #include "../../include/dsa_gfx950.h"
 
@@ -37,35 +44,38 @@ namespace dsa {
 namespace {
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef short v4s __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int kQkDim = 576;
 constexpr int kVDim = 512;
-constexpr int kRope = 64;
 constexpr int kHeadsPerGroup = 64;
-constexpr int kBlock = 32;             // keys per block per key half
-constexpr int kKeysPerIter = 2 * kBlock;
-constexpr int kKStride = kQkDim + 8;   // bf16 elements per K row in LDS
-constexpr int kVtStride = kBlock + 8;  // bf16 elements per V^T row in LDS
-constexpr int kSteps = kQkDim / 32;    // 18 k-steps of 32 dims
-constexpr int kThreads = 512;
+constexpr int kBlock = 32;            // keys per block
+constexpr int kRowBytes = kQkDim * 2; // bf16 block row (swizzled chunks)
+constexpr int kSteps = kQkDim / 32;   // 18 k-steps of 32 dims
+constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int kNt = 1;                  // 16-head tiles per wave
-constexpr int kRecordFp8 = 656;
+constexpr int kMaxSelected = 4096;    // rows table capacity per query row
 constexpr int kPageTokens = 64;
 constexpr float kRescaleThreshold = 8.0f;
 
-struct __align__(16) Lds {
-  uint16_t k[kKeysPerIter][kKStride];
-  uint16_t vt[2][kVDim][kVtStride];
-  int32_t valid[kKeysPerIter];
+template <bool kFp8>
+struct Geometry {
+  static constexpr int kRecordBytes = kFp8 ? 656 : kRowBytes;
+  static constexpr int kChunks = kRecordBytes / 16;           // 41 or 72 per record
+  static constexpr int kStageChunks = kBlock * kChunks;       // 1312 or 2304
+  static constexpr int kLoadsPerWave = (kStageChunks + kThreads - 1) / kThreads;  // 6 or 9
+  static constexpr int kStageBytes = kLoadsPerWave * kThreads * 16;
+  static constexpr int kRing = kFp8 ? 4 : 2;
 };
 
-// Position of block key k (0..31) in the V^T key order.
-__device__ __forceinline__ int vt_slot(int k) {
-  const int t = k >> 4, g = (k >> 2) & 3, r = k & 3;
-  return 8 * g + 4 * t + r;
-}
+template <bool kFp8>
+struct __align__(16) Lds {
+  uint8_t block[kBlock * kRowBytes];                                 // bf16, swizzled
+  uint8_t ring[Geometry<kFp8>::kRing][Geometry<kFp8>::kStageBytes];  // raw records
+  int32_t rows[kMaxSelected];  // physical record row per selected position, -1 = padding
+};
 
 __device__ __forceinline__ v8bf as_v8bf(uint4 v) { return __builtin_bit_cast(v8bf, v); }
 
@@ -73,90 +83,106 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
 }
 
-// Gather the 64 records of this iteration into LDS. Thread -> (key = lane,
-// part = wave + 8i), so a wave covers 64 keys at one record offset and the
-// transposed V^T stores of a wave are 64 consecutive slots of one row.
+// Position of logical 16-byte chunk j (of 72) in block row `row`.
+__device__ __forceinline__ int chunk_slot(int j, int row) {
+  return j < 64 ? (j ^ (row & 15)) : 64 + ((j - 64) ^ (row & 7));
+}
+
+// LDS barrier that does not wait for the in-flight DMA stages: finish this
+// wave's LDS traffic, then s_barrier. The memory clobber keeps the compiler
+// from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <int kOutstanding>
+__device__ __forceinline__ void wait_dma() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kOutstanding) : "memory");
+}
+
+// One wave's LDS DMA for 64 consecutive 16-byte chunks of a raw stage: lane l
+// copies its chunk to lds_base + 16 l.
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               ::"s"(lds_base), "v"(src) : "memory", "m0");
+}
+
+// Issue the DMA of block `blk` into ring slot `slot`. Every wave issues
+// exactly kLoadsPerWave loads per stage (padding and invalid rows read the
+// first record), which keeps the vmcnt accounting uniform.
 template <bool kFp8>
-__device__ __forceinline__ void gather_block(Lds& lds, const uint8_t* __restrict__ kv,
-                                             const int32_t* __restrict__ page_table,
-                                             const int32_t* __restrict__ ids, int64_t n_tokens,
-                                             int64_t pages, int64_t topk, int64_t nblk_half,
-                                             int64_t it) {
+__device__ __forceinline__ void issue_stage(Lds<kFp8>& lds, const uint8_t* __restrict__ kv,
+                                            int64_t blk, int64_t iters, int slot) {
+  using G = Geometry<kFp8>;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int key = lane;
-  const int half = key >> 5;
-  const int kin = key & 31;
-  const int64_t blk = half * nblk_half + it;
-  const int64_t pos = blk * kBlock + kin;
-  int64_t id = -1;
-  if (blk < (half ? 2 * nblk_half : nblk_half) && pos < topk) id = ids[pos];
-  bool valid = id >= 0 && id < n_tokens;
-  const uint8_t* rec = nullptr;
-  if (valid) {
-    if (kFp8) {
-      // A page number outside the cache is treated like a padding id.
-      const int64_t page = page_table[id / kPageTokens];
-      valid = page >= 0 && page < pages;
-      rec = kv + (page * kPageTokens + id % kPageTokens) * kRecordFp8;
-    } else {
-      rec = kv + id * (int64_t)(kQkDim * 2);
+#pragma unroll
+  for (int k = 0; k < G::kLoadsPerWave; ++k) {
+    const int inst = k * kWaves + wave;
+    const int chunk = inst * 64 + lane;
+    const uint8_t* src = kv;
+    if (blk < iters && chunk < G::kStageChunks) {
+      const int r = chunk / G::kChunks;
+      const int j = chunk - r * G::kChunks;
+      const int32_t row = lds.rows[blk * kBlock + r];
+      src = kv + (int64_t)(row >= 0 ? row : 0) * G::kRecordBytes + 16 * j;
     }
+    const uint32_t base = (uint32_t)(uintptr_t)(&lds.ring[slot][inst * 64 * 16]);
+    dma16(src, __builtin_amdgcn_readfirstlane(base));
   }
-  if (wave == 0) lds.valid[key] = valid ? 1 : 0;
-  const int slot = vt_slot(kin);
-  uint16_t* krow = lds.k[key];
+}
 
-  if (kFp8) {
-    // 32 latent parts of 16 e4m3 values; tile scale per 8 parts.
+template <bool kHigh>
+__device__ __forceinline__ uint32_t dequant_pair(uint32_t word, float scale) {
+  v2bf v = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(word, scale, kHigh);
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Raw stage -> swizzled bf16 block. Thread -> (row = t % 32, part = t / 32).
+// Padding slots hold a placeholder record in the ring and become zeros here:
+// their probability is 0, but 0 x NaN would still poison the PV product.
+template <bool kFp8>
+__device__ __forceinline__ void convert_stage(Lds<kFp8>& lds, int slot, int64_t blk) {
+  using G = Geometry<kFp8>;
+  const int r = threadIdx.x & 31;
+  const int part = threadIdx.x >> 5;
+  const uint8_t* rec = &lds.ring[slot][r * G::kRecordBytes];
+  uint8_t* row = &lds.block[r * kRowBytes];
+  if (lds.rows[blk * kBlock + r] < 0) {
+    const uint4 zero = make_uint4(0, 0, 0, 0);
 #pragma unroll
-    for (int i = 0; i < 32 / kWaves; ++i) {
-      const int part = wave + kWaves * i;
-      uint4 raw = make_uint4(0, 0, 0, 0);
-      float scale = 0.0f;
-      if (valid) {
-        raw = *reinterpret_cast<const uint4*>(rec + part * 16);
-        scale = *reinterpret_cast<const float*>(rec + kVDim + 4 * (part >> 3));
-      }
-      const uint32_t words[4] = {raw.x, raw.y, raw.z, raw.w};
-      uint32_t packed[8];
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        float v0 = e4m3fn_to_f32(words[w] & 0xFF) * scale;
-        float v1 = e4m3fn_to_f32((words[w] >> 8) & 0xFF) * scale;
-        float v2 = e4m3fn_to_f32((words[w] >> 16) & 0xFF) * scale;
-        float v3 = e4m3fn_to_f32(words[w] >> 24) * scale;
-        packed[2 * w] = pack_bf16(v0, v1);
-        packed[2 * w + 1] = pack_bf16(v2, v3);
-      }
-      uint4* dst = reinterpret_cast<uint4*>(krow + part * 16);
-      dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-      dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
-#pragma unroll
-      for (int e = 0; e < 16; ++e)
-        lds.vt[half][part * 16 + e][slot] = (uint16_t)(packed[e >> 1] >> (16 * (e & 1)));
-    }
-  } else {
-#pragma unroll 4
-    for (int i = 0; i < 64 / kWaves; ++i) {
-      const int part = wave + kWaves * i;
-      uint4 raw = make_uint4(0, 0, 0, 0);
-      if (valid) raw = *reinterpret_cast<const uint4*>(rec + part * 16);
-      *reinterpret_cast<uint4*>(krow + part * 8) = raw;
-      const uint32_t words[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        lds.vt[half][part * 8 + e][slot] = (uint16_t)(words[e >> 1] >> (16 * (e & 1)));
-    }
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4*>(row + 16 * (8 * part + i)) = zero;
+    *reinterpret_cast<uint4*>(row + 16 * (64 + part)) = zero;
+    return;
   }
-  // RoPE: 8 parts of 8 bf16.
-  const int rope_offset = kFp8 ? kVDim + 16 : kVDim * 2;
+  if (kFp8) {
+    const float scale = *reinterpret_cast<const float*>(rec + kVDim + 4 * (part >> 1));
 #pragma unroll
-  for (int i = 0; i < 8 / kWaves; ++i) {
-    const int part = wave + kWaves * i;
-    uint4 raw = make_uint4(0, 0, 0, 0);
-    if (valid) raw = *reinterpret_cast<const uint4*>(rec + rope_offset + part * 16);
-    *reinterpret_cast<uint4*>(krow + kVDim + part * 8) = raw;
+    for (int i = 0; i < 4; ++i) {
+      const int j = 4 * part + i;  // fp8 chunk: values 16j .. 16j+15
+      const uint4 w = *reinterpret_cast<const uint4*>(rec + 16 * j);
+      const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+      uint32_t o[8];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        o[2 * q] = dequant_pair<false>(words[q], scale);
+        o[2 * q + 1] = dequant_pair<true>(words[q], scale);
+      }
+      *reinterpret_cast<uint4*>(row + 16 * chunk_slot(2 * j, r)) = make_uint4(o[0], o[1], o[2], o[3]);
+      *reinterpret_cast<uint4*>(row + 16 * chunk_slot(2 * j + 1, r)) =
+          make_uint4(o[4], o[5], o[6], o[7]);
+    }
+    const uint4 rope = *reinterpret_cast<const uint4*>(rec + kVDim + 16 + 16 * part);
+    *reinterpret_cast<uint4*>(row + 16 * chunk_slot(64 + part, r)) = rope;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int j = 8 * part + i;
+      *reinterpret_cast<uint4*>(row + 16 * chunk_slot(j, r)) =
+          *reinterpret_cast<const uint4*>(rec + 16 * j);
+    }
+    *reinterpret_cast<uint4*>(row + 16 * chunk_slot(64 + part, r)) =
+        *reinterpret_cast<const uint4*>(rec + 16 * (64 + part));
   }
 }
 
@@ -166,213 +192,182 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
     const int32_t* __restrict__ page_table, int64_t n_tokens, int64_t pages,
     const int32_t* __restrict__ indices, int64_t heads, int64_t topk, float scale_log2,
     uint16_t* __restrict__ out) {
-  __shared__ Lds lds;
+  using G = Geometry<kFp8>;
+  __shared__ Lds<kFp8> lds;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int half = wave >> 2;
   const int g = lane >> 4;
   const int c = lane & 15;
   const int64_t row = blockIdx.x;
-  const int64_t head0 = (int64_t)blockIdx.y * kHeadsPerGroup + 16 * kNt * (wave & 3);
+  const int64_t head0 = (int64_t)blockIdx.y * kHeadsPerGroup + 16 * wave;
   const int32_t* ids = indices + row * topk;
   const float neg_inf = -__builtin_inff();
+  const int64_t iters = (topk + kBlock - 1) / kBlock;
 
-  // Q^T operands: head 16n + c, dims 32ks + 8g .. +8.
-  v8bf qb[kNt][kSteps];
-#pragma unroll
-  for (int n = 0; n < kNt; ++n) {
-    const uint16_t* qrow = q + ((row * heads + head0 + 16 * n + c) * kQkDim) + 8 * g;
+  // Physical rows of every selected position.
+  for (int64_t i = threadIdx.x; i < iters * kBlock; i += kThreads) {
+    int32_t phys = -1;
+    if (i < topk) {
+      const int64_t id = ids[i];
+      if (id >= 0 && id < n_tokens) {
+        if (kFp8) {
+          const int64_t page = page_table[id / kPageTokens];
+          if (page >= 0 && page < pages) phys = (int32_t)(page * kPageTokens + id % kPageTokens);
+        } else {
+          phys = (int32_t)id;
+        }
+      }
+    }
+    lds.rows[i] = phys;
+  }
+
+  // Q^T operands: head head0 + c, dims 32ks + 8g .. +8.
+  v8bf qb[kSteps];
+  {
+    const uint16_t* qrow = q + ((row * heads + head0 + c) * kQkDim) + 8 * g;
 #pragma unroll
     for (int ks = 0; ks < kSteps; ++ks)
-      qb[n][ks] = as_v8bf(*reinterpret_cast<const uint4*>(qrow + 32 * ks));
+      qb[ks] = as_v8bf(*reinterpret_cast<const uint4*>(qrow + 32 * ks));
   }
+  v4f o[kVDim / 16];
+#pragma unroll
+  for (int m = 0; m < kVDim / 16; ++m) o[m] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  float m_run = neg_inf;
+  float l_run = 0.0f;
 
-  v4f o[kVDim / 16][kNt];
+  // All compiler-visible global loads must be complete before the DMA wait
+  // accounting starts; the builtin (vmcnt(0), expcnt/lgkmcnt untouched) also
+  // tells the compiler so, which keeps it from re-waiting inside the loop.
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  lds_barrier();
 #pragma unroll
-  for (int m = 0; m < kVDim / 16; ++m)
-#pragma unroll
-    for (int n = 0; n < kNt; ++n) o[m][n] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-  float m_run[kNt], l_run[kNt];
-#pragma unroll
-  for (int n = 0; n < kNt; ++n) {
-    m_run[n] = neg_inf;
-    l_run[n] = 0.0f;
-  }
+  for (int s = 0; s < G::kRing; ++s) issue_stage<kFp8>(lds, kv, s, iters, s);
 
-  const int64_t nblk = (topk + kBlock - 1) / kBlock;
-  const int64_t nblk_half = (nblk + 1) / 2;
-  const int kbase = half * kBlock;
+  // Block-row addresses of this lane's operands (row & 15 == c for S^T rows
+  // c and 16 + c; == 4g + jj for the V rows).
+  const int jj = c >> 2;
+  const int qq = c & 3;
+  const uint8_t* srow0 = &lds.block[c * kRowBytes];
+  const uint8_t* srow1 = &lds.block[(16 + c) * kRowBytes];
+  const int vr = 4 * g + jj;
+  const uint8_t* vrow0 = &lds.block[vr * kRowBytes + 8 * (qq & 1)];
+  const uint8_t* vrow1 = &lds.block[(16 + vr) * kRowBytes + 8 * (qq & 1)];
+  typedef v4s __attribute__((address_space(3))) * lds_v4s;
 
-  for (int64_t it = 0; it < nblk_half; ++it) {
-    __syncthreads();
-    gather_block<kFp8>(lds, kv, page_table, ids, n_tokens, pages, topk, nblk_half, it);
-    __syncthreads();
+  for (int64_t it = 0; it < iters; ++it) {
+    const int slot = (int)(it % G::kRing);
+    wait_dma<G::kLoadsPerWave*(G::kRing - 1)>();  // this wave's loads of block `it`
+    lds_barrier();                                 // everyone's loads landed; block free
+    convert_stage<kFp8>(lds, slot, it);
+    lds_barrier();
+    issue_stage<kFp8>(lds, kv, it + G::kRing, iters, slot);
 
-    // ---- S^T = K Q^T for this wave's 32 keys x 32 heads. Operands for the
-    // next k-step are loaded while the current one issues; the scheduling
-    // barriers stop the compiler from hoisting every LDS load (which would
-    // need ~150 extra registers).
-    v4f s[2][kNt];
+    // ---- S^T = K Q^T for 32 keys x this wave's 16 heads. Operands run two
+    // k-steps ahead of the MFMAs; the scheduling barriers keep that order.
+    v4f s0 = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    v4f s1 = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    uint4 ka[2][2];
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int n = 0; n < kNt; ++n) s[t][n] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    const uint16_t* krow0 = &lds.k[kbase + c][8 * g];
-    const uint16_t* krow1 = &lds.k[kbase + 16 + c][8 * g];
-    uint4 a0 = *reinterpret_cast<const uint4*>(krow0);
-    uint4 a1 = *reinterpret_cast<const uint4*>(krow1);
+    for (int d = 0; d < 2; ++d) {
+      const int off = 16 * chunk_slot(4 * d + g, c);
+      ka[d][0] = *reinterpret_cast<const uint4*>(srow0 + off);
+      ka[d][1] = *reinterpret_cast<const uint4*>(srow1 + off);
+    }
 #pragma unroll
     for (int ks = 0; ks < kSteps; ++ks) {
-      uint4 n0 = a0, n1 = a1;
-      if (ks + 1 < kSteps) {
-        n0 = *reinterpret_cast<const uint4*>(krow0 + 32 * (ks + 1));
-        n1 = *reinterpret_cast<const uint4*>(krow1 + 32 * (ks + 1));
+      const uint4 a0 = ka[ks & 1][0];
+      const uint4 a1 = ka[ks & 1][1];
+      if (ks + 2 < kSteps) {
+        const int off = 16 * chunk_slot(4 * (ks + 2) + g, c);
+        ka[ks & 1][0] = *reinterpret_cast<const uint4*>(srow0 + off);
+        ka[ks & 1][1] = *reinterpret_cast<const uint4*>(srow1 + off);
       }
-#pragma unroll
-      for (int n = 0; n < kNt; ++n) {
-        s[0][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(a0), qb[n][ks], s[0][n], 0, 0, 0);
-        s[1][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(a1), qb[n][ks], s[1][n], 0, 0, 0);
-      }
-      a0 = n0;
-      a1 = n1;
+      s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(a0), qb[ks], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(a1), qb[ks], s1, 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
 
-    // ---- online softmax (log2 domain), lane holds head 16n+c, keys 16t+4g+r.
-    int valid_bits = 0;
+    // ---- online softmax (log2 domain); lane holds head c, keys 16t+4g+r.
+    float x[8];
+    float mx = neg_inf;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        valid_bits |= lds.valid[kbase + 16 * t + 4 * g + r] << (4 * t + r);
-
-    float x[kNt][8];
-    float bmax[kNt];
-#pragma unroll
-    for (int n = 0; n < kNt; ++n) {
-      float mx = neg_inf;
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int j = 4 * t + r;
-          const float v = ((valid_bits >> j) & 1) ? s[t][n][r] * scale_log2 : neg_inf;
-          x[n][j] = v;
-          mx = fmaxf(mx, v);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      bmax[n] = mx;
-    }
-    bool need = false;
-#pragma unroll
-    for (int n = 0; n < kNt; ++n)
-      need |= bmax[n] > m_run[n] + kRescaleThreshold || (m_run[n] == neg_inf && bmax[n] != neg_inf);
+      for (int r = 0; r < 4; ++r) {
+        const bool valid = lds.rows[it * kBlock + 16 * t + 4 * g + r] >= 0;
+        const float v = valid ? (t ? s1[r] : s0[r]) * scale_log2 : neg_inf;
+        x[4 * t + r] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const bool need = mx > m_run + kRescaleThreshold || (m_run == neg_inf && mx != neg_inf);
     if (__builtin_amdgcn_ballot_w64(need)) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = (m_run == neg_inf) ? 0.0f : exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
 #pragma unroll
-      for (int n = 0; n < kNt; ++n) {
-        const float m_new = fmaxf(m_run[n], bmax[n]);
-        const float alpha = (m_run[n] == neg_inf) ? 0.0f : exp2f(m_run[n] - m_new);
-        m_run[n] = m_new;
-        l_run[n] *= alpha;
-#pragma unroll
-        for (int m = 0; m < kVDim / 16; ++m) o[m][n] *= alpha;
-      }
+      for (int m = 0; m < kVDim / 16; ++m) o[m] *= alpha;
     }
-    v8bf pb[kNt];
+    float p[8];
+    const bool live = m_run != neg_inf;
 #pragma unroll
-    for (int n = 0; n < kNt; ++n) {
-      float p[8];
-      const bool live = m_run[n] != neg_inf;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        p[j] = live ? exp2f(x[n][j] - m_run[n]) : 0.0f;
-        l_run[n] += p[j];
-      }
-      uint4 packed = make_uint4(pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]),
-                                pack_bf16(p[4], p[5]), pack_bf16(p[6], p[7]));
-      pb[n] = as_v8bf(packed);
+    for (int j = 0; j < 8; ++j) {
+      p[j] = live ? exp2f(x[j] - m_run) : 0.0f;
+      l_run += p[j];
     }
+    const v8bf pb = as_v8bf(make_uint4(pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]),
+                                       pack_bf16(p[4], p[5]), pack_bf16(p[6], p[7])));
 
-    // ---- O^T += V^T P^T over 512 dims, one M-tile of 16 dims ahead.
-    const uint16_t* vrow = &lds.vt[half][c][8 * g];
-    uint4 va = *reinterpret_cast<const uint4*>(vrow);
+    // ---- O^T += V^T P^T over 512 dims: dims 16m + 4qq are logical chunk
+    // 2m + qq/2 of rows vr and 16 + vr. Transpose loads run kVAhead m-tiles
+    // ahead of the MFMAs.
+    constexpr int kVAhead = 4;
+    v4s vlo[kVAhead], vhi[kVAhead];
+#pragma unroll
+    for (int d = 0; d < kVAhead; ++d) {
+      const int off = 16 * chunk_slot(2 * d + (qq >> 1), vr);
+      vlo[d] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(vrow0 + off));
+      vhi[d] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(vrow1 + off));
+    }
 #pragma unroll
     for (int m = 0; m < kVDim / 16; ++m) {
-      uint4 vn = va;
-      if (m + 1 < kVDim / 16) vn = *reinterpret_cast<const uint4*>(vrow + 16 * (m + 1) * kVtStride);
-#pragma unroll
-      for (int n = 0; n < kNt; ++n)
-        o[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(va), pb[n], o[m][n], 0, 0, 0);
-      va = vn;
+      const v8bf a = __builtin_bit_cast(
+          v8bf, __builtin_shufflevector(vlo[m % kVAhead], vhi[m % kVAhead], 0, 1, 2, 3, 4, 5, 6, 7));
+      if (m + kVAhead < kVDim / 16) {
+        const int off = 16 * chunk_slot(2 * (m + kVAhead) + (qq >> 1), vr);
+        vlo[m % kVAhead] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(vrow0 + off));
+        vhi[m % kVAhead] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(vrow1 + off));
+      }
+      o[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, o[m], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
+  // Drain the DMA issued past the last block (padding loads) before exit.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  // ---- merge the two key halves: waves 4-7 hand (m, l, O) to waves 0-3.
+  l_run += __shfl_xor(l_run, 16);
+  l_run += __shfl_xor(l_run, 32);
+  const float inv_l = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+  // Lane holds head c, dims 16m + 4g + r.
+  uint16_t* orow = out + ((row * heads + head0 + c) * kVDim) + 4 * g;
 #pragma unroll
-  for (int n = 0; n < kNt; ++n) {
-    l_run[n] += __shfl_xor(l_run[n], 16);
-    l_run[n] += __shfl_xor(l_run[n], 32);
-  }
-  constexpr int kStashRegs = kVDim / 16 * kNt * 4 + 2 * kNt;
-  static_assert(4 * kStashRegs * 64 * 4 <= (int)sizeof(Lds), "merge stash exceeds LDS");
-  __syncthreads();
-  float* stash = reinterpret_cast<float*>(&lds) + (wave & 3) * kStashRegs * 64;
-  const int mbase = kVDim / 16 * kNt * 4;
-  if (half == 1) {
-#pragma unroll
-    for (int m = 0; m < kVDim / 16; ++m)
-#pragma unroll
-      for (int n = 0; n < kNt; ++n)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) stash[((m * kNt + n) * 4 + r) * 64 + lane] = o[m][n][r];
-#pragma unroll
-    for (int n = 0; n < kNt; ++n) {
-      stash[(mbase + n) * 64 + lane] = m_run[n];
-      stash[(mbase + kNt + n) * 64 + lane] = l_run[n];
-    }
-  }
-  __syncthreads();
-  if (half == 1) return;
-  float a_own[kNt], a_other[kNt], inv_l[kNt];
-#pragma unroll
-  for (int n = 0; n < kNt; ++n) {
-    const float m_other = stash[(mbase + n) * 64 + lane];
-    const float l_other = stash[(mbase + kNt + n) * 64 + lane];
-    const float m_new = fmaxf(m_run[n], m_other);
-    a_own[n] = m_run[n] == neg_inf ? 0.0f : exp2f(m_run[n] - m_new);
-    a_other[n] = m_other == neg_inf ? 0.0f : exp2f(m_other - m_new);
-    const float l = l_run[n] * a_own[n] + l_other * a_other[n];
-    inv_l[n] = l > 0.0f ? 1.0f / l : 0.0f;
-  }
-  // Lane holds head 16n + c, dims 16m + 4g + r.
-#pragma unroll
-  for (int n = 0; n < kNt; ++n) {
-    uint16_t* orow = out + ((row * heads + head0 + 16 * n + c) * kVDim) + 4 * g;
-#pragma unroll
-    for (int m = 0; m < kVDim / 16; ++m) {
-      float v[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float other = stash[((m * kNt + n) * 4 + r) * 64 + lane];
-        v[r] = (o[m][n][r] * a_own[n] + other * a_other[n]) * inv_l[n];
-      }
-      *reinterpret_cast<uint2*>(orow + 16 * m) =
-          make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
-    }
-  }
+  for (int m = 0; m < kVDim / 16; ++m)
+    *reinterpret_cast<uint2*>(orow + 16 * m) =
+        make_uint2(pack_bf16(o[m][0] * inv_l, o[m][1] * inv_l),
+                   pack_bf16(o[m][2] * inv_l, o[m][3] * inv_l));
 }
 
 template <bool kFp8>
 int launch(const void* q, int64_t rows, int64_t heads, const void* kv, const int32_t* page_table,
-           int64_t n_tokens, int64_t pages, const int32_t* indices, int64_t topk, float scale, void* out,
-           hipStream_t stream) {
+           int64_t n_tokens, int64_t pages, const int32_t* indices, int64_t topk, float scale,
+           void* out, hipStream_t stream) {
   const float scale_log2 = scale * 1.4426950408889634f;
   hipLaunchKernelGGL(sparse_mla_fwd<kFp8>, dim3((unsigned)rows, (unsigned)(heads / kHeadsPerGroup)),
                      dim3(kThreads), 0, stream, static_cast<const uint16_t*>(q),
-                     static_cast<const uint8_t*>(kv), page_table, n_tokens, pages, indices, heads, topk,
-                     scale_log2, static_cast<uint16_t*>(out));
+                     static_cast<const uint8_t*>(kv), page_table, n_tokens, pages, indices, heads,
+                     topk, scale_log2, static_cast<uint16_t*>(out));
   DSA_CHECK_LAUNCH("sparse MLA");
   return kOk;
 }
@@ -380,6 +375,7 @@ int launch(const void* q, int64_t rows, int64_t heads, const void* kv, const int
 int check_common(const void* q, int64_t rows, int64_t heads, const int32_t* indices, int64_t topk,
                  float scale, void* out) {
   DSA_CHECK_ARG(rows >= 0 && topk >= 1, "invalid sparse MLA shape");
+  DSA_CHECK_ARG(topk <= kMaxSelected, "sparse MLA supports at most 4096 selected tokens per row");
   DSA_CHECK_ARG(heads > 0 && heads % kHeadsPerGroup == 0 && heads / kHeadsPerGroup < 65536,
                 "heads must be a positive multiple of 64");
   DSA_CHECK_ARG(__builtin_isfinite(scale), "scale must be finite");
@@ -400,8 +396,8 @@ extern "C" int dsa_sparse_mla_bf16(const void* q, int64_t rows, int64_t heads, c
   using namespace dsa;
   int status = check_common(q, rows, heads, indices, topk, scale, out);
   if (status != kOk || rows == 0) return status;
-  DSA_CHECK_ARG(kv_rows >= 0 && kv_rows < 0x7FFFFFFF, "KV row count must fit int32");
-  DSA_CHECK_ARG(kv != nullptr || kv_rows == 0, "null kv");
+  DSA_CHECK_ARG(kv_rows >= 1 && kv_rows < 0x7FFFFFFF, "KV row count must be in [1, 2^31)");
+  DSA_CHECK_ARG(kv != nullptr, "null kv");
   DSA_CHECK_ARG(reinterpret_cast<uintptr_t>(kv) % 16 == 0, "kv must be 16-byte aligned");
   return launch<false>(q, rows, heads, kv, nullptr, kv_rows, 0, indices, topk, scale, out,
                        stream);
@@ -415,10 +411,10 @@ extern "C" int dsa_sparse_mla_fp8_paged(const void* q, int64_t rows, int64_t hea
   using namespace dsa;
   int status = check_common(q, rows, heads, indices, topk, scale, out);
   if (status != kOk || rows == 0) return status;
-  DSA_CHECK_ARG(n_tokens >= 0 && n_tokens <= pages * kPageTokens,
-                "page table must cover every token");
-  DSA_CHECK_ARG(n_tokens < 0x7FFFFFFF, "token count must fit int32");
-  DSA_CHECK_ARG(n_tokens == 0 || (cache && page_table), "null cache or page table");
+  DSA_CHECK_ARG(pages >= 1 && n_tokens >= 1 && n_tokens <= pages * kPageTokens,
+                "page table must cover every token of a nonempty cache");
+  DSA_CHECK_ARG(pages * kPageTokens < 0x7FFFFFFF, "cache rows must fit int32");
+  DSA_CHECK_ARG(cache && page_table, "null cache or page table");
   DSA_CHECK_ARG(reinterpret_cast<uintptr_t>(cache) % 16 == 0, "cache must be 16-byte aligned");
   return launch<true>(q, rows, heads, cache, page_table, n_tokens, pages, indices, topk, scale,
                       out, stream);
