@@ -37,6 +37,15 @@ FLAGS = [
 ]
 
 
+# Per-source device code generation flags.
+# sparse_mla: MFMA accumulators in VGPRs. The O accumulators are rescaled by
+# the online softmax (a VALU multiply); in AGPRs the compiler would keep a
+# VGPR copy of them and move all 128 registers on every key block.
+SOURCE_FLAGS = {
+    "sparse_mla.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def hipcc():
     path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not os.path.exists(path):
@@ -50,7 +59,7 @@ def sources():
 
 def _compile(source):
     obj = BUILD_DIR / (source.stem + ".o")
-    cmd = [hipcc(), *FLAGS, "-c", str(source), "-o", str(obj)]
+    cmd = [hipcc(), *FLAGS, *SOURCE_FLAGS.get(source.name, []), "-c", str(source), "-o", str(obj)]
     result = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     stderr = "\n".join(line for line in result.stderr.splitlines() if noise not in line)

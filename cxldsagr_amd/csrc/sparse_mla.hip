@@ -47,6 +47,7 @@ typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
 constexpr int kQkDim = 576;
 constexpr int kVDim = 512;
@@ -78,9 +79,12 @@ struct __align__(16) Lds {
 };
 
 __device__ __forceinline__ v8bf as_v8bf(uint4 v) { return __builtin_bit_cast(v8bf, v); }
+__device__ __forceinline__ v8bf as_v8bf(v4u v) { return __builtin_bit_cast(v8bf, v); }
 
+// Two floats -> packed bf16 pair, round-to-nearest-even (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+  typedef float v2f __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f){lo, hi}, v2bf));
 }
 
 // Position of logical 16-byte chunk j (of 72) in block row `row`.
@@ -243,16 +247,36 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
 #pragma unroll
   for (int s = 0; s < G::kRing; ++s) issue_stage<kFp8>(lds, kv, s, iters, s);
 
-  // Block-row addresses of this lane's operands (row & 15 == c for S^T rows
-  // c and 16 + c; == 4g + jj for the V rows).
+  // Operand addresses. S^T rows c and 16 + c share the swizzle (row & 15 ==
+  // c); k-step ks reads logical chunk 4 ks + g, whose slot is
+  // 16 (ks >> 2) + 4 ((ks & 3) ^ (c >> 2)) + (g ^ (c & 3)): four base
+  // addresses plus an immediate offset cover all 18 k-steps (the two RoPE
+  // steps use their own pair). V rows vr and 16 + vr (vr = 4g + jj) read
+  // logical chunk 2m + (qq >> 1), at slot 16 (m >> 3) + 2 ((m & 7) ^ (vr >> 1))
+  // + ((qq >> 1) ^ (vr & 1)): eight bases.
   const int jj = c >> 2;
   const int qq = c & 3;
-  const uint8_t* srow0 = &lds.block[c * kRowBytes];
-  const uint8_t* srow1 = &lds.block[(16 + c) * kRowBytes];
   const int vr = 4 * g + jj;
-  const uint8_t* vrow0 = &lds.block[vr * kRowBytes + 8 * (qq & 1)];
-  const uint8_t* vrow1 = &lds.block[(16 + vr) * kRowBytes + 8 * (qq & 1)];
+  const uint32_t block_base = (uint32_t)(uintptr_t)lds.block;
+  uint32_t kbase[4], rbase[2], vbase[8];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+    kbase[t] = block_base + c * kRowBytes + 64 * (t ^ (c >> 2)) + 16 * (g ^ (c & 3));
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+    rbase[t] = block_base + c * kRowBytes + 16 * (64 + ((4 * t + g) ^ (c & 7)));
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+    vbase[t] = block_base + vr * kRowBytes + 32 * (t ^ (vr >> 1)) + 16 * ((qq >> 1) ^ (vr & 1)) +
+               8 * (qq & 1);
   typedef v4s __attribute__((address_space(3))) * lds_v4s;
+  typedef v4u __attribute__((address_space(3))) * lds_u4;
+  // Row offset of the second 16-key half of the block.
+  constexpr uint32_t kHalf = 16 * kRowBytes;
+  auto k_addr = [&](int ks) -> uint32_t {
+    return ks < 16 ? kbase[ks & 3] + 256 * (ks >> 2) : rbase[ks - 16];
+  };
+  auto v_addr = [&](int m) -> uint32_t { return vbase[m & 7] + 256 * (m >> 3); };
 
   for (int64_t it = 0; it < iters; ++it) {
     const int slot = (int)(it % G::kRing);
@@ -266,21 +290,19 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
     // k-steps ahead of the MFMAs; the scheduling barriers keep that order.
     v4f s0 = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     v4f s1 = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    uint4 ka[2][2];
+    v4u ka[2][2];
 #pragma unroll
     for (int d = 0; d < 2; ++d) {
-      const int off = 16 * chunk_slot(4 * d + g, c);
-      ka[d][0] = *reinterpret_cast<const uint4*>(srow0 + off);
-      ka[d][1] = *reinterpret_cast<const uint4*>(srow1 + off);
+      ka[d][0] = *(lds_u4)(uintptr_t)k_addr(d);
+      ka[d][1] = *(lds_u4)(uintptr_t)(k_addr(d) + kHalf);
     }
 #pragma unroll
     for (int ks = 0; ks < kSteps; ++ks) {
-      const uint4 a0 = ka[ks & 1][0];
-      const uint4 a1 = ka[ks & 1][1];
+      const v4u a0 = ka[ks & 1][0];
+      const v4u a1 = ka[ks & 1][1];
       if (ks + 2 < kSteps) {
-        const int off = 16 * chunk_slot(4 * (ks + 2) + g, c);
-        ka[ks & 1][0] = *reinterpret_cast<const uint4*>(srow0 + off);
-        ka[ks & 1][1] = *reinterpret_cast<const uint4*>(srow1 + off);
+        ka[ks & 1][0] = *(lds_u4)(uintptr_t)k_addr(ks + 2);
+        ka[ks & 1][1] = *(lds_u4)(uintptr_t)(k_addr(ks + 2) + kHalf);
       }
       s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(a0), qb[ks], s0, 0, 0, 0);
       s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(a1), qb[ks], s1, 0, 0, 0);
@@ -304,7 +326,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
     const bool need = mx > m_run + kRescaleThreshold || (m_run == neg_inf && mx != neg_inf);
     if (__builtin_amdgcn_ballot_w64(need)) {
       const float m_new = fmaxf(m_run, mx);
-      const float alpha = (m_run == neg_inf) ? 0.0f : exp2f(m_run - m_new);
+      const float alpha = (m_run == neg_inf) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
       m_run = m_new;
       l_run *= alpha;
 #pragma unroll
@@ -314,7 +336,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
     const bool live = m_run != neg_inf;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      p[j] = live ? exp2f(x[j] - m_run) : 0.0f;
+      p[j] = live ? __builtin_amdgcn_exp2f(x[j] - m_run) : 0.0f;
       l_run += p[j];
     }
     const v8bf pb = as_v8bf(make_uint4(pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]),
@@ -327,18 +349,17 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
     v4s vlo[kVAhead], vhi[kVAhead];
 #pragma unroll
     for (int d = 0; d < kVAhead; ++d) {
-      const int off = 16 * chunk_slot(2 * d + (qq >> 1), vr);
-      vlo[d] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(vrow0 + off));
-      vhi[d] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(vrow1 + off));
+      vlo[d] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)v_addr(d));
+      vhi[d] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)(v_addr(d) + kHalf));
     }
 #pragma unroll
     for (int m = 0; m < kVDim / 16; ++m) {
       const v8bf a = __builtin_bit_cast(
           v8bf, __builtin_shufflevector(vlo[m % kVAhead], vhi[m % kVAhead], 0, 1, 2, 3, 4, 5, 6, 7));
       if (m + kVAhead < kVDim / 16) {
-        const int off = 16 * chunk_slot(2 * (m + kVAhead) + (qq >> 1), vr);
-        vlo[m % kVAhead] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(vrow0 + off));
-        vhi[m % kVAhead] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(vrow1 + off));
+        const uint32_t va = v_addr(m + kVAhead);
+        vlo[m % kVAhead] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)va);
+        vhi[m % kVAhead] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)(va + kHalf));
       }
       o[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, o[m], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
