@@ -8,35 +8,46 @@
 // a record; P = softmax(q[r,h] . rec * scale); out[r,h] = P @ rec[:512],
 // rounded to bf16; a row with no valid id is zero.
 //
-// Mapping (gfx950, wave64, v_mfma_f32_16x16x32_bf16):
-// * Work-group = (query row, 64 heads), 4 waves, one per SIMD (each wave has
-//   the whole register file: 256 VGPRs plus AGPRs as spill space). Wave w
-//   owns heads 16w .. 16w+16 and walks every selected key, keeping its 16
-//   heads of Q (72 VGPRs) and O (16 heads x 512 dims, 128 VGPRs) resident.
-//   (32 heads per wave would halve LDS bytes per flop but needs ~400 live
-//   registers; the online-softmax rescale keeps O out of AGPRs.)
-// * Scores are computed transposed, S^T = K Q^T (keys x heads): the C layout
-//   of S^T puts head l%16 and keys 4(l/16)+r in lane l, which is the B-operand
-//   layout of O^T += V^T P^T when the 32 keys of a block are ordered
-//   (l/16, j) -> key 16(j/4) + 4(l/16) + j%4. The probabilities never leave
-//   their lane.
-// * The records of a block live once in LDS as bf16 rows of 1152 bytes whose
-//   16-byte chunks are XOR-swizzled by the row (chunk ^ (row & 15) for the
-//   latent, ^ (row & 7) within the RoPE chunks), so the 16 rows read by a
-//   16-lane group hit 16 different bank groups. The V^T operand (8 keys of
-//   one dim per lane) is read straight from these rows with
-//   ds_read_b64_tr_b16: lane 4j+q of a 16-lane group addresses row key_j,
-//   dims d0+4q..+3, and lane i receives dim d0+i of key_0..key_3.
-// * Gather: the selected records are copied by LDS DMA (global_load_lds,
-//   16 bytes per lane, no registers) into a ring of raw stages kRing blocks
-//   ahead, with the wait counts managed explicitly, so the random record
-//   reads stay in flight while earlier blocks compute. Each iteration then
-//   converts one raw stage into the bf16 block (fp8: one
-//   v_cvt_scalef32_pk_bf16_fp8 per two values; e4m3 x power-of-two scale is
-//   exact in bf16). Physical rows of the whole selection are resolved once
-//   into an LDS table.
-// * Online softmax in log2 units with lazy rescaling (only when a block
-//   raises the running max by more than 8, so p <= 2^8).
+// Mapping (gfx950, wave64, v_mfma_f32_16x16x32_bf16). A work-group owns one
+// query row and 64 heads and walks the selection in blocks of 32 keys; its 4
+// waves (one per SIMD) split each block twice:
+// * Scores: wave w computes S^T = K Q^T for key half kh = w / 2 (16 keys)
+//   and head half hh = w % 2 (32 heads), keeping Q^T of its 32 heads in
+//   registers (144). Each K operand read from LDS feeds two MFMAs.
+// * Values: wave w accumulates O^T for dims 128 w .. 128 w + 127 (one fp8
+//   scale tile) and all 64 heads (128 VGPRs). Each V operand feeds four MFMAs.
+// * Between the two, the per-head block maxima and the probabilities go
+//   through LDS. Every wave tracks the running max of all 64 heads (4 per
+//   lane) and updates it identically, so the rescale factors never travel.
+// LDS traffic per block is ~110 KB for 4.5 MFLOP (fp8), against ~330 KB when
+// every wave reads every key for 16 heads.
+//
+// Records reach LDS by LDS DMA (global_load_lds_dwordx4: 16 bytes per lane,
+// no registers) into a ring of raw stages kRing - 1 blocks ahead, with the
+// wait counts managed explicitly. A block's loads are issued in three parts
+// spread over the iteration (a full memory queue stalls the issuing wave),
+// and the score operands of block it + 1 are read during the PV product of
+// block it. fp8 records are consumed raw:
+// * K operand: lane (c, g) = (lane % 16, lane / 16) reads 8 e4m3 of key c and
+//   converts them with the key's tile scale (v_cvt_scalef32_pk_bf16_fp8;
+//   e4m3 x 2^k is exact in bf16).
+// * V^T operand: ds_read_b64_tr_b8 - within a 16-lane group, lane 8q + b
+//   receives byte b of the 8-byte segments addressed by lanes 2j + q,
+//   j = 0..7. Lanes 2j + q address key j at dims d0 + 8q, so lane i gets dim
+//   d0 + i of 8 keys: the A operand of O^T += V^T P^T after an unscaled
+//   conversion. The per-key scale of the wave's tile is folded into P
+//   (P x 2^k is exact in bf16), so the score waves write one P copy per dim
+//   tile.
+// bf16 records are DMA'd straight into rows whose 16-byte chunks are
+// XOR-swizzled by the key (chunk ^ (key & 15) for the latent, ^ (key & 7)
+// within the RoPE chunks); V^T then comes from ds_read_b64_tr_b16.
+//
+// Key order inside a block: MFMA k-index 8g + j of the PV product is key
+// 16 (j / 4) + 4g + j % 4, which is where the S^T C layout of the two key
+// halves puts them (lane (c, g) holds keys 4g + r of its half, head c).
+//
+// Online softmax in log2 units with lazy rescaling (only when a block raises
+// the running max by more than 8, so p <= 2^8).
 #include "dsa_common.h"
 #include "../../include/dsa_gfx950.h"
 
@@ -45,15 +56,18 @@ namespace {
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
-typedef short v4s __attribute__((ext_vector_type(4)));
+typedef float v2f __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+typedef int32_t v2i __attribute__((ext_vector_type(2)));
+typedef int32_t v4i __attribute__((ext_vector_type(4)));
+typedef short v4s __attribute__((ext_vector_type(4)));
 
 constexpr int kQkDim = 576;
 constexpr int kVDim = 512;
 constexpr int kHeadsPerGroup = 64;
 constexpr int kBlock = 32;            // keys per block
-constexpr int kRowBytes = kQkDim * 2; // bf16 block row (swizzled chunks)
 constexpr int kSteps = kQkDim / 32;   // 18 k-steps of 32 dims
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
@@ -63,33 +77,102 @@ constexpr float kRescaleThreshold = 8.0f;
 
 template <bool kFp8>
 struct Geometry {
-  static constexpr int kRecordBytes = kFp8 ? 656 : kRowBytes;
-  static constexpr int kChunks = kRecordBytes / 16;           // 41 or 72 per record
-  static constexpr int kStageChunks = kBlock * kChunks;       // 1312 or 2304
+  static constexpr int kRecordBytes = kFp8 ? 656 : kQkDim * 2;
+  static constexpr int kChunks = kRecordBytes / 16;  // 41 or 72 per record
+  // fp8: record r at chunk 41 r, plus 8 chunks (128 bytes) for the second
+  // key half. 8-byte LDS reads are served 32 lanes at a time from 64 4-byte
+  // banks; with the 656-byte stride alone, keys r and r + 16 share banks, and
+  // the V^T reads of one cycle (keys 0-7 and 16-23, or 8-15 and 24-31) would
+  // conflict. The shift moves the second half onto the complementary banks.
+  // bf16: record r at chunk 72 r.
+  static constexpr int kHalfPad = kFp8 ? 8 : 0;
+  static constexpr int kStageChunks = kBlock * kChunks + kHalfPad;
   static constexpr int kLoadsPerWave = (kStageChunks + kThreads - 1) / kThreads;  // 6 or 9
   static constexpr int kStageBytes = kLoadsPerWave * kThreads * 16;
-  static constexpr int kRing = kFp8 ? 4 : 2;
+  static constexpr int kRing = kFp8 ? 5 : 3;
+  static constexpr int kPVersions = kFp8 ? 4 : 1;  // P copies (one per V scale tile)
+  __device__ static constexpr uint32_t record_offset(int r) {
+    return 16u * (uint32_t)(kChunks * r + (r >= 16 ? kHalfPad : 0));
+  }
 };
 
 template <bool kFp8>
 struct __align__(16) Lds {
-  uint8_t block[kBlock * kRowBytes];                                 // bf16, swizzled
   uint8_t ring[Geometry<kFp8>::kRing][Geometry<kFp8>::kStageBytes];  // raw records
+  // P^T in PV B-operand order: [version][head tile][lane][key half][4 keys]
+  // bf16; lane (c, g) of tile t holds head 16t + c, keys 4g + r (+16).
+  uint8_t p[Geometry<kFp8>::kPVersions][4][64][16];
+  float block_max[2][kHeadsPerGroup];  // per key half
+  float row_sum[2][kHeadsPerGroup];
   int32_t rows[kMaxSelected];  // physical record row per selected position, -1 = padding
 };
 
-__device__ __forceinline__ v8bf as_v8bf(uint4 v) { return __builtin_bit_cast(v8bf, v); }
+// Source of padding slots and invalid ids: a zero record (zero scales), so
+// that their V^T operands are zeros rather than whatever the cache holds.
+__device__ __align__(16) uint8_t zero_record[kQkDim * 2];
+
 __device__ __forceinline__ v8bf as_v8bf(v4u v) { return __builtin_bit_cast(v8bf, v); }
 
 // Two floats -> packed bf16 pair, round-to-nearest-even (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  typedef float v2f __attribute__((ext_vector_type(2)));
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f){lo, hi}, v2bf));
 }
 
-// Position of logical 16-byte chunk j (of 72) in block row `row`.
-__device__ __forceinline__ int chunk_slot(int j, int row) {
-  return j < 64 ? (j ^ (row & 15)) : 64 + ((j - 64) ^ (row & 7));
+template <bool kHigh>
+__device__ __forceinline__ uint32_t dequant_pair(uint32_t word, float scale) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(word, scale, kHigh));
+}
+
+// acc += a b for the score MFMAs, with b (Q^T) pinned to AGPRs: Q^T of 32
+// heads (144 registers) and the O accumulators (128) do not both fit the 256
+// VGPRs, and as a compiler-chosen spill Q^T is copied back into an aligned
+// tuple before every use. As inline assembly the MFMA is invisible to the
+// hazard recognizer, so it covers its own wait states: the leading s_nop 1
+// gives the 2 required after a VALU write of `a` or `acc`; the reader of the
+// final accumulators waits with mfma_drain().
+__device__ __forceinline__ void mfma_qb(v4f& acc, v8bf a, v8bf b) {
+  asm volatile("s_nop 1\n\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "a"(b));
+}
+
+// Max over the four 16-lane rows (lanes l, l ^ 16, l ^ 32, l ^ 48) with the
+// gfx950 row-swap permutes instead of LDS-routed shuffles.
+__device__ __forceinline__ float max_across_rows(float v) {
+  const uint32_t u = __float_as_uint(v);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const float m = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const uint32_t w = __float_as_uint(m);
+  const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+// Wait states between the last inline-assembly MFMAs and any read of their
+// results (more than the 11 an 8-pass XDL op needs). The accumulators are
+// operands, so no read of them can be scheduled above the wait.
+__device__ __forceinline__ void mfma_drain(v4f& a, v4f& b, v4f& c, v4f& d) {
+  asm volatile("s_nop 7\n\ts_nop 7" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+}
+
+// 8 e4m3 (two dwords) x scale -> 8 bf16.
+__device__ __forceinline__ v8bf dequant8(v2u w, float scale) {
+  return as_v8bf(v4u{dequant_pair<false>(w.x, scale), dequant_pair<true>(w.x, scale),
+                     dequant_pair<false>(w.y, scale), dequant_pair<true>(w.y, scale)});
+}
+
+// Position of logical 16-byte chunk j (of 72) in bf16 record `key`.
+__device__ __forceinline__ int chunk_slot(int j, int key) {
+  return j < 64 ? (j ^ (key & 15)) : 64 + ((j - 64) ^ (key & 7));
+}
+
+typedef v2i __attribute__((address_space(3))) * lds_v2i;
+typedef v4s __attribute__((address_space(3))) * lds_v4s;
+
+template <typename T>
+__device__ __forceinline__ T lds_load(uint32_t addr) {
+  return *(T __attribute__((address_space(3)))*)(uintptr_t)addr;
+}
+template <typename T>
+__device__ __forceinline__ void lds_store(uint32_t addr, T v) {
+  *(T __attribute__((address_space(3)))*)(uintptr_t)addr = v;
 }
 
 // LDS barrier that does not wait for the in-flight DMA stages: finish this
@@ -111,84 +194,84 @@ __device__ __forceinline__ void dma16(const void* src, uint32_t lds_base) {
                ::"s"(lds_base), "v"(src) : "memory", "m0");
 }
 
-// Issue the DMA of block `blk` into ring slot `slot`. Every wave issues
-// exactly kLoadsPerWave loads per stage (padding and invalid rows read the
-// first record), which keeps the vmcnt accounting uniform.
+// Stage chunk -> (record slot r, logical chunk j) of the DMA source, or r = -1
+// for padding.
 template <bool kFp8>
-__device__ __forceinline__ void issue_stage(Lds<kFp8>& lds, const uint8_t* __restrict__ kv,
-                                            int64_t blk, int64_t iters, int slot) {
+__device__ __forceinline__ void stage_chunk(int sc, int& r, int& j) {
   using G = Geometry<kFp8>;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int k = 0; k < G::kLoadsPerWave; ++k) {
-    const int inst = k * kWaves + wave;
-    const int chunk = inst * 64 + lane;
-    const uint8_t* src = kv;
-    if (blk < iters && chunk < G::kStageChunks) {
-      const int r = chunk / G::kChunks;
-      const int j = chunk - r * G::kChunks;
-      const int32_t row = lds.rows[blk * kBlock + r];
-      src = kv + (int64_t)(row >= 0 ? row : 0) * G::kRecordBytes + 16 * j;
-    }
-    const uint32_t base = (uint32_t)(uintptr_t)(&lds.ring[slot][inst * 64 * 16]);
-    dma16(src, __builtin_amdgcn_readfirstlane(base));
-  }
-}
-
-template <bool kHigh>
-__device__ __forceinline__ uint32_t dequant_pair(uint32_t word, float scale) {
-  v2bf v = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(word, scale, kHigh);
-  return __builtin_bit_cast(uint32_t, v);
-}
-
-// Raw stage -> swizzled bf16 block. Thread -> (row = t % 32, part = t / 32).
-// Padding slots hold a placeholder record in the ring and become zeros here:
-// their probability is 0, but 0 x NaN would still poison the PV product.
-template <bool kFp8>
-__device__ __forceinline__ void convert_stage(Lds<kFp8>& lds, int slot, int64_t blk) {
-  using G = Geometry<kFp8>;
-  const int r = threadIdx.x & 31;
-  const int part = threadIdx.x >> 5;
-  const uint8_t* rec = &lds.ring[slot][r * G::kRecordBytes];
-  uint8_t* row = &lds.block[r * kRowBytes];
-  if (lds.rows[blk * kBlock + r] < 0) {
-    const uint4 zero = make_uint4(0, 0, 0, 0);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4*>(row + 16 * (8 * part + i)) = zero;
-    *reinterpret_cast<uint4*>(row + 16 * (64 + part)) = zero;
-    return;
-  }
   if (kFp8) {
-    const float scale = *reinterpret_cast<const float*>(rec + kVDim + 4 * (part >> 1));
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int j = 4 * part + i;  // fp8 chunk: values 16j .. 16j+15
-      const uint4 w = *reinterpret_cast<const uint4*>(rec + 16 * j);
-      const uint32_t words[4] = {w.x, w.y, w.z, w.w};
-      uint32_t o[8];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        o[2 * q] = dequant_pair<false>(words[q], scale);
-        o[2 * q + 1] = dequant_pair<true>(words[q], scale);
-      }
-      *reinterpret_cast<uint4*>(row + 16 * chunk_slot(2 * j, r)) = make_uint4(o[0], o[1], o[2], o[3]);
-      *reinterpret_cast<uint4*>(row + 16 * chunk_slot(2 * j + 1, r)) =
-          make_uint4(o[4], o[5], o[6], o[7]);
+    constexpr int kHalf = 16 * G::kChunks;
+    int base = sc;
+    int r0 = 0;
+    if (sc >= kHalf) {
+      base = sc - kHalf - G::kHalfPad;
+      r0 = 16;
     }
-    const uint4 rope = *reinterpret_cast<const uint4*>(rec + kVDim + 16 + 16 * part);
-    *reinterpret_cast<uint4*>(row + 16 * chunk_slot(64 + part, r)) = rope;
+    if (base < 0 || base >= kHalf) {
+      r = -1;
+      j = 0;
+      return;
+    }
+    const int rr = base / G::kChunks;
+    r = r0 + rr;
+    j = base - rr * G::kChunks;
   } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int j = 8 * part + i;
-      *reinterpret_cast<uint4*>(row + 16 * chunk_slot(j, r)) =
-          *reinterpret_cast<const uint4*>(rec + 16 * j);
+    if (sc >= G::kStageChunks) {
+      r = -1;
+      j = 0;
+      return;
     }
-    *reinterpret_cast<uint4*>(row + 16 * chunk_slot(64 + part, r)) =
-        *reinterpret_cast<const uint4*>(rec + 16 * (64 + part));
+    r = sc / G::kChunks;
+    const int p = sc - r * G::kChunks;  // physical slot; the swizzle is an involution
+    j = chunk_slot(p, r);
   }
 }
+
+// DMA plan of one lane: for each of its kLoadsPerWave loads per stage, the
+// record slot r (0xFFFF for padding) and the chunk's byte offset 16 j.
+template <bool kFp8>
+struct DmaPlan {
+  uint32_t rj[Geometry<kFp8>::kLoadsPerWave];  // (r << 16) | 16 j
+  int32_t row[Geometry<kFp8>::kLoadsPerWave];  // physical rows of the next block to issue
+
+  __device__ __forceinline__ void init() {
+    using G = Geometry<kFp8>;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int k = 0; k < G::kLoadsPerWave; ++k) {
+      int r, j;
+      stage_chunk<kFp8>((k * kWaves + wave) * 64 + lane, r, j);
+      rj[k] = r < 0 ? 0xFFFF0000u : ((uint32_t)r << 16) | (uint32_t)(16 * j);
+    }
+  }
+  // Reads the physical rows of block `blk` (-1 where nothing is fetched).
+  __device__ __forceinline__ void load_rows(const int32_t* rows, int blk, int n_blocks) {
+    using G = Geometry<kFp8>;
+#pragma unroll
+    for (int k = 0; k < G::kLoadsPerWave; ++k) {
+      const uint32_t r = rj[k] >> 16;
+      const bool use = blk < n_blocks && r != 0xFFFF;
+      const int32_t v = rows[use ? blk * kBlock + (int)r : 0];
+      row[k] = use ? v : -1;
+    }
+  }
+  // Issues loads [k0, k1) of the block whose rows were loaded, into the stage
+  // at slot_base. Loads without a record read the zero record.
+  template <int k0, int k1>
+  __device__ __forceinline__ void issue(const uint8_t* __restrict__ kv, const uint8_t* zero,
+                                        uint32_t slot_base) const {
+    using G = Geometry<kFp8>;
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int k = k0; k < k1; ++k) {
+      const bool use = row[k] >= 0;
+      const uint8_t* src = (use ? kv : zero) +
+                           (use ? (int64_t)row[k] * G::kRecordBytes + (rj[k] & 0xFFFF) : 0);
+      dma16(src, __builtin_amdgcn_readfirstlane(slot_base + (k * kWaves + wave) * 64 * 16));
+    }
+  }
+};
 
 template <bool kFp8>
 __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
@@ -202,8 +285,10 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
   const int wave = threadIdx.x >> 6;
   const int g = lane >> 4;
   const int c = lane & 15;
+  const int kh = wave >> 1;  // key half of the score phase
+  const int hh = wave & 1;   // head half of the score phase
   const int64_t row = blockIdx.x;
-  const int64_t head0 = (int64_t)blockIdx.y * kHeadsPerGroup + 16 * wave;
+  const int64_t head0 = (int64_t)blockIdx.y * kHeadsPerGroup;
   const int32_t* ids = indices + row * topk;
   const float neg_inf = -__builtin_inff();
   const int64_t iters = (topk + kBlock - 1) / kBlock;
@@ -225,159 +310,309 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
     lds.rows[i] = phys;
   }
 
-  // Q^T operands: head head0 + c, dims 32ks + 8g .. +8.
-  v8bf qb[kSteps];
-  {
-    const uint16_t* qrow = q + ((row * heads + head0 + c) * kQkDim) + 8 * g;
+  // Q^T operands of the score phase: head hh*32 + 16t + c, dims 32ks + 8g .. +8.
+  v8bf qb[2][kSteps];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const uint16_t* qrow = q + ((row * heads + head0 + 32 * hh + 16 * t + c) * kQkDim) + 8 * g;
 #pragma unroll
     for (int ks = 0; ks < kSteps; ++ks)
-      qb[ks] = as_v8bf(*reinterpret_cast<const uint4*>(qrow + 32 * ks));
+      qb[t][ks] = as_v8bf(*reinterpret_cast<const v4u*>(qrow + 32 * ks));
   }
-  v4f o[kVDim / 16];
+  // O^T: head tile t (heads 16t + c), dims 128 wave + 16m + 4g + r.
+  v4f o[4][8];
 #pragma unroll
-  for (int m = 0; m < kVDim / 16; ++m) o[m] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-  float m_run = neg_inf;
-  float l_run = 0.0f;
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int m = 0; m < 8; ++m) o[t][m] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  float m_run[4] = {neg_inf, neg_inf, neg_inf, neg_inf};  // heads 16t + c
+  // The same running max for the score heads 32 hh + 16t + c, and their row
+  // sums over this wave's key half.
+  float m_own[2] = {neg_inf, neg_inf};
+  float l_part[2] = {0.0f, 0.0f};
 
   // All compiler-visible global loads must be complete before the DMA wait
   // accounting starts; the builtin (vmcnt(0), expcnt/lgkmcnt untouched) also
   // tells the compiler so, which keeps it from re-waiting inside the loop.
   __builtin_amdgcn_s_waitcnt(0x0F70);
   lds_barrier();
+  const uint8_t* zero = zero_record;
+  const uint32_t ring_base = (uint32_t)(uintptr_t)&lds.ring[0][0];
+  const int n_blocks = (int)iters;
+  constexpr int kL = G::kLoadsPerWave;
+  DmaPlan<kFp8> dma;
+  dma.init();
 #pragma unroll
-  for (int s = 0; s < G::kRing; ++s) issue_stage<kFp8>(lds, kv, s, iters, s);
+  for (int s = 0; s < G::kRing - 1; ++s) {
+    dma.load_rows(lds.rows, s, n_blocks);
+    dma.template issue<0, kL>(kv, zero, ring_base + s * G::kStageBytes);
+  }
+  dma.load_rows(lds.rows, G::kRing - 1, n_blocks);
 
-  // Operand addresses. S^T rows c and 16 + c share the swizzle (row & 15 ==
-  // c); k-step ks reads logical chunk 4 ks + g, whose slot is
-  // 16 (ks >> 2) + 4 ((ks & 3) ^ (c >> 2)) + (g ^ (c & 3)): four base
-  // addresses plus an immediate offset cover all 18 k-steps (the two RoPE
-  // steps use their own pair). V rows vr and 16 + vr (vr = 4g + jj) read
-  // logical chunk 2m + (qq >> 1), at slot 16 (m >> 3) + 2 ((m & 7) ^ (vr >> 1))
-  // + ((qq >> 1) ^ (vr & 1)): eight bases.
-  const int jj = c >> 2;
-  const int qq = c & 3;
-  const int vr = 4 * g + jj;
-  const uint32_t block_base = (uint32_t)(uintptr_t)lds.block;
-  uint32_t kbase[4], rbase[2], vbase[8];
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-    kbase[t] = block_base + c * kRowBytes + 64 * (t ^ (c >> 2)) + 16 * (g ^ (c & 3));
-#pragma unroll
-  for (int t = 0; t < 2; ++t)
-    rbase[t] = block_base + c * kRowBytes + 16 * (64 + ((4 * t + g) ^ (c & 7)));
-#pragma unroll
-  for (int t = 0; t < 8; ++t)
-    vbase[t] = block_base + vr * kRowBytes + 32 * (t ^ (vr >> 1)) + 16 * ((qq >> 1) ^ (vr & 1)) +
-               8 * (qq & 1);
-  typedef v4s __attribute__((address_space(3))) * lds_v4s;
-  typedef v4u __attribute__((address_space(3))) * lds_u4;
-  // Row offset of the second 16-key half of the block.
-  constexpr uint32_t kHalf = 16 * kRowBytes;
-  auto k_addr = [&](int ks) -> uint32_t {
-    return ks < 16 ? kbase[ks & 3] + 256 * (ks >> 2) : rbase[ks - 16];
+  const uint32_t p_base = (uint32_t)(uintptr_t)&lds.p[0][0][0][0];
+  const uint32_t max_base = (uint32_t)(uintptr_t)&lds.block_max[0][0];
+  const uint32_t rows_base = (uint32_t)(uintptr_t)&lds.rows[0];
+  // V^T (tr8) rows: lane 2j + q of each 16-lane group reads key
+  // 16 (j / 4) + 4g + j % 4 at dims +8q.
+  const int vj = c >> 1;
+  const int vq = c & 1;
+  const int vkey = 16 * (vj >> 2) + 4 * g + (vj & 3);
+
+  // Loop-invariant lane parts of the stage addresses.
+  const uint32_t s_lane = G::record_offset(16 * kh + c) + (kFp8 ? 8 * g : 0);
+  int slot = 0;                 // ring slot of block it
+  int free_slot = G::kRing - 1;  // ring slot that receives block it + kRing - 1
+  // bf16 K operand of k-step ks: logical chunk 4 ks + g of key 16 kh + c
+  // sits at slot 16 (ks >> 2) + 4 ((ks & 3) ^ (c >> 2)) + (g ^ (c & 3)).
+  auto k_addr_bf16 = [&](uint32_t srec, int ks) -> uint32_t {
+    return ks < 16 ? srec + 256 * (ks >> 2) + 64 * ((ks & 3) ^ (c >> 2)) + 16 * (g ^ (c & 3))
+                   : srec + 16 * (64 + ((4 * (ks - 16) + g) ^ (c & 7)));
   };
-  auto v_addr = [&](int m) -> uint32_t { return vbase[m & 7] + 256 * (m >> 3); };
+  // Score-phase operands of the next block, loaded ahead (fp8: the key's tile
+  // scales and the first raw K chunks; bf16: the first K chunks).
+  constexpr int kKAhead = kFp8 ? 6 : 3;
+  v4f ksc;
+  v2u raw[kKAhead];
+  v4u ka[kKAhead];
+  auto prefetch_k = [&](uint32_t stage_k) {
+    const uint32_t srec = stage_k + s_lane;
+    if (kFp8) {
+      ksc = lds_load<v4f>(srec - 8 * g + kVDim);
+#pragma unroll
+      for (int d = 0; d < kKAhead; ++d) raw[d] = lds_load<v2u>(srec + 32 * d);
+    } else {
+#pragma unroll
+      for (int d = 0; d < kKAhead; ++d) ka[d] = lds_load<v4u>(k_addr_bf16(srec, d));
+    }
+  };
+  wait_dma<G::kLoadsPerWave*(G::kRing - 2)>();  // this wave's loads of block 0
+  lds_barrier();
+  prefetch_k(ring_base);
 
-  for (int64_t it = 0; it < iters; ++it) {
-    const int slot = (int)(it % G::kRing);
-    wait_dma<G::kLoadsPerWave*(G::kRing - 1)>();  // this wave's loads of block `it`
-    lds_barrier();                                 // everyone's loads landed; block free
-    convert_stage<kFp8>(lds, slot, it);
+  for (int it = 0; it < n_blocks; ++it) {
+    // Block it landed before the previous iteration's last barrier (or the
+    // prologue's); this barrier only frees the slot of block it - 1.
     lds_barrier();
-    issue_stage<kFp8>(lds, kv, it + G::kRing, iters, slot);
+    // Block it + kRing - 1 goes into the slot block it - 1 used, in three
+    // parts spread over the iteration so that a full memory queue stalls the
+    // wave as little as possible.
+    const uint32_t fill = ring_base + (uint32_t)free_slot * G::kStageBytes;
+    dma.template issue<0, kL / 3>(kv, zero, fill);
+    const uint32_t stage = ring_base + (uint32_t)slot * G::kStageBytes;
+    slot = slot + 1 == G::kRing ? 0 : slot + 1;
+    free_slot = free_slot + 1 == G::kRing ? 0 : free_slot + 1;
 
-    // ---- S^T = K Q^T for 32 keys x this wave's 16 heads. Operands run two
-    // k-steps ahead of the MFMAs; the scheduling barriers keep that order.
-    v4f s0 = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    v4f s1 = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    v4u ka[2][2];
-#pragma unroll
-    for (int d = 0; d < 2; ++d) {
-      ka[d][0] = *(lds_u4)(uintptr_t)k_addr(d);
-      ka[d][1] = *(lds_u4)(uintptr_t)(k_addr(d) + kHalf);
-    }
-#pragma unroll
-    for (int ks = 0; ks < kSteps; ++ks) {
-      const v4u a0 = ka[ks & 1][0];
-      const v4u a1 = ka[ks & 1][1];
-      if (ks + 2 < kSteps) {
-        ka[ks & 1][0] = *(lds_u4)(uintptr_t)k_addr(ks + 2);
-        ka[ks & 1][1] = *(lds_u4)(uintptr_t)(k_addr(ks + 2) + kHalf);
-      }
-      s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(a0), qb[ks], s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(a1), qb[ks], s1, 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-
-    // ---- online softmax (log2 domain); lane holds head c, keys 16t+4g+r.
-    float x[8];
-    float mx = neg_inf;
+    // ---- S^T = K Q^T: keys 16 kh + (0..15) x heads 32 hh + (0..31); two
+    // accumulators per head tile (even / odd k-steps) keep four MFMA chains.
+    const uint32_t srec = stage + s_lane;  // fp8: + 8g already
+    v4f sa[2][2];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const bool valid = lds.rows[it * kBlock + 16 * t + 4 * g + r] >= 0;
-        const float v = valid ? (t ? s1[r] : s0[r]) * scale_log2 : neg_inf;
-        x[4 * t + r] = v;
-        mx = fmaxf(mx, v);
+      for (int u = 0; u < 2; ++u) sa[t][u] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    if (kFp8) {
+      v4u rope[2];
+#pragma unroll
+      for (int ks = 0; ks < kSteps; ++ks) {
+        v8bf a;
+        if (ks < 16) {
+          a = dequant8(raw[ks % kKAhead], ksc[ks >> 2]);
+          if (ks + kKAhead < 16) {
+            raw[ks % kKAhead] = lds_load<v2u>(srec + 32 * (ks + kKAhead));
+          } else if (ks + kKAhead < 18) {
+            rope[ks + kKAhead - 16] = lds_load<v4u>(srec + 8 * g + kVDim + 16 + 64 * (ks + kKAhead - 16));
+          }
+        } else {
+          a = as_v8bf(rope[ks - 16]);
+        }
+        mfma_qb(sa[0][ks & 1], a, qb[0][ks]);
+        mfma_qb(sa[1][ks & 1], a, qb[1][ks]);
+        __builtin_amdgcn_sched_barrier(0);
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const bool need = mx > m_run + kRescaleThreshold || (m_run == neg_inf && mx != neg_inf);
-    if (__builtin_amdgcn_ballot_w64(need)) {
-      const float m_new = fmaxf(m_run, mx);
-      const float alpha = (m_run == neg_inf) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-      m_run = m_new;
-      l_run *= alpha;
+    } else {
 #pragma unroll
-      for (int m = 0; m < kVDim / 16; ++m) o[m] *= alpha;
+      for (int ks = 0; ks < kSteps; ++ks) {
+        const v8bf a = as_v8bf(ka[ks % kKAhead]);
+        if (ks + kKAhead < kSteps) ka[ks % kKAhead] = lds_load<v4u>(k_addr_bf16(srec, ks + kKAhead));
+        mfma_qb(sa[0][ks & 1], a, qb[0][ks]);
+        mfma_qb(sa[1][ks & 1], a, qb[1][ks]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
-    float p[8];
-    const bool live = m_run != neg_inf;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      p[j] = live ? __builtin_amdgcn_exp2f(x[j] - m_run) : 0.0f;
-      l_run += p[j];
-    }
-    const v8bf pb = as_v8bf(make_uint4(pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]),
-                                       pack_bf16(p[4], p[5]), pack_bf16(p[6], p[7])));
 
-    // ---- O^T += V^T P^T over 512 dims: dims 16m + 4qq are logical chunk
-    // 2m + qq/2 of rows vr and 16 + vr. Transpose loads run kVAhead m-tiles
-    // ahead of the MFMAs.
-    constexpr int kVAhead = 4;
-    v4s vlo[kVAhead], vhi[kVAhead];
+    dma.template issue<kL / 3, 2 * kL / 3>(kv, zero, fill);
+
+    // Operands of the softmax, issued before the MFMA results are read.
+    const v4i valid = lds_load<v4i>(rows_base + 4 * (uint32_t)(it * kBlock + 16 * kh + 4 * g));
+    v4f vsc[4];  // fp8: tile scales of keys 16 kh + 4g + r
+    if (kFp8) {
 #pragma unroll
-    for (int d = 0; d < kVAhead; ++d) {
-      vlo[d] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)v_addr(d));
-      vhi[d] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)(v_addr(d) + kHalf));
+      for (int r = 0; r < 4; ++r) vsc[r] = lds_load<v4f>(stage + G::record_offset(16 * kh + 4 * g + r) + kVDim);
     }
+    mfma_drain(sa[0][0], sa[0][1], sa[1][0], sa[1][1]);
+
+    // ---- block max per head. Lane (c, g) holds keys 16 kh + 4g + r of
+    // heads 32 hh + 16t + c; the max over g uses the row-swap permutes.
+    float x[2][4];
 #pragma unroll
-    for (int m = 0; m < kVDim / 16; ++m) {
-      const v8bf a = __builtin_bit_cast(
-          v8bf, __builtin_shufflevector(vlo[m % kVAhead], vhi[m % kVAhead], 0, 1, 2, 3, 4, 5, 6, 7));
-      if (m + kVAhead < kVDim / 16) {
-        const uint32_t va = v_addr(m + kVAhead);
-        vlo[m % kVAhead] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)va);
-        vhi[m % kVAhead] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)(va + kHalf));
+    for (int t = 0; t < 2; ++t) {
+      const v4f s = sa[t][0] + sa[t][1];
+      float mx = neg_inf;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        x[t][r] = valid[r] >= 0 ? s[r] * scale_log2 : neg_inf;
+        mx = fmaxf(mx, x[t][r]);
       }
-      o[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, o[m], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
+      mx = max_across_rows(mx);
+      if (g == 0) lds_store<float>(max_base + 4 * (kh * kHeadsPerGroup + 32 * hh + 16 * t + c), mx);
+    }
+    lds_barrier();
+
+    // ---- running max of all 64 heads, identical in every wave.
+    float alpha[4];
+    bool any = false;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float mx = fmaxf(lds_load<float>(max_base + 4 * (16 * t + c)),
+                             lds_load<float>(max_base + 4 * (kHeadsPerGroup + 16 * t + c)));
+      const bool need = mx > m_run[t] + kRescaleThreshold || (m_run[t] == neg_inf && mx != neg_inf);
+      const float m_new = need ? fmaxf(m_run[t], mx) : m_run[t];
+      // exp2(-inf) = 0 covers the first valid block.
+      alpha[t] = need ? __builtin_amdgcn_exp2f(m_run[t] - m_new) : 1.0f;
+      m_run[t] = m_new;
+      any |= need;
+    }
+    const bool rescale = __builtin_amdgcn_ballot_w64(any) != 0;
+
+    // ---- probabilities of this wave's keys and heads -> LDS (one copy per
+    // V scale tile for fp8, scaled by that tile's per-key scale).
+    float p[2][4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      // Head tile 2 hh + t. The empty asm hides where the two candidates come
+      // from, so the select is not turned into a dynamically indexed (and
+      // therefore private-memory) array access.
+      float m_lo = m_run[t], m_hi = m_run[2 + t], a_lo = alpha[t], a_hi = alpha[2 + t];
+      asm volatile("" : "+v"(m_lo), "+v"(m_hi), "+v"(a_lo), "+v"(a_hi));
+      const float mr = hh ? m_hi : m_lo;
+      l_part[t] *= hh ? a_hi : a_lo;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        p[t][r] = mr == neg_inf ? 0.0f : __builtin_amdgcn_exp2f(x[t][r] - mr);
+        l_part[t] += p[t][r];
+      }
+    }
+    // P^T of head tile t for PV lane (c, g) sits at [version][t][lane], 16
+    // bytes: keys 4g + r from key half 0, then 16 + 4g + r from half 1.
+    const uint32_t p_own = p_base + (uint32_t)(2 * hh * 64 + lane) * 16 + 8 * kh;
+    if (kFp8) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const v2u pk{pack_bf16(p[t][0] * vsc[0][v], p[t][1] * vsc[1][v]),
+                       pack_bf16(p[t][2] * vsc[2][v], p[t][3] * vsc[3][v])};
+          lds_store<v2u>(p_own + (uint32_t)(v * 4 + t) * 1024, pk);
+        }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const v2u pk{pack_bf16(p[t][0], p[t][1]), pack_bf16(p[t][2], p[t][3])};
+        lds_store<v2u>(p_own + (uint32_t)t * 1024, pk);
+      }
+    }
+    dma.template issue<2 * kL / 3, kL>(kv, zero, fill);
+    wait_dma<G::kLoadsPerWave*(G::kRing - 2)>();  // this wave's loads of block it + 1
+    lds_barrier();  // P visible; every wave's loads of block it + 1 landed
+    dma.load_rows(lds.rows, it + G::kRing, n_blocks);  // for the next iteration
+    const uint32_t next_stage = ring_base + (uint32_t)slot * G::kStageBytes;  // slot of it + 1
+    if (it + 1 < n_blocks) prefetch_k(next_stage);
+
+    // ---- O^T += V^T P^T for dims 128 wave + (0..127), all 64 heads.
+    if (rescale) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int m = 0; m < 8; ++m) o[t][m] *= alpha[t];
+    }
+    v8bf pb[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      pb[t] = as_v8bf(lds_load<v4u>(p_base + (uint32_t)(((kFp8 ? wave : 0) * 4 + t) * 64 + lane) * 16));
+    if (kFp8) {
+      const uint32_t vaddr = stage + G::record_offset(vkey) + 128 * wave + 8 * vq;
+      constexpr int kAhead = 3;
+      v2u vr[kAhead];
+#pragma unroll
+      for (int d = 0; d < kAhead; ++d)
+        vr[d] = __builtin_bit_cast(v2u, __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i)(uintptr_t)(vaddr + 16 * d)));
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const v8bf a = dequant8(vr[m % kAhead], 1.0f);
+        if (m + kAhead < 8)
+          vr[m % kAhead] = __builtin_bit_cast(
+              v2u, __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i)(uintptr_t)(vaddr + 16 * (m + kAhead))));
+#pragma unroll
+        for (int t = 0; t < 4; ++t) o[t][m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[t], o[t][m], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+      // Dims 16 mg + 4 qq of rows vrow and 16 + vrow (vrow = 4g + jj): logical
+      // chunk 2 mg + (qq >> 1), slot 16 (mg >> 3) + 2 ((mg & 7) ^ (vrow >> 1)) +
+      // ((qq >> 1) ^ (vrow & 1)), with mg = 8 wave + m.
+      const int jj = c >> 2;
+      const int qq = c & 3;
+      const int vrow = 4 * g + jj;
+      const uint32_t vbase = stage + G::record_offset(vrow) + 256 * wave +
+                             16 * ((qq >> 1) ^ (vrow & 1)) + 8 * (qq & 1);
+      constexpr uint32_t kHalf = 16 * G::kRecordBytes;
+      auto v_addr = [&](int m) -> uint32_t { return vbase + 32 * (m ^ (vrow >> 1)); };
+      constexpr int kAhead = 3;
+      v4s vlo[kAhead], vhi[kAhead];
+#pragma unroll
+      for (int d = 0; d < kAhead; ++d) {
+        vlo[d] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)v_addr(d));
+        vhi[d] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)(v_addr(d) + kHalf));
+      }
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const v8bf a = __builtin_bit_cast(
+            v8bf, __builtin_shufflevector(vlo[m % kAhead], vhi[m % kAhead], 0, 1, 2, 3, 4, 5, 6, 7));
+        if (m + kAhead < 8) {
+          vlo[m % kAhead] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)v_addr(m + kAhead));
+          vhi[m % kAhead] =
+              __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)(v_addr(m + kAhead) + kHalf));
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) o[t][m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[t], o[t][m], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
   }
   // Drain the DMA issued past the last block (padding loads) before exit.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  l_run += __shfl_xor(l_run, 16);
-  l_run += __shfl_xor(l_run, 32);
-  const float inv_l = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-  // Lane holds head c, dims 16m + 4g + r.
-  uint16_t* orow = out + ((row * heads + head0 + c) * kVDim) + 4 * g;
+  // ---- row sums of all 64 heads, then O / l.
 #pragma unroll
-  for (int m = 0; m < kVDim / 16; ++m)
-    *reinterpret_cast<uint2*>(orow + 16 * m) =
-        make_uint2(pack_bf16(o[m][0] * inv_l, o[m][1] * inv_l),
-                   pack_bf16(o[m][2] * inv_l, o[m][3] * inv_l));
+  for (int t = 0; t < 2; ++t) {
+    float l = l_part[t];
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    if (g == 0) lds.row_sum[kh][32 * hh + 16 * t + c] = l;
+  }
+  __syncthreads();
+  uint16_t* obase = out + ((row * heads + head0 + c) * kVDim) + 128 * wave + 4 * g;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const float l = lds.row_sum[0][16 * t + c] + lds.row_sum[1][16 * t + c];
+    const float inv_l = l > 0.0f ? 1.0f / l : 0.0f;
+    uint16_t* orow = obase + (int64_t)16 * t * kVDim;
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+      *reinterpret_cast<uint2*>(orow + 16 * m) =
+          make_uint2(pack_bf16(o[t][m][0] * inv_l, o[t][m][1] * inv_l),
+                     pack_bf16(o[t][m][2] * inv_l, o[t][m][3] * inv_l));
+  }
 }
 
 template <bool kFp8>
@@ -432,8 +667,8 @@ extern "C" int dsa_sparse_mla_fp8_paged(const void* q, int64_t rows, int64_t hea
   using namespace dsa;
   int status = check_common(q, rows, heads, indices, topk, scale, out);
   if (status != kOk || rows == 0) return status;
-  DSA_CHECK_ARG(pages >= 1 && n_tokens >= 1 && n_tokens <= pages * kPageTokens,
-                "page table must cover every token of a nonempty cache");
+  DSA_CHECK_ARG(pages >= 1 && n_tokens >= 1 && n_tokens < 0x7FFFFFFF,
+                "need a nonempty cache and 1 <= n_tokens < 2^31");
   DSA_CHECK_ARG(pages * kPageTokens < 0x7FFFFFFF, "cache rows must fit int32");
   DSA_CHECK_ARG(cache && page_table, "null cache or page table");
   DSA_CHECK_ARG(reinterpret_cast<uintptr_t>(cache) % 16 == 0, "cache must be 16-byte aligned");
