@@ -41,8 +41,11 @@ FLAGS = [
 # sparse_mla: MFMA accumulators in VGPRs. The O accumulators are rescaled by
 # the online softmax (a VALU multiply); in AGPRs the compiler would keep a
 # VGPR copy of them and move all 128 registers on every key block.
+# logits: the same, plus no NaN canonicalisation around the ReLU (fmaxf would
+# otherwise cost two v_max_f32 per value in a VALU-bound epilogue).
 SOURCE_FLAGS = {
     "sparse_mla.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "logits.hip": ["-fno-honor-nans", "-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

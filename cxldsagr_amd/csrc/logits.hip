@@ -9,17 +9,25 @@
 // Mapping (gfx950, wave64):
 // * v_mfma_f32_16x16x128_f8f6f4 with A = 16 heads x 128 dims of one query
 //   (resident in VGPRs for the whole key loop) and B = 128 dims x 16 keys
-//   streamed from LDS; one instruction is a full 128-deep dot product.
+//   read from LDS; one instruction is a full 128-deep dot product.
 // * C layout: lane l, register r -> head 16t + 4(l/16) + r, key l%16. The
-//   head-weighted ReLU sum is 16 in-lane FMAs per key per query; the four
-//   lane groups are then combined with a 2-step reduce-scatter so lane l ends
-//   with key l of a 64-key stage, giving one coalesced 256-byte row store.
-// * Work-group: 8 waves x 2 queries = 16 queries; key range split so the
-//   grid is about one work-group per CU. Work-groups that share a key range
-//   have block ids 8 apart when the split count is a multiple of 8, so they
-//   land on the same XCD and share its L2.
-// * K stages of 64 keys x 128 B are double-buffered through LDS with an XOR
-//   swizzle of the 16-byte chunks (chunk ^ (key & 7)) against bank conflicts.
+//   head-weighted ReLU sum is 16 in-lane (max, fma) pairs per key per query;
+//   the four lane rows are then combined with a reduce-scatter on the gfx950
+//   row-swap permutes (v_permlane32_swap, v_permlane16_swap) so lane l ends
+//   with key l of a 64-key stage: one coalesced 256-byte row store.
+// * The epilogue of one (query, 16-key) unit runs while the four MFMAs of the
+//   next unit execute (explicitly interleaved).
+// * Work-group: 4 waves (one per SIMD, so Q of 4 queries stays in registers
+//   and each B operand read from LDS feeds 16 MFMAs) x 4 queries = 16
+//   queries; the key range is split so the grid is about one work-group per CU.
+// * K stages (64 keys x 128 B, plus the 64 key scales) arrive by LDS DMA
+//   (global_load_lds_dwordx4 / _dword) into a ring kRing - 1 stages ahead,
+//   with the 16-byte chunks of each key XOR-swizzled by (key & 7) against
+//   bank conflicts of the B-operand reads.
+// * Loads and stores never share a wave: vmcnt counts both, and with stores
+//   pending it no longer says which loads are done. Wave 0 issues every DMA
+//   (and waits on vmcnt for them) but stores nothing; its rows go through LDS
+//   to waves 1-3, which store their own rows and wave 0's in turn.
 #include "dsa_common.h"
 #include "../../include/dsa_gfx950.h"
 
@@ -28,35 +36,63 @@ namespace {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
 constexpr int kHeads = 64;
 constexpr int kDim = 128;
-constexpr int kWaves = 8;
-constexpr int kQueriesPerWave = 2;
+constexpr int kWaves = 4;
+constexpr int kQueriesPerWave = 4;
 constexpr int kQueriesPerBlock = kWaves * kQueriesPerWave;
 constexpr int kStageKeys = 64;
 constexpr int kThreads = kWaves * 64;
+constexpr int kRing = 4;
+constexpr int kKBytes = kStageKeys * kDim;         // 8 KB of keys per stage
+constexpr int kKLoads = kKBytes / (64 * 16);       // DMA instructions for the keys (wave 0)
+constexpr int kStageBytes = kKBytes + 64 * 4;      // + the stage's 64 key scales
 
-__device__ __forceinline__ v8i load_operand(const uint8_t* p) {
-  uint4 a = *reinterpret_cast<const uint4*>(p);
-  uint4 b = *reinterpret_cast<const uint4*>(p + 16);
-  v8i r;
-  r[0] = a.x; r[1] = a.y; r[2] = a.z; r[3] = a.w;
-  r[4] = b.x; r[5] = b.y; r[6] = b.z; r[7] = b.w;
-  return r;
+
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// part[u] holds lane-group partial sums for key (16u + l%16). Returns the
-// full sum for key l of the stage.
-__device__ __forceinline__ float reduce_scatter4(const float part[4], int group) {
-  const bool low = group < 2;
-  float send0 = low ? part[2] : part[0];
-  float send1 = low ? part[3] : part[1];
-  float a0 = (low ? part[0] : part[2]) + __shfl_xor(send0, 32);
-  float a1 = (low ? part[1] : part[3]) + __shfl_xor(send1, 32);
-  const bool even = (group & 1) == 0;
-  float send = even ? a1 : a0;
-  return (even ? a0 : a1) + __shfl_xor(send, 16);
+template <int kOutstanding>
+__device__ __forceinline__ void wait_dma() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kOutstanding) : "memory");
+}
+
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               ::"s"(lds_base), "v"(src) : "memory", "m0");
+}
+// Scalar-base forms: 16 or 4 bytes per lane from base + off (32-bit lane
+// offset) to lds_base + 16 l or + 4 l.
+__device__ __forceinline__ void dma16_s(const void* base, uint32_t off, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               ::"s"(lds_base), "v"(off), "s"(base) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4_s(const void* base, uint32_t off, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2"
+               ::"s"(lds_base), "v"(off), "s"(base) : "memory", "m0");
+}
+
+// Sum of x over lanes l and l ^ 32 (first operand) and of y likewise, with
+// the results exchanged so that lanes 0-31 get x's sum and lanes 32-63 y's.
+__device__ __forceinline__ float fold32(float x, float y) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// The same for lanes l and l ^ 16: rows 0 and 2 get x's sums, rows 1 and 3 y's.
+__device__ __forceinline__ float fold16(float x, float y) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// part[u] holds the row-partial sums for key 16u + l % 16; returns the total
+// for key l of the stage.
+__device__ __forceinline__ float reduce_scatter4(const float part[4]) {
+  const float a0 = fold32(part[0], part[2]);  // rows 0-1: key group 0, rows 2-3: group 2
+  const float a1 = fold32(part[1], part[3]);  // rows 0-1: group 1, rows 2-3: group 3
+  return fold16(a0, a1);                      // row g: key group g
 }
 
 __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
@@ -64,7 +100,7 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
     const float* __restrict__ kscale, const int32_t* __restrict__ starts,
     const int32_t* __restrict__ ends, int64_t query_start, int64_t rows, int64_t columns,
     int64_t ldo, int64_t keys_per_split, float* __restrict__ out) {
-  __shared__ __align__(16) uint8_t lds_k[2][kStageKeys * kDim];
+  __shared__ __align__(16) uint8_t ring[kRing][kStageBytes];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -82,108 +118,182 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
   for (int i = 0; i < kQueriesPerBlock; ++i) {
     const int64_t qi = q0 + i;
     if (qi < rows) {
-      int64_t e = ends ? (int64_t)ends[qi] : query_start + qi + 1;
+      const int64_t e = ends ? (int64_t)ends[qi] : query_start + qi + 1;
       max_end = e > max_end ? e : max_end;
     }
   }
   if (max_end > columns) max_end = columns;
   const int64_t kend = ke < max_end ? ke : max_end;
-  const int64_t stages = kend > kb ? (kend - kb + kStageKeys - 1) / kStageKeys : 0;
+  const int stages = kend > kb ? (int)((kend - kb + kStageKeys - 1) / kStageKeys) : 0;
 
-  // Per-wave query operands and weights.
+  // Per-wave query operands and head weights (lane rows: heads 16t + 4g + r).
+  // Key positions fit int32 (the launcher checks ldo < 2^31).
   v8i qa[kQueriesPerWave][4];
   float wt[kQueriesPerWave][16];
-  int64_t qrow[kQueriesPerWave];
-  int64_t qs[kQueriesPerWave], qe[kQueriesPerWave];
-  bool qlive[kQueriesPerWave];
+  int32_t qs[kQueriesPerWave], qe[kQueriesPerWave];
+  const int64_t qw = q0 + wave * kQueriesPerWave;
 #pragma unroll
   for (int j = 0; j < kQueriesPerWave; ++j) {
-    const int64_t qi = q0 + wave * kQueriesPerWave + j;
-    qrow[j] = qi;
-    qlive[j] = qi < rows;
-    const int64_t qc = qlive[j] ? qi : 0;
+    const int64_t qi = qw + j;
+    const bool live = qi < rows;
+    const int64_t qc = live ? qi : 0;
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
-      qa[j][t] = load_operand(q + ((qc * kHeads + 16 * t + col) * kDim + 32 * group));
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        wt[j][4 * t + r] = qlive[j] ? w[qc * kHeads + 16 * t + 4 * group + r] : 0.0f;
-    qs[j] = starts ? (int64_t)starts[qc] : 0;
-    qe[j] = ends ? (int64_t)ends[qc] : query_start + qc + 1;
-    if (qe[j] > columns) qe[j] = columns;
-  }
-
-  // Stage loader: thread -> (key tid/8, 16-byte chunk tid%8).
-  const int lkey = tid >> 3;
-  const int lchunk = tid & 7;
-  const int lds_store_off = lkey * kDim + ((lchunk ^ (lkey & 7)) << 4);
-  auto gload = [&](int64_t key0) -> uint4 {
-    const int64_t key = key0 + lkey;
-    if (key < columns) return *reinterpret_cast<const uint4*>(k + key * kDim + lchunk * 16);
-    return make_uint4(0, 0, 0, 0);
-  };
-
-  if (stages > 0) {
-    uint4 v = gload(kb);
-    *reinterpret_cast<uint4*>(&lds_k[0][lds_store_off]) = v;
-  }
-  __syncthreads();
-
-  for (int64_t s = 0; s < stages; ++s) {
-    const int64_t key0 = kb + s * kStageKeys;
-    const int buf = (int)(s & 1);
-    uint4 next = make_uint4(0, 0, 0, 0);
-    if (s + 1 < stages) next = gload(key0 + kStageKeys);
-
-    float part[kQueriesPerWave][4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int key = 16 * u + col;
-      const uint8_t* base = &lds_k[buf][key * kDim];
-      const int c0 = (2 * group) ^ (key & 7);
-      const int c1 = (2 * group + 1) ^ (key & 7);
-      uint4 lo = *reinterpret_cast<const uint4*>(base + (c0 << 4));
-      uint4 hi = *reinterpret_cast<const uint4*>(base + (c1 << 4));
-      v8i b;
-      b[0] = lo.x; b[1] = lo.y; b[2] = lo.z; b[3] = lo.w;
-      b[4] = hi.x; b[5] = hi.y; b[6] = hi.z; b[7] = hi.w;
-#pragma unroll
-      for (int j = 0; j < kQueriesPerWave; ++j) {
-        v4f acc[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
-          acc[t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(qa[j][t], b, zero, 0, 0, 0,
-                                                                    0, 0, 0);
-        }
-        float p = 0.0f;
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) p = fmaf(fmaxf(acc[t][r], 0.0f), wt[j][4 * t + r], p);
-        part[j][u] = p;
-      }
+    for (int t = 0; t < 4; ++t) {
+      const v4u* src = reinterpret_cast<const v4u*>(q + ((qc * kHeads + 16 * t + col) * kDim + 32 * group));
+      const v4u lo = src[0], hi = src[1];
+      qa[j][t] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
     }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const v4f wv = *reinterpret_cast<const v4f*>(w + qc * kHeads + 16 * t + 4 * group);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) wt[j][4 * t + r] = live ? wv[r] : 0.0f;
+    }
+    // A dead query gets an empty visible range; its stores are skipped anyway.
+    int64_t e = ends ? (int64_t)ends[qc] : query_start + qc + 1;
+    if (e > columns) e = columns;
+    qs[j] = live ? (starts ? starts[qc] : 0) : 0;
+    qe[j] = live ? (int32_t)e : 0;
+  }
 
-    const int64_t key = key0 + lane;
-    const float ks = key < columns ? kscale[key] : 0.0f;
+  // DMA plan (wave 0 only): K chunk p = 64 i + lane of a stage (load i) is
+  // key 8i + lane / 8, stored chunk lane % 8 = logical chunk ^ (key & 7); then
+  // one 4-byte load per lane of the 64 key scales. Keys past the end re-read
+  // the last key (their columns are -inf), and stages past the end key 0.
+  const uint32_t ring_base = (uint32_t)(uintptr_t)&ring[0][0];
+  const int lane_key = lane >> 3;
+  const uint32_t lane_chunk = 16u * (uint32_t)((lane & 7) ^ (lane_key & 7));
+  auto issue = [&](int s) {
+    const uint32_t slot_base = ring_base + (uint32_t)(s % kRing) * kStageBytes;
+    const bool live = s < stages;
+    const int64_t key0 = live ? kb + (int64_t)s * kStageKeys : 0;
+    const int32_t last = live ? (int32_t)(columns - 1 - key0) : 0;  // >= 0: key0 < columns
+    const uint8_t* kbase = k + key0 * kDim;
+#pragma unroll
+    for (int i = 0; i < kKLoads; ++i) {
+      const int32_t key = min(8 * i + lane_key, last);
+      dma16_s(kbase, (uint32_t)key * kDim + lane_chunk, slot_base + i * 1024);
+    }
+    dma4_s(kscale + key0, 4u * (uint32_t)min(lane, last), slot_base + kKBytes);
+  };
+  // Wave 0's finished rows, [stage parity][query][key].
+  __shared__ __align__(16) float staged[2][kQueriesPerWave][kStageKeys];
+  auto store_staged = [&](int st) {
+    const int64_t key = kb + (int64_t)st * kStageKeys + lane;
 #pragma unroll
     for (int j = 0; j < kQueriesPerWave; ++j) {
-      const float total = reduce_scatter4(part[j], group);
-      if (qlive[j] && key < ke) {
-        const bool visible = key >= qs[j] && key < qe[j];
-        out[qrow[j] * ldo + key] = visible ? total * ks : neg_inf;
-      }
+      const int64_t qi = q0 + j;  // wave 0's queries
+      if (qi < rows && key < ke) out[qi * ldo + key] = staged[st & 1][j][lane];
     }
+  };
 
-    if (s + 1 < stages) *reinterpret_cast<uint4*>(&lds_k[buf ^ 1][lds_store_off]) = next;
-    __syncthreads();
+  // All compiler-visible global loads must be complete before the DMA wait
+  // accounting starts.
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  if (wave == 0) {
+#pragma unroll
+    for (int s = 0; s < kRing - 1; ++s) issue(s);
   }
 
+  for (int s = 0; s < stages; ++s) {
+    // Wave 0's loads of stage s have landed; stage s - 1 is free.
+    if (wave == 0) wait_dma<(kKLoads + 1) * (kRing - 2)>();
+    lds_barrier();
+    if (wave == 0) {
+      issue(s + kRing - 1);
+    } else if (s > 0 && wave == 1 + (s - 1) % (kWaves - 1)) {
+      store_staged(s - 1);
+    }
+
+    const uint32_t stage = ring_base + (uint32_t)(s % kRing) * kStageBytes;
+    const int64_t key0 = kb + (int64_t)s * kStageKeys;
+
+    // B operand of key group u: key 16u + col, logical chunks 2g, 2g + 1.
+    auto load_b = [&](int u) -> v8i {
+      const int key = 16 * u + col;
+      const uint32_t base = stage + key * kDim;
+      const v4u lo = *(const v4u __attribute__((address_space(3)))*)(uintptr_t)(base + (((2 * group) ^ (key & 7)) << 4));
+      const v4u hi = *(const v4u __attribute__((address_space(3)))*)(uintptr_t)(base + (((2 * group + 1) ^ (key & 7)) << 4));
+      return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    };
+
+    // Units i = 4u + j (key group u, query j): the MFMAs of unit i are issued
+    // before the epilogue of unit i - 1.
+    constexpr int kUnits = 4 * kQueriesPerWave;
+    float part[kQueriesPerWave][4];
+    v8i b[2];
+    b[0] = load_b(0);
+    b[1] = load_b(1);
+    v4f acc[2][4];
+    auto mfmas = [&](int i) {
+      const int u = i / kQueriesPerWave, j = i % kQueriesPerWave;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        acc[i & 1][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+            qa[j][t], b[u & 1], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0, 0, 0, 0);
+    };
+    auto epilogue = [&](int i) {
+      const int u = i / kQueriesPerWave, j = i % kQueriesPerWave;
+      // Four independent chains (one per head tile), so no fma waits on the
+      // previous one.
+      float pt[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) pt[t] = fmaxf(acc[i & 1][t][0], 0.0f) * wt[j][4 * t];
+#pragma unroll
+      for (int r = 1; r < 4; ++r)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) pt[t] = fmaf(fmaxf(acc[i & 1][t][r], 0.0f), wt[j][4 * t + r], pt[t]);
+      float p = (pt[0] + pt[1]) + (pt[2] + pt[3]);
+      // Pins the epilogue here: otherwise instruction selection sinks it below
+      // every MFMA of the stage and all 64 results stay live.
+      asm volatile("" : "+v"(p));
+      part[j][u] = p;
+    };
+    mfmas(0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 1; i < kUnits; ++i) {
+      mfmas(i);
+      // b[u & 1] is free once the last query of group u has its MFMAs issued.
+      const bool refill = i % kQueriesPerWave == kQueriesPerWave - 1 && i / kQueriesPerWave + 2 < 4;
+      if (refill) b[(i / kQueriesPerWave) & 1] = load_b(i / kQueriesPerWave + 2);
+      epilogue(i - 1);
+      // One MFMA, then the (max, fma) pairs of one accumulator of the
+      // previous unit, four times: the results read were issued a full unit
+      // earlier, and the VALU work runs under the MFMAs.
+      if (refill) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 9, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    epilogue(kUnits - 1);
+
+    const int32_t key = (int32_t)(key0 + lane);
+    const float ks = *(const float __attribute__((address_space(3)))*)(uintptr_t)(stage + kKBytes + 4 * lane);
+#pragma unroll
+    for (int j = 0; j < kQueriesPerWave; ++j) {
+      const float total = reduce_scatter4(part[j]);
+      const bool visible = key >= qs[j] && key < qe[j];
+      const float v = visible ? total * ks : neg_inf;
+      if (wave == 0) {
+        staged[s & 1][j][lane] = v;
+      } else if (qw + j < rows && key < ke) {
+        out[(qw + j) * ldo + key] = v;
+      }
+    }
+  }
+  if (stages > 0) {
+    lds_barrier();  // wave 0's last rows are staged
+    if (wave == 1 + (stages - 1) % (kWaves - 1)) store_staged(stages - 1);
+  }
+  // Drain the DMA issued past the last stage before exit.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
   // Columns of this split at or beyond every causal end: -inf.
-  const int64_t tail = kb + stages * kStageKeys;
+  const int64_t tail = kb + (int64_t)stages * kStageKeys;
   if (tail < ke) {
     for (int i = wave; i < kQueriesPerBlock; i += kWaves) {
       const int64_t qi = q0 + i;
@@ -210,8 +320,11 @@ extern "C" int dsa_indexer_logits_fp8(const void* q, const void* k, const float*
   if (rows == 0) return kOk;
   DSA_CHECK_ARG(q && k && weights && kscale && out, "null pointer");
   DSA_CHECK_ARG(reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
-                    reinterpret_cast<uintptr_t>(k) % 16 == 0,
-                "q and k must be 16-byte aligned");
+                    reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(weights) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(kscale) % 4 == 0,
+                "q, k and weights must be 16-byte aligned");
+  DSA_CHECK_ARG(columns * kDim < 0xFFFFFFFFll, "K must be addressable with 32-bit offsets");
   const int64_t qgroups = (rows + kQueriesPerBlock - 1) / kQueriesPerBlock;
   const int64_t cus = device_cu_count();
   int64_t splits = (cus + qgroups - 1) / qgroups;
@@ -220,6 +333,7 @@ extern "C" int dsa_indexer_logits_fp8(const void* q, const void* k, const float*
   per = (per + kStageKeys - 1) / kStageKeys * kStageKeys;
   splits = (ldo + per - 1) / per;
   DSA_CHECK_ARG(qgroups < 65536, "too many query rows for one launch");
+  DSA_CHECK_ARG(ldo < 0x7FFFFFFF - 64, "the logits row stride must fit int32");
   hipLaunchKernelGGL(logits_fp8_mfma, dim3((unsigned)splits, (unsigned)qgroups), dim3(kThreads),
                      0, stream, static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(k),
                      weights, kscale, starts, ends, query_start, rows, columns, ldo, per, out);

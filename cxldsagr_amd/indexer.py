@@ -152,6 +152,8 @@ def logits(q, k, weights, kscale, query_start, prefetch=None, *, _bounds=None,
         starts, ends = _bounds
         _check_tensor(starts, (rows,), torch.int32, device, "starts")
         _check_tensor(ends, (rows,), torch.int32, device, "ends")
+    # The kernel reads q, k and weights in 16-byte units.
+    q, k, weights = (t if t.data_ptr() % 16 == 0 else t.clone() for t in (q, k, weights))
     width = padded_columns(columns)
     output = torch.empty((rows, width), dtype=torch.float32, device=device)
     with torch.cuda.device(device):
