@@ -49,8 +49,10 @@ __device__ __forceinline__ uint64_t composite(float v, int64_t column) {
   return ((uint64_t)radix_key(v) << 32) | (uint64_t)(~(uint32_t)column);
 }
 
+constexpr int kSubHists = 4;  // histogram copies (by wave % 4) against atomic contention
+
 struct Shared {
-  uint32_t hist[kBins];
+  uint32_t hist[kSubHists][kBins];
   uint64_t sel[kMaxK];
   uint64_t buf[kRefineCap];
   uint32_t wave_sums[kThreads / 64];
@@ -68,8 +70,12 @@ __device__ void find_bucket(Shared& sh, uint32_t remaining) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const uint32_t h0 = sh.hist[2 * tid];
-  const uint32_t h1 = sh.hist[2 * tid + 1];
+  uint32_t h0 = 0, h1 = 0;
+#pragma unroll
+  for (int c = 0; c < kSubHists; ++c) {
+    h0 += sh.hist[c][2 * tid];
+    h1 += sh.hist[c][2 * tid + 1];
+  }
   uint32_t local = h0 + h1;
   // inclusive prefix over threads
   uint32_t incl = local;
@@ -103,27 +109,143 @@ __device__ void find_bucket(Shared& sh, uint32_t remaining) {
   __syncthreads();
 }
 
-__device__ __forceinline__ void clear_hist(Shared& sh) {
-  for (int i = threadIdx.x; i < kBins; i += kThreads) sh.hist[i] = 0;
+// Slot allocation with one LDS atomic per wave: lanes with `take` get
+// consecutive slots of `counter` in lane order.
+__device__ __forceinline__ uint32_t wave_slot(uint32_t* counter, bool take) {
+  const uint64_t mask = __builtin_amdgcn_ballot_w64(take);
+  if (mask == 0) return 0;
+  const uint32_t lanes_below =
+      __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
+  const int leader = __builtin_ffsll((long long)mask) - 1;
+  uint32_t base = 0;
+  if ((int)(threadIdx.x & 63) == leader) base = atomicAdd(counter, (uint32_t)__builtin_popcountll(mask));
+  return __builtin_amdgcn_readlane(base, leader) + lanes_below;
 }
 
+__device__ __forceinline__ void clear_hist(Shared& sh) {
+  for (int i = threadIdx.x; i < kSubHists * kBins; i += kThreads) (&sh.hist[0][0])[i] = 0;
+}
+
+__device__ __forceinline__ uint32_t* my_hist(Shared& sh) { return sh.hist[(threadIdx.x >> 6) % kSubHists]; }
+
+// Calls f(value, column) for every element of the row, each thread with four
+// 16-byte loads in flight.
 template <typename F>
 __device__ __forceinline__ void for_each_element(const float* row, int64_t cols, bool vec, F&& f) {
   if (vec) {
     const int64_t nvec = cols >> 2;
     const float4* row4 = reinterpret_cast<const float4*>(row);
-    for (int64_t i = threadIdx.x; i < nvec; i += kThreads) {
+    constexpr int kDepth = 4;
+    int64_t i = threadIdx.x;
+    for (; i + (kDepth - 1) * kThreads < nvec; i += kDepth * kThreads) {
+      float4 v[kDepth];
+#pragma unroll
+      for (int d = 0; d < kDepth; ++d) v[d] = row4[i + d * kThreads];
+#pragma unroll
+      for (int d = 0; d < kDepth; ++d) {
+        const int64_t c = 4 * (i + d * kThreads);
+        f(v[d].x, c);
+        f(v[d].y, c + 1);
+        f(v[d].z, c + 2);
+        f(v[d].w, c + 3);
+      }
+    }
+    for (; i < nvec; i += kThreads) {
       const float4 v = row4[i];
       f(v.x, 4 * i);
       f(v.y, 4 * i + 1);
       f(v.z, 4 * i + 2);
       f(v.w, 4 * i + 3);
     }
-    for (int64_t i = 4 * nvec + threadIdx.x; i < cols; i += kThreads) f(row[i], i);
+    for (int64_t j = 4 * nvec + threadIdx.x; j < cols; j += kThreads) f(row[j], j);
   } else {
-    for (int64_t i = threadIdx.x; i < cols; i += kThreads) f(row[i], i);
+    for (int64_t j = threadIdx.x; j < cols; j += kThreads) f(row[j], j);
   }
 }
+
+// Row elements in batches: each thread gets kBatch elements per call of f
+// (values, columns, validity), loaded as kBatch / 4 float4 in flight, with
+// every lane active in every call (invalid slots past the row end).
+constexpr int kBatch = 16;
+template <typename F>
+__device__ __forceinline__ void for_each_batch(const float* row, int64_t cols, bool vec, F&& f) {
+  const int64_t nvec = (cols + 3) >> 2;
+  constexpr int kVec = kBatch / 4;
+  for (int64_t base = 0; base < nvec; base += (int64_t)kVec * kThreads) {
+    float v[kBatch];
+    int64_t c[kVec];
+#pragma unroll
+    for (int d = 0; d < kVec; ++d) {
+      const int64_t i = base + (int64_t)d * kThreads + threadIdx.x;
+      c[d] = 4 * i;
+      if (vec && 4 * i + 3 < cols) {
+        const float4 x = reinterpret_cast<const float4*>(row)[i];
+        v[4 * d] = x.x;
+        v[4 * d + 1] = x.y;
+        v[4 * d + 2] = x.z;
+        v[4 * d + 3] = x.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[4 * d + e] = 4 * i + e < cols ? row[4 * i + e] : 0.0f;
+      }
+    }
+    f(v, c);
+  }
+}
+
+// A row of up to kResident * kThreads elements is read from memory once and
+// kept in registers (thread t: float4 slots d * kThreads + t) for both the
+// histogram and the selection pass.
+constexpr int kResidentVec = 17;
+constexpr int64_t kResidentCols = 4 * kResidentVec * kThreads;  // 69632
+
+struct Resident {
+  float v[4 * kResidentVec];
+  __device__ __forceinline__ void load(const float* row, int64_t cols) {
+#pragma unroll
+    for (int d = 0; d < kResidentVec; ++d) {
+      const int64_t i = (int64_t)d * kThreads + threadIdx.x;
+      if (4 * i + 3 < cols) {
+        const float4 x = reinterpret_cast<const float4*>(row)[i];
+        v[4 * d] = x.x;
+        v[4 * d + 1] = x.y;
+        v[4 * d + 2] = x.z;
+        v[4 * d + 3] = x.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[4 * d + e] = 4 * i + e < cols ? row[4 * i + e] : 0.0f;
+      }
+    }
+  }
+  template <typename F>
+  __device__ __forceinline__ void for_each(int64_t cols, F&& f) const {
+#pragma unroll
+    for (int d = 0; d < kResidentVec; ++d) {
+      const int64_t c = 4 * ((int64_t)d * kThreads + threadIdx.x);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (c + e < cols) f(v[4 * d + e], c + e);
+    }
+  }
+  // Batches of 16 values (4 float4 slots) in the for_each_batch format; slots
+  // past kResidentVec get columns past the row end.
+  template <typename F>
+  __device__ __forceinline__ void for_each_batch(int64_t cols, F&& f) const {
+#pragma unroll
+    for (int b = 0; b < (kResidentVec + 3) / 4; ++b) {
+      float bv[16];
+      int64_t bc[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int d = 4 * b + q;
+        bc[q] = d < kResidentVec ? 4 * ((int64_t)d * kThreads + threadIdx.x) : cols;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bv[4 * q + e] = d < kResidentVec ? v[4 * d + e] : 0.0f;
+      }
+      f(bv, bc);
+    }
+  }
+};
 
 __global__ __launch_bounds__(kThreads, 1) void topk_rows(const float* __restrict__ scores,
                                                         int64_t cols, int64_t ld, int count,
@@ -144,11 +266,14 @@ __global__ __launch_bounds__(kThreads, 1) void topk_rows(const float* __restrict
     for (int64_t i = tid; i < cols; i += kThreads) sh.sel[i] = composite(row[i], i);
   } else {
     // ---- level 0 histogram over the row
+    const bool resident = vec && cols <= kResidentCols;
+    Resident res;
+    if (resident) res.load(row, cols);
     clear_hist(sh);
     __syncthreads();
-    for_each_element(row, cols, vec, [&](float v, int64_t) {
-      atomicAdd(&sh.hist[radix_key(v) >> 21], 1u);
-    });
+    auto count_top = [&](float v, int64_t) { atomicAdd(&my_hist(sh)[radix_key(v) >> 21], 1u); };
+    if (resident) res.for_each(cols, count_top);
+    else for_each_element(row, cols, vec, count_top);
     __syncthreads();
     uint32_t remaining = (uint32_t)count;
     find_bucket(sh, remaining);
@@ -161,17 +286,53 @@ __global__ __launch_bounds__(kThreads, 1) void topk_rows(const float* __restrict
 
     if (in_lds) {
       const uint64_t d0 = prefix >> shift;
-      for_each_element(row, cols, vec, [&](float v, int64_t i) {
-        const uint64_t key = composite(v, i);
-        const uint64_t d = key >> 53;
-        if (d > d0) {
-          const uint32_t slot = atomicAdd(&sh.n_sel, 1u);
-          if (slot < kMaxK) sh.sel[slot] = key;
-        } else if (d == d0) {
-          const uint32_t slot = atomicAdd(&sh.n_buf, 1u);
-          if (slot < kRefineCap) sh.buf[slot] = key;
+      const uint32_t d0_32 = (uint32_t)d0;
+      const uint32_t lane = threadIdx.x & 63;
+      auto select_batch = [&](const float (&v)[kBatch], const int64_t (&c)[kBatch / 4]) {
+        // Per-lane counts of selected / candidate elements, their exclusive
+        // prefix over the wave from 5 bit-plane ballots (counts <= 16), and
+        // one LDS atomic per list per batch.
+        uint32_t dig[kBatch];
+        uint32_t cnt_sel = 0, cnt_buf = 0;
+#pragma unroll
+        for (int e = 0; e < kBatch; ++e) {
+          const bool ok = (int32_t)(c[e / 4] + (e % 4)) < (int32_t)cols;
+          dig[e] = ok ? radix_key(v[e]) >> 21 : 0xFFFFu;  // 0xFFFF: past the row end
+          cnt_sel += (dig[e] > d0_32 && dig[e] != 0xFFFFu) ? 1u : 0u;
+          cnt_buf += dig[e] == d0_32 ? 1u : 0u;
         }
-      });
+        uint32_t pre_sel = 0, pre_buf = 0, tot_sel = 0, tot_buf = 0;
+#pragma unroll
+        for (int bit = 0; bit < 5; ++bit) {
+          const uint64_t ms = __builtin_amdgcn_ballot_w64((cnt_sel >> bit) & 1u);
+          const uint64_t mb = __builtin_amdgcn_ballot_w64((cnt_buf >> bit) & 1u);
+          pre_sel += __builtin_amdgcn_mbcnt_hi((uint32_t)(ms >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)ms, 0)) << bit;
+          pre_buf += __builtin_amdgcn_mbcnt_hi((uint32_t)(mb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mb, 0)) << bit;
+          tot_sel += (uint32_t)__builtin_popcountll(ms) << bit;
+          tot_buf += (uint32_t)__builtin_popcountll(mb) << bit;
+        }
+        if (tot_sel + tot_buf == 0) return;
+        uint32_t base_sel = 0, base_buf = 0;
+        if (lane == 0) {
+          if (tot_sel) base_sel = atomicAdd(&sh.n_sel, tot_sel);
+          if (tot_buf) base_buf = atomicAdd(&sh.n_buf, tot_buf);
+        }
+        uint32_t at_sel = __builtin_amdgcn_readfirstlane(base_sel) + pre_sel;
+        uint32_t at_buf = __builtin_amdgcn_readfirstlane(base_buf) + pre_buf;
+#pragma unroll
+        for (int e = 0; e < kBatch; ++e) {
+          if (dig[e] == 0xFFFFu) continue;
+          if (dig[e] > d0_32) {
+            if (at_sel < kMaxK) sh.sel[at_sel] = composite(v[e], c[e / 4] + (e % 4));
+            ++at_sel;
+          } else if (dig[e] == d0_32) {
+            if (at_buf < kRefineCap) sh.buf[at_buf] = composite(v[e], c[e / 4] + (e % 4));
+            ++at_buf;
+          }
+        }
+      };
+      if (resident) res.for_each_batch(cols, select_batch);
+      else for_each_batch(row, cols, vec, select_batch);
       __syncthreads();
       const uint32_t nbuf = sh.n_buf < kRefineCap ? sh.n_buf : kRefineCap;
       for (int level = 1; level < kLevels && !resolved; ++level) {
@@ -181,7 +342,7 @@ __global__ __launch_bounds__(kThreads, 1) void topk_rows(const float* __restrict
         const uint64_t mask = (1ull << kWidth[level]) - 1;
         for (uint32_t i = tid; i < nbuf; i += kThreads) {
           const uint64_t key = sh.buf[i];
-          if ((key >> shift) == (prefix >> shift)) atomicAdd(&sh.hist[(key >> s) & mask], 1u);
+          if ((key >> shift) == (prefix >> shift)) atomicAdd(&my_hist(sh)[(key >> s) & mask], 1u);
         }
         __syncthreads();
         find_bucket(sh, remaining);
@@ -193,10 +354,9 @@ __global__ __launch_bounds__(kThreads, 1) void topk_rows(const float* __restrict
       }
       for (uint32_t i = tid; i < nbuf; i += kThreads) {
         const uint64_t key = sh.buf[i];
-        if ((key >> shift) >= (prefix >> shift)) {
-          const uint32_t slot = atomicAdd(&sh.n_sel, 1u);
-          if (slot < kMaxK) sh.sel[slot] = key;
-        }
+        const bool take = (key >> shift) >= (prefix >> shift);
+        const uint32_t slot = wave_slot(&sh.n_sel, take);
+        if (take && slot < kMaxK) sh.sel[slot] = key;
       }
     } else {
       for (int level = 1; level < kLevels && !resolved; ++level) {
@@ -208,7 +368,7 @@ __global__ __launch_bounds__(kThreads, 1) void topk_rows(const float* __restrict
         const int cur = shift;
         for_each_element(row, cols, vec, [&](float v, int64_t i) {
           const uint64_t key = composite(v, i);
-          if ((key >> cur) == want) atomicAdd(&sh.hist[(key >> s) & mask], 1u);
+          if ((key >> cur) == want) atomicAdd(&my_hist(sh)[(key >> s) & mask], 1u);
         });
         __syncthreads();
         find_bucket(sh, remaining);
@@ -222,36 +382,73 @@ __global__ __launch_bounds__(kThreads, 1) void topk_rows(const float* __restrict
       const int cur = shift;
       for_each_element(row, cols, vec, [&](float v, int64_t i) {
         const uint64_t key = composite(v, i);
-        if ((key >> cur) >= floor) {
-          const uint32_t slot = atomicAdd(&sh.n_sel, 1u);
-          if (slot < kMaxK) sh.sel[slot] = key;
-        }
+        const bool take = (key >> cur) >= floor;
+        const uint32_t slot = wave_slot(&sh.n_sel, take);
+        if (take && slot < kMaxK) sh.sel[slot] = key;
       });
     }
   }
   __syncthreads();
 
   // ---- bitonic sort of `count` keys, descending (padding keys are 0).
-  int padded = 1;
+  // Thread t holds positions 2t and 2t + 1 in registers. Partners at stride
+  // 1 are in the same thread, strides 2..64 in the same wave (lane ^ s/2,
+  // exchanged with lane shuffles); only strides >= 128 go through LDS.
+  int padded = 2;
   while (padded < count) padded <<= 1;
   for (int i = count + tid; i < padded; i += kThreads) sh.sel[i] = 0;
   __syncthreads();
+  const bool active = 2 * tid < padded;
+  uint64_t x0 = active ? sh.sel[2 * tid] : 0;
+  uint64_t x1 = active ? sh.sel[2 * tid + 1] : 0;
+  const int p0 = 2 * tid;
+  // Keeps the larger key at the lower position inside descending blocks.
+  auto order = [](uint64_t& lo, uint64_t& hi, bool descending) {
+    const bool swap = descending ? lo < hi : lo > hi;
+    const uint64_t a = lo, b = hi;
+    lo = swap ? b : a;
+    hi = swap ? a : b;
+  };
+  auto shfl64 = [](uint64_t v, int mask) -> uint64_t {
+    const uint32_t lo = __shfl_xor((uint32_t)v, mask);
+    const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), mask);
+    return ((uint64_t)hi << 32) | lo;
+  };
   for (int size = 2; size <= padded; size <<= 1) {
+    const bool desc = (p0 & size) == 0;  // same for p0 and p0 + 1 (size >= 2)
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = tid; i < (padded >> 1); i += kThreads) {
-        const int lo = 2 * stride * (i / stride) + (i % stride);
-        const int hi = lo + stride;
-        const uint64_t a = sh.sel[lo];
-        const uint64_t b = sh.sel[hi];
-        const bool descending = (lo & size) == 0;
-        if (descending ? (a < b) : (a > b)) {
-          sh.sel[lo] = b;
-          sh.sel[hi] = a;
+      if (stride == 1) {
+        order(x0, x1, desc);
+      } else if (stride <= 64) {
+        const int m = stride >> 1;  // partner lane distance
+        const uint64_t y0 = shfl64(x0, m);
+        const uint64_t y1 = shfl64(x1, m);
+        const bool lower = (p0 & stride) == 0;  // this lane holds the lower positions
+        // keep = the larger of the pair iff (lower == desc)
+        const bool keep_max = lower == desc;
+        x0 = keep_max ? (x0 > y0 ? x0 : y0) : (x0 < y0 ? x0 : y0);
+        x1 = keep_max ? (x1 > y1 ? x1 : y1) : (x1 < y1 ? x1 : y1);
+      } else {
+        if (active) {
+          sh.sel[p0] = x0;
+          sh.sel[p0 + 1] = x1;
         }
+        __syncthreads();
+        const uint64_t y0 = active ? sh.sel[p0 ^ stride] : 0;
+        const uint64_t y1 = active ? sh.sel[(p0 + 1) ^ stride] : 0;
+        const bool lower = (p0 & stride) == 0;
+        const bool keep_max = lower == desc;
+        x0 = keep_max ? (x0 > y0 ? x0 : y0) : (x0 < y0 ? x0 : y0);
+        x1 = keep_max ? (x1 > y1 ? x1 : y1) : (x1 < y1 ? x1 : y1);
+        __syncthreads();
       }
-      __syncthreads();
     }
   }
+  if (active) {
+    sh.sel[p0] = x0;
+    sh.sel[p0 + 1] = x1;
+  }
+  __syncthreads();
 
   float* vout = values + (int64_t)blockIdx.x * out_ld;
   int32_t* iout = ids + (int64_t)blockIdx.x * out_ld;
