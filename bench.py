@@ -49,6 +49,10 @@ def parse_args():
     p.add_argument("--copy-calibration-mib", type=int, default=0,
                    help="first run one plain device copy of this many MiB (scales PMC byte "
                         "counters in profiler runs)")
+    p.add_argument("--config", type=int, choices=[1, 3, 4], default=1,
+                   help="1: the headline layer (configs 1+2, default); 3: GR multi-user recall "
+                        "over a pinned-host token pool; 4: long-context stress, fp8 and bf16 KV")
+    p.add_argument("--users", type=int, default=16, help="config 3: users")
     return p.parse_args()
 
 
@@ -126,6 +130,10 @@ def main():
     from cxldsagr_amd.layer import DSALayer
     from cxldsagr_amd.workloads import make_layer_inputs
 
+    if args.config == 3:
+        return bench_config3(args)
+    if args.config == 4:
+        return bench_config4(args)
     device = torch.device("cuda", 0)
     history, queries, topk = args.history, args.queries, 2048
     tokens = history + queries
@@ -253,6 +261,152 @@ def main():
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(inputs, args.cpu_rows, topk)
     print(json.dumps(result))
+
+
+def stage_times(torch, fns, steps):
+    return {name: round(event_time_us(torch, fn, steps), 2) for name, fn in fns.items()}
+
+
+def bench_config4(args):
+    """Long-context stress: 131072 history + 512 queries, 10 % heavy
+    hitters in 8 spans, the layer over the fp8 paged cache and over bf16 records."""
+    import torch
+
+    from cxldsagr_amd import indexer
+    from cxldsagr_amd.layer import DSALayer
+    from cxldsagr_amd.workloads import make_layer_inputs
+
+    device = torch.device("cuda", 0)
+    history, queries, topk = 131072, 512, 2048
+    tokens = history + queries
+    inputs = make_layer_inputs(history, queries, seed=args.seed, heavy_fraction=0.10, spans=8)
+    result = {"config": 4, "history": history, "queries": queries, "topk": topk, "formats": {}}
+    for kv_format in ("fp8_paged", "bf16"):
+        layer = DSALayer(tokens, device=device, kv_format=kv_format,
+                         page_table=inputs.page_table if kv_format == "fp8_paged" else None)
+        layer.write_history(inputs.index_k[:history].to(device), inputs.kv[:history].to(device))
+        index_q, weights = inputs.index_q.to(device), inputs.weights.to(device)
+        index_k_new = inputs.index_k[history:].to(device).contiguous()
+        mla_q, kv_new = inputs.mla_q.to(device), inputs.kv[history:].to(device).contiguous()
+
+        def step():
+            layer.written = history
+            return layer.forward(index_q, index_k_new, weights, mla_q, kv_new)
+
+        out, selection = step()
+        for _ in range(args.warmup):
+            step()
+        layer_us = event_time_us(torch, step, args.steps)
+        q8, q_scale = indexer.quantize_index(index_q)
+        w_eff = (weights * q_scale[..., 0]).contiguous()
+        keys, kscale = layer.index_keys[:tokens], layer.index_scales[:tokens]
+        scores = indexer.logits(q8, keys, w_eff, kscale, history, _pad_to_stride=True)
+        ids = selection.token_ids
+        fns = {
+            "logits": lambda: indexer.logits(q8, keys, w_eff, kscale, history, _pad_to_stride=True),
+            "topk": lambda: indexer.exact_topk(scores, topk),
+            "sparse_mla": lambda: layer.consume(mla_q, selection, kv_new, history),
+        }
+        times = stage_times(torch, fns, args.steps)
+        pairs = queries * history + queries * (queries + 1) // 2
+        logits_flop = 2 * 64 * 128 * pairs
+        mla_flop = 2 * queries * topk * 128 * (576 + 512)
+        record = 656 if kv_format == "fp8_paged" else 1152
+        result["formats"][kv_format] = {
+            "layer_us": round(layer_us, 2),
+            "stage_us": times,
+            "logits_frac_fp8_peak": round(logits_flop / times["logits"] / 1e6 / PEAKS["fp8_TFLOPs"], 4),
+            "mla_frac_bf16_peak": round(mla_flop / times["sparse_mla"] / 1e6 / PEAKS["bf16_TFLOPs"], 4),
+            "gather_GBps": round(queries * topk * record / times["sparse_mla"] / 1e3, 1),
+        }
+        del layer, scores, out
+        torch.cuda.empty_cache()
+    print(json.dumps(result))
+
+
+def bench_config3(args):
+    """GR multi-user recall: `users` sessions of 65536 fp8 history records
+    in a pinned host arena, a shared HBM pool of 25 % of all history (262,144 slots for 16
+    users), resident indexer keys for every user, two rounds of 128 fresh candidate tokens per
+    user. Per user and layer: logits -> top-k -> exact recall (gather of the misses from pinned
+    host) -> sparse MLA over the pool."""
+    import torch
+
+    from cxldsagr_amd import indexer
+    from cxldsagr_amd.token_pool import TokenPool
+    from cxldsagr_amd.workloads import make_layer_inputs
+
+    device = torch.device("cuda", 0)
+    users, history, queries, topk = args.users, 65536, 128, 2048
+    tokens = history + queries
+    slots = users * history // 4
+    pool = TokenPool(users * history, slots, device=device, candidate_slots=queries,
+                     history_capacity=history)
+    state = []
+    for u in range(users):
+        inputs = make_layer_inputs(history, queries, seed=args.seed + u)
+        session = pool.allocate_session(history)
+        pool.write_history(session, inputs.kv[:history].to(device))
+        keys = torch.empty((tokens, 128), dtype=torch.float8_e4m3fn, device=device)
+        scales = torch.empty(tokens, dtype=torch.float32, device=device)
+        indexer.quantize_into(inputs.index_k[:history].to(device), keys[:history], scales[:history])
+        state.append({"session": session, "keys": keys, "scales": scales,
+                      "history_index_k": None})
+        del inputs
+    torch.cuda.synchronize()
+
+    def round_inputs(round_seed):
+        per_user = []
+        for u in range(users):
+            # Fresh candidates: new queries, index keys and KV for the 128 new tokens.
+            fresh = make_layer_inputs(0, queries, seed=round_seed * 1000 + u)
+            per_user.append({k: getattr(fresh, k).to(device) for k in
+                             ("index_q", "index_k", "weights", "mla_q", "kv")})
+        return per_user
+
+    def run_user(u, x, timing):
+        st = state[u]
+        q8, q_scale = indexer.quantize_index(x["index_q"])
+        w_eff = (x["weights"] * q_scale[..., 0]).contiguous()
+        indexer.quantize_into(x["index_k"], st["keys"][history:], st["scales"][history:])
+        scores = indexer.logits(q8, st["keys"], w_eff, st["scales"], history, _pad_to_stride=True)
+        _, ids = indexer.exact_topk(scores, topk)
+        pool.write_candidates(x["kv"])
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        physical = pool.ensure(ids, st["session"], written=tokens, transient_start=history)
+        e1.record()
+        timing.append((e0, e1))
+        return pool.attend(x["mla_q"], physical, 576**-0.5)
+
+    rounds = []
+    for r in range(2):
+        x = round_inputs(r + 1)
+        before = pool.metrics()["recalled_records"]
+        timing = []
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for u in range(users):
+            run_user(u, x[u], timing)
+        stop.record()
+        torch.cuda.synchronize()
+        pool.check_status()
+        recalled = pool.metrics()["recalled_records"] - before
+        fetch_us = sum(a.elapsed_time(b) for a, b in timing) * 1e3
+        fetch_bytes = recalled * 656
+        rounds.append({
+            "round": r + 1,
+            "layer_us": round(start.elapsed_time(stop) * 1e3, 1),
+            "fetch_records": recalled,
+            "fetch_bytes_per_layer": fetch_bytes,
+            "fetch_bytes_per_user": fetch_bytes // users,
+            "recall_us": round(fetch_us, 1),
+            "pcie_GBps": round(fetch_bytes / fetch_us / 1e3, 2) if fetch_us > 0 else None,
+        })
+    print(json.dumps({"config": 3, "users": users, "history": history, "queries": queries,
+                      "pool_slots": slots, "rounds": rounds}))
 
 
 if __name__ == "__main__":

@@ -210,7 +210,7 @@ def _topk_check(scores, k):
 @pytest.mark.parametrize(
     "rows,columns,k",
     [(1, 1, 1), (3, 17, 2048), (5, 257, 32), (32, 4099, 1024), (64, 1024, 2048),
-     (16, 65536, 1), (24, 66560, 2048)],
+     (16, 65536, 1), (24, 66560, 2048), (4, 69633, 2048), (8, 131584, 2048)],
 )
 def test_topk_bit_exact_with_causal_masks(gpu, rows, columns, k):
     generator = torch.Generator(device="cuda").manual_seed(191)
@@ -221,6 +221,16 @@ def test_topk_bit_exact_with_causal_masks(gpu, rows, columns, k):
     values, indices = _topk_check(scores, k)
     reference = scores.topk(min(k, columns), dim=-1)
     torch.testing.assert_close(values, reference.values, atol=0, rtol=0)
+
+
+def test_topk_misaligned_rows_stream_from_memory(gpu):
+    """Rows that do not start on a 16-byte boundary take the scalar streaming path."""
+    generator = torch.Generator(device="cuda").manual_seed(7)
+    base = torch.randn(6, 70004, device=gpu, generator=generator)
+    for offset, width in ((1, 70001), (3, 4099)):
+        scores = base[:, offset:offset + width]
+        assert scores.data_ptr() % 16
+        _topk_check(scores, 2048)
 
 
 def test_topk_every_k_small_ties(gpu):
