@@ -11,23 +11,22 @@
 // Mapping (gfx950, wave64, v_mfma_f32_16x16x32_bf16). A work-group owns one
 // query row and 64 heads and walks the selection in blocks of 32 keys; its 4
 // waves (one per SIMD) split each block twice:
-// * Scores: wave w computes S^T = K Q^T for key half kh = w / 2 (16 keys)
-//   and head half hh = w % 2 (32 heads), keeping Q^T of its 32 heads in
-//   registers (144). Each K operand read from LDS feeds two MFMAs.
+// * Scores: wave w computes S^T = K Q^T for all 32 keys (two 16-key tiles)
+//   and its 16 heads 16 w .. 16 w + 15, keeping Q^T of those heads in AGPRs
+//   (72). The block max of a head is then a reduction inside the wave, and
+//   the wave owns the running max, rescale factor and row sum of its heads.
 // * Values: wave w accumulates O^T for dims 128 w .. 128 w + 127 (one fp8
 //   scale tile) and all 64 heads (128 VGPRs). Each V operand feeds four MFMAs.
-// * Between the two, the per-head block maxima and the probabilities go
-//   through LDS. Every wave tracks the running max of all 64 heads (4 per
-//   lane) and updates it identically, so the rescale factors never travel.
-// LDS traffic per block is ~110 KB for 4.5 MFLOP (fp8), against ~330 KB when
-// every wave reads every key for 16 heads.
-//
+// * The probabilities and per-head rescale factors go through LDS, double
+//   buffered by block parity, behind the one barrier of the block. That
+//   barrier also publishes the next block's records and frees the ring slot
+//   of the previous block.
 // Records reach LDS by LDS DMA (global_load_lds_dwordx4: 16 bytes per lane,
 // no registers) into a ring of raw stages kRing - 1 blocks ahead, with the
 // wait counts managed explicitly. A block's loads are issued in three parts
-// spread over the iteration (a full memory queue stalls the issuing wave),
-// and the score operands of block it + 1 are read during the PV product of
-// block it. fp8 records are consumed raw:
+// spread over the PV product (a full memory queue stalls the issuing wave),
+// and the first score operands of block it + 1 are read right after the
+// barrier. fp8 records are consumed raw:
 // * K operand: lane (c, g) = (lane % 16, lane / 16) reads 8 e4m3 of key c and
 //   converts them with the key's tile scale (v_cvt_scalef32_pk_bf16_fp8;
 //   e4m3 x 2^k is exact in bf16).
@@ -44,7 +43,7 @@
 //
 // Key order inside a block: MFMA k-index 8g + j of the PV product is key
 // 16 (j / 4) + 4g + j % 4, which is where the S^T C layout of the two key
-// halves puts them (lane (c, g) holds keys 4g + r of its half, head c).
+// tiles puts them (lane (c, g) holds keys 4g + r of each tile, head c).
 //
 // Online softmax in log2 units with lazy rescaling (only when a block raises
 // the running max by more than 8, so p <= 2^8).
@@ -89,7 +88,7 @@ struct Geometry {
   static constexpr int kStageChunks = kBlock * kChunks + kHalfPad;
   static constexpr int kLoadsPerWave = (kStageChunks + kThreads - 1) / kThreads;  // 6 or 9
   static constexpr int kStageBytes = kLoadsPerWave * kThreads * 16;
-  static constexpr int kRing = kFp8 ? 5 : 3;
+  static constexpr int kRing = kFp8 ? 4 : 3;
   static constexpr int kPVersions = kFp8 ? 4 : 1;  // P copies (one per V scale tile)
   __device__ static constexpr uint32_t record_offset(int r) {
     return 16u * (uint32_t)(kChunks * r + (r >= 16 ? kHalfPad : 0));
@@ -99,11 +98,12 @@ struct Geometry {
 template <bool kFp8>
 struct __align__(16) Lds {
   uint8_t ring[Geometry<kFp8>::kRing][Geometry<kFp8>::kStageBytes];  // raw records
-  // P^T in PV B-operand order: [version][head tile][lane][key half][4 keys]
-  // bf16; lane (c, g) of tile t holds head 16t + c, keys 4g + r (+16).
-  uint8_t p[Geometry<kFp8>::kPVersions][4][64][16];
-  float block_max[2][kHeadsPerGroup];  // per key half
-  float row_sum[2][kHeadsPerGroup];
+  // P^T in PV B-operand order, by block parity: [parity][version][head tile]
+  // [lane] 16 bytes, lane (c, g) of tile t holding head 16t + c, keys 4g + r
+  // (r = 0..3) then 16 + 4g + r, bf16.
+  uint8_t p[2][Geometry<kFp8>::kPVersions][4][64][16];
+  float alpha[2][kHeadsPerGroup];  // per-head rescale factor of the block, by parity
+  float row_sum[kHeadsPerGroup];
   int32_t rows[kMaxSelected];  // physical record row per selected position, -1 = padding
 };
 
@@ -285,8 +285,6 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
   const int wave = threadIdx.x >> 6;
   const int g = lane >> 4;
   const int c = lane & 15;
-  const int kh = wave >> 1;  // key half of the score phase
-  const int hh = wave & 1;   // head half of the score phase
   const int64_t row = blockIdx.x;
   const int64_t head0 = (int64_t)blockIdx.y * kHeadsPerGroup;
   const int32_t* ids = indices + row * topk;
@@ -310,14 +308,12 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
     lds.rows[i] = phys;
   }
 
-  // Q^T operands of the score phase: head hh*32 + 16t + c, dims 32ks + 8g .. +8.
-  v8bf qb[2][kSteps];
+  // Q^T operands of the score phase: head 16 wave + c, dims 32ks + 8g .. +8.
+  v8bf qb[kSteps];
+  {
+    const uint16_t* qrow = q + ((row * heads + head0 + 16 * wave + c) * kQkDim) + 8 * g;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const uint16_t* qrow = q + ((row * heads + head0 + 32 * hh + 16 * t + c) * kQkDim) + 8 * g;
-#pragma unroll
-    for (int ks = 0; ks < kSteps; ++ks)
-      qb[t][ks] = as_v8bf(*reinterpret_cast<const v4u*>(qrow + 32 * ks));
+    for (int ks = 0; ks < kSteps; ++ks) qb[ks] = as_v8bf(*reinterpret_cast<const v4u*>(qrow + 32 * ks));
   }
   // O^T: head tile t (heads 16t + c), dims 128 wave + 16m + 4g + r.
   v4f o[4][8];
@@ -325,11 +321,8 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
   for (int t = 0; t < 4; ++t)
 #pragma unroll
     for (int m = 0; m < 8; ++m) o[t][m] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-  float m_run[4] = {neg_inf, neg_inf, neg_inf, neg_inf};  // heads 16t + c
-  // The same running max for the score heads 32 hh + 16t + c, and their row
-  // sums over this wave's key half.
-  float m_own[2] = {neg_inf, neg_inf};
-  float l_part[2] = {0.0f, 0.0f};
+  float m_run = neg_inf;  // running max of head 16 wave + c
+  float l_run = 0.0f;     // its row sum over this lane's keys
 
   // All compiler-visible global loads must be complete before the DMA wait
   // accounting starts; the builtin (vmcnt(0), expcnt/lgkmcnt untouched) also
@@ -349,196 +342,187 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
   }
   dma.load_rows(lds.rows, G::kRing - 1, n_blocks);
 
-  const uint32_t p_base = (uint32_t)(uintptr_t)&lds.p[0][0][0][0];
-  const uint32_t max_base = (uint32_t)(uintptr_t)&lds.block_max[0][0];
+  const uint32_t p_base = (uint32_t)(uintptr_t)&lds.p[0][0][0][0][0];
   const uint32_t rows_base = (uint32_t)(uintptr_t)&lds.rows[0];
+  constexpr uint32_t kPParity = G::kPVersions * 4 * 64 * 16;
   // V^T (tr8) rows: lane 2j + q of each 16-lane group reads key
   // 16 (j / 4) + 4g + j % 4 at dims +8q.
   const int vj = c >> 1;
   const int vq = c & 1;
   const int vkey = 16 * (vj >> 2) + 4 * g + (vj & 3);
 
-  // Loop-invariant lane parts of the stage addresses.
-  const uint32_t s_lane = G::record_offset(16 * kh + c) + (kFp8 ? 8 * g : 0);
-  int slot = 0;                 // ring slot of block it
-  int free_slot = G::kRing - 1;  // ring slot that receives block it + kRing - 1
-  // bf16 K operand of k-step ks: logical chunk 4 ks + g of key 16 kh + c
-  // sits at slot 16 (ks >> 2) + 4 ((ks & 3) ^ (c >> 2)) + (g ^ (c & 3)).
+  // bf16 K operand of k-step ks: logical chunk 4 ks + g of key 16t + c sits
+  // at slot 16 (ks >> 2) + 4 ((ks & 3) ^ (c >> 2)) + (g ^ (c & 3)).
   auto k_addr_bf16 = [&](uint32_t srec, int ks) -> uint32_t {
     return ks < 16 ? srec + 256 * (ks >> 2) + 64 * ((ks & 3) ^ (c >> 2)) + 16 * (g ^ (c & 3))
                    : srec + 16 * (64 + ((4 * (ks - 16) + g) ^ (c & 7)));
   };
-  // Score-phase operands of the next block, loaded ahead (fp8: the key's tile
-  // scales and the first raw K chunks; bf16: the first K chunks).
-  constexpr int kKAhead = kFp8 ? 6 : 3;
-  v4f ksc;
-  v2u raw[kKAhead];
-  v4u ka[kKAhead];
+  // Score operands of key tiles t = 0, 1 (keys 16t + c), loaded ahead (fp8:
+  // the key's tile scales and the first raw K chunks; bf16: the first chunks).
+  constexpr int kKAhead = kFp8 ? 4 : 2;
+  v4f ksc[2];
+  v2u raw[2][kKAhead];
+  v4u ka[2][kKAhead];
+  auto s_rec = [&](uint32_t stage_k, int t) -> uint32_t {
+    return stage_k + G::record_offset(16 * t + c) + (kFp8 ? 8 * g : 0);
+  };
   auto prefetch_k = [&](uint32_t stage_k) {
-    const uint32_t srec = stage_k + s_lane;
-    if (kFp8) {
-      ksc = lds_load<v4f>(srec - 8 * g + kVDim);
 #pragma unroll
-      for (int d = 0; d < kKAhead; ++d) raw[d] = lds_load<v2u>(srec + 32 * d);
-    } else {
+    for (int t = 0; t < 2; ++t) {
+      const uint32_t srec = s_rec(stage_k, t);
+      if (kFp8) {
+        ksc[t] = lds_load<v4f>(srec - 8 * g + kVDim);
 #pragma unroll
-      for (int d = 0; d < kKAhead; ++d) ka[d] = lds_load<v4u>(k_addr_bf16(srec, d));
+        for (int d = 0; d < kKAhead; ++d) raw[t][d] = lds_load<v2u>(srec + 32 * d);
+      } else {
+#pragma unroll
+        for (int d = 0; d < kKAhead; ++d) ka[t][d] = lds_load<v4u>(k_addr_bf16(srec, d));
+      }
     }
   };
-  wait_dma<G::kLoadsPerWave*(G::kRing - 2)>();  // this wave's loads of block 0
+  wait_dma<kL * (G::kRing - 2)>();  // this wave's loads of block 0
   lds_barrier();
   prefetch_k(ring_base);
 
+  int slot = 0;                  // ring slot of block it
+  int free_slot = G::kRing - 1;  // slot of block it - 1, refilled with block it + kRing - 1
   for (int it = 0; it < n_blocks; ++it) {
-    // Block it landed before the previous iteration's last barrier (or the
-    // prologue's); this barrier only frees the slot of block it - 1.
-    lds_barrier();
-    // Block it + kRing - 1 goes into the slot block it - 1 used, in three
-    // parts spread over the iteration so that a full memory queue stalls the
-    // wave as little as possible.
-    const uint32_t fill = ring_base + (uint32_t)free_slot * G::kStageBytes;
-    dma.template issue<0, kL / 3>(kv, zero, fill);
     const uint32_t stage = ring_base + (uint32_t)slot * G::kStageBytes;
-    slot = slot + 1 == G::kRing ? 0 : slot + 1;
-    free_slot = free_slot + 1 == G::kRing ? 0 : free_slot + 1;
+    const uint32_t parity = (uint32_t)(it & 1);
 
-    // ---- S^T = K Q^T: keys 16 kh + (0..15) x heads 32 hh + (0..31); two
-    // accumulators per head tile (even / odd k-steps) keep four MFMA chains.
-    const uint32_t srec = stage + s_lane;  // fp8: + 8g already
+    // ---- S^T = K Q^T: keys 0..31 (two 16-key tiles) x heads 16 wave + c;
+    // two accumulators per tile (even / odd k-steps).
     v4f sa[2][2];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int u = 0; u < 2; ++u) sa[t][u] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     if (kFp8) {
-      v4u rope[2];
+      v4u rope[2][2];
 #pragma unroll
       for (int ks = 0; ks < kSteps; ++ks) {
-        v8bf a;
-        if (ks < 16) {
-          a = dequant8(raw[ks % kKAhead], ksc[ks >> 2]);
-          if (ks + kKAhead < 16) {
-            raw[ks % kKAhead] = lds_load<v2u>(srec + 32 * (ks + kKAhead));
-          } else if (ks + kKAhead < 18) {
-            rope[ks + kKAhead - 16] = lds_load<v4u>(srec + 8 * g + kVDim + 16 + 64 * (ks + kKAhead - 16));
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const uint32_t srec = s_rec(stage, t);
+          v8bf a;
+          if (ks < 16) {
+            a = dequant8(raw[t][ks % kKAhead], ksc[t][ks >> 2]);
+            if (ks + kKAhead < 16) {
+              raw[t][ks % kKAhead] = lds_load<v2u>(srec + 32 * (ks + kKAhead));
+            } else if (ks + kKAhead < 18) {
+              rope[t][ks + kKAhead - 16] = lds_load<v4u>(srec + 8 * g + kVDim + 16 + 64 * (ks + kKAhead - 16));
+            }
+          } else {
+            a = as_v8bf(rope[t][ks - 16]);
           }
-        } else {
-          a = as_v8bf(rope[ks - 16]);
+          mfma_qb(sa[t][ks & 1], a, qb[ks]);
         }
-        mfma_qb(sa[0][ks & 1], a, qb[0][ks]);
-        mfma_qb(sa[1][ks & 1], a, qb[1][ks]);
         __builtin_amdgcn_sched_barrier(0);
       }
     } else {
 #pragma unroll
       for (int ks = 0; ks < kSteps; ++ks) {
-        const v8bf a = as_v8bf(ka[ks % kKAhead]);
-        if (ks + kKAhead < kSteps) ka[ks % kKAhead] = lds_load<v4u>(k_addr_bf16(srec, ks + kKAhead));
-        mfma_qb(sa[0][ks & 1], a, qb[0][ks]);
-        mfma_qb(sa[1][ks & 1], a, qb[1][ks]);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const v8bf a = as_v8bf(ka[t][ks % kKAhead]);
+          if (ks + kKAhead < kSteps) ka[t][ks % kKAhead] = lds_load<v4u>(k_addr_bf16(s_rec(stage, t), ks + kKAhead));
+          mfma_qb(sa[t][ks & 1], a, qb[ks]);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
 
-    dma.template issue<kL / 3, 2 * kL / 3>(kv, zero, fill);
-
     // Operands of the softmax, issued before the MFMA results are read.
-    const v4i valid = lds_load<v4i>(rows_base + 4 * (uint32_t)(it * kBlock + 16 * kh + 4 * g));
-    v4f vsc[4];  // fp8: tile scales of keys 16 kh + 4g + r
+    v4i valid[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      valid[t] = lds_load<v4i>(rows_base + 4 * (uint32_t)(it * kBlock + 16 * t + 4 * g));
+    v4f vsc[2][4];  // fp8: tile scales of keys 16t + 4g + r
     if (kFp8) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) vsc[r] = lds_load<v4f>(stage + G::record_offset(16 * kh + 4 * g + r) + kVDim);
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) vsc[t][r] = lds_load<v4f>(stage + G::record_offset(16 * t + 4 * g + r) + kVDim);
     }
     mfma_drain(sa[0][0], sa[0][1], sa[1][0], sa[1][1]);
 
-    // ---- block max per head. Lane (c, g) holds keys 16 kh + 4g + r of
-    // heads 32 hh + 16t + c; the max over g uses the row-swap permutes.
+    // ---- online softmax of head 16 wave + c over the whole block (lane
+    // (c, g) holds keys 16t + 4g + r; the max over g uses the row-swap permutes).
     float x[2][4];
+    float mx = neg_inf;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      const v4f s = sa[t][0] + sa[t][1];
-      float mx = neg_inf;
+      const v4f sum = sa[t][0] + sa[t][1];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        x[t][r] = valid[r] >= 0 ? s[r] * scale_log2 : neg_inf;
+        x[t][r] = valid[t][r] >= 0 ? sum[r] * scale_log2 : neg_inf;
         mx = fmaxf(mx, x[t][r]);
       }
-      mx = max_across_rows(mx);
-      if (g == 0) lds_store<float>(max_base + 4 * (kh * kHeadsPerGroup + 32 * hh + 16 * t + c), mx);
     }
-    lds_barrier();
-
-    // ---- running max of all 64 heads, identical in every wave.
-    float alpha[4];
-    bool any = false;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const float mx = fmaxf(lds_load<float>(max_base + 4 * (16 * t + c)),
-                             lds_load<float>(max_base + 4 * (kHeadsPerGroup + 16 * t + c)));
-      const bool need = mx > m_run[t] + kRescaleThreshold || (m_run[t] == neg_inf && mx != neg_inf);
-      const float m_new = need ? fmaxf(m_run[t], mx) : m_run[t];
-      // exp2(-inf) = 0 covers the first valid block.
-      alpha[t] = need ? __builtin_amdgcn_exp2f(m_run[t] - m_new) : 1.0f;
-      m_run[t] = m_new;
-      any |= need;
-    }
-    const bool rescale = __builtin_amdgcn_ballot_w64(any) != 0;
-
-    // ---- probabilities of this wave's keys and heads -> LDS (one copy per
-    // V scale tile for fp8, scaled by that tile's per-key scale).
+    mx = max_across_rows(mx);
+    const bool need = mx > m_run + kRescaleThreshold || (m_run == neg_inf && mx != neg_inf);
+    const float m_new = need ? fmaxf(m_run, mx) : m_run;
+    // exp2(-inf) = 0 covers the first valid block.
+    const float alpha = need ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+    m_run = m_new;
+    l_run *= alpha;
     float p[2][4];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      // Head tile 2 hh + t. The empty asm hides where the two candidates come
-      // from, so the select is not turned into a dynamically indexed (and
-      // therefore private-memory) array access.
-      float m_lo = m_run[t], m_hi = m_run[2 + t], a_lo = alpha[t], a_hi = alpha[2 + t];
-      asm volatile("" : "+v"(m_lo), "+v"(m_hi), "+v"(a_lo), "+v"(a_hi));
-      const float mr = hh ? m_hi : m_lo;
-      l_part[t] *= hh ? a_hi : a_lo;
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        p[t][r] = mr == neg_inf ? 0.0f : __builtin_amdgcn_exp2f(x[t][r] - mr);
-        l_part[t] += p[t][r];
+        p[t][r] = m_run == neg_inf ? 0.0f : __builtin_amdgcn_exp2f(x[t][r] - m_run);
+        l_run += p[t][r];
       }
-    }
-    // P^T of head tile t for PV lane (c, g) sits at [version][t][lane], 16
-    // bytes: keys 4g + r from key half 0, then 16 + 4g + r from half 1.
-    const uint32_t p_own = p_base + (uint32_t)(2 * hh * 64 + lane) * 16 + 8 * kh;
+    if (g == 0) lds.alpha[parity][16 * wave + c] = alpha;
+    // P^T -> LDS, one copy per V scale tile for fp8 (scaled by each key's
+    // scale of that tile; P x 2^k is exact in bf16).
+    const uint32_t p_own = p_base + parity * kPParity + (uint32_t)(wave * 64 + lane) * 16;
     if (kFp8) {
 #pragma unroll
-      for (int v = 0; v < 4; ++v)
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const v2u pk{pack_bf16(p[t][0] * vsc[0][v], p[t][1] * vsc[1][v]),
-                       pack_bf16(p[t][2] * vsc[2][v], p[t][3] * vsc[3][v])};
-          lds_store<v2u>(p_own + (uint32_t)(v * 4 + t) * 1024, pk);
-        }
-    } else {
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const v2u pk{pack_bf16(p[t][0], p[t][1]), pack_bf16(p[t][2], p[t][3])};
-        lds_store<v2u>(p_own + (uint32_t)t * 1024, pk);
+      for (int v = 0; v < 4; ++v) {
+        const v4u pk{pack_bf16(p[0][0] * vsc[0][0][v], p[0][1] * vsc[0][1][v]),
+                     pack_bf16(p[0][2] * vsc[0][2][v], p[0][3] * vsc[0][3][v]),
+                     pack_bf16(p[1][0] * vsc[1][0][v], p[1][1] * vsc[1][1][v]),
+                     pack_bf16(p[1][2] * vsc[1][2][v], p[1][3] * vsc[1][3][v])};
+        lds_store<v4u>(p_own + (uint32_t)v * 4096, pk);
       }
+    } else {
+      const v4u pk{pack_bf16(p[0][0], p[0][1]), pack_bf16(p[0][2], p[0][3]),
+                   pack_bf16(p[1][0], p[1][1]), pack_bf16(p[1][2], p[1][3])};
+      lds_store<v4u>(p_own, pk);
     }
-    dma.template issue<2 * kL / 3, kL>(kv, zero, fill);
-    wait_dma<G::kLoadsPerWave*(G::kRing - 2)>();  // this wave's loads of block it + 1
-    lds_barrier();  // P visible; every wave's loads of block it + 1 landed
-    dma.load_rows(lds.rows, it + G::kRing, n_blocks);  // for the next iteration
-    const uint32_t next_stage = ring_base + (uint32_t)slot * G::kStageBytes;  // slot of it + 1
-    if (it + 1 < n_blocks) prefetch_k(next_stage);
+
+    // Block it + 1's records: this wave's loads first, then the barrier
+    // makes everyone's visible, publishes P and alpha, and (every wave having
+    // finished PV of block it - 1) frees the slot of block it - 1.
+    wait_dma<kL * (G::kRing - 3)>();
+    lds_barrier();
+    const uint32_t fill = ring_base + (uint32_t)free_slot * G::kStageBytes;
+    dma.template issue<0, kL / 3>(kv, zero, fill);
+    slot = slot + 1 == G::kRing ? 0 : slot + 1;
+    free_slot = free_slot + 1 == G::kRing ? 0 : free_slot + 1;
+    if (it + 1 < n_blocks) prefetch_k(ring_base + (uint32_t)slot * G::kStageBytes);
 
     // ---- O^T += V^T P^T for dims 128 wave + (0..127), all 64 heads.
-    if (rescale) {
+    float al[4];
+    bool rescale = false;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      al[t] = lds.alpha[parity][16 * t + c];
+      rescale |= al[t] != 1.0f;
+    }
+    if (__builtin_amdgcn_ballot_w64(rescale)) {
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int m = 0; m < 8; ++m) o[t][m] *= alpha[t];
+        for (int m = 0; m < 8; ++m) o[t][m] *= al[t];
     }
     v8bf pb[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
-      pb[t] = as_v8bf(lds_load<v4u>(p_base + (uint32_t)(((kFp8 ? wave : 0) * 4 + t) * 64 + lane) * 16));
+      pb[t] = as_v8bf(lds_load<v4u>(p_base + parity * kPParity +
+                                    (uint32_t)(((kFp8 ? wave : 0) * 4 + t) * 64 + lane) * 16));
     if (kFp8) {
       const uint32_t vaddr = stage + G::record_offset(vkey) + 128 * wave + 8 * vq;
       constexpr int kAhead = 3;
@@ -554,6 +538,8 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
               v2u, __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i)(uintptr_t)(vaddr + 16 * (m + kAhead))));
 #pragma unroll
         for (int t = 0; t < 4; ++t) o[t][m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[t], o[t][m], 0, 0, 0);
+        if (m == 2) dma.template issue<kL / 3, 2 * kL / 3>(kv, zero, fill);
+        if (m == 5) dma.template issue<2 * kL / 3, kL>(kv, zero, fill);
         __builtin_amdgcn_sched_barrier(0);
       }
     } else {
@@ -585,27 +571,27 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
         }
 #pragma unroll
         for (int t = 0; t < 4; ++t) o[t][m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[t], o[t][m], 0, 0, 0);
+        if (m == 2) dma.template issue<kL / 3, 2 * kL / 3>(kv, zero, fill);
+        if (m == 5) dma.template issue<2 * kL / 3, kL>(kv, zero, fill);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+    dma.load_rows(lds.rows, it + G::kRing, n_blocks);  // rows of the next refill
   }
   // Drain the DMA issued past the last block (padding loads) before exit.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // ---- row sums of all 64 heads, then O / l.
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    float l = l_part[t];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
-    if (g == 0) lds.row_sum[kh][32 * hh + 16 * t + c] = l;
-  }
+  float l = l_run;
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+  if (g == 0) lds.row_sum[16 * wave + c] = l;
   __syncthreads();
   uint16_t* obase = out + ((row * heads + head0 + c) * kVDim) + 128 * wave + 4 * g;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    const float l = lds.row_sum[0][16 * t + c] + lds.row_sum[1][16 * t + c];
-    const float inv_l = l > 0.0f ? 1.0f / l : 0.0f;
+    const float lt = lds.row_sum[16 * t + c];
+    const float inv_l = lt > 0.0f ? 1.0f / lt : 0.0f;
     uint16_t* orow = obase + (int64_t)16 * t * kVDim;
 #pragma unroll
     for (int m = 0; m < 8; ++m)
