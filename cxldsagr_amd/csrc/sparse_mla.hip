@@ -18,28 +18,22 @@
 // * Values: wave w accumulates O^T for dims 128 w .. 128 w + 127 (one fp8
 //   scale tile) and all 64 heads (128 VGPRs). Each V operand feeds four MFMAs.
 // * The probabilities and per-head rescale factors go through LDS, double
-//   buffered by block parity, behind the one barrier of the block. That
-//   barrier also publishes the next block's records and frees the ring slot
-//   of the previous block.
-// Records reach LDS by LDS DMA (global_load_lds_dwordx4: 16 bytes per lane,
-// no registers) into a ring of raw stages kRing - 1 blocks ahead, with the
-// wait counts managed explicitly. A block's loads are issued in three parts
-// spread over the PV product (a full memory queue stalls the issuing wave),
-// and the first score operands of block it + 1 are read right after the
-// barrier. fp8 records are consumed raw:
-// * K operand: lane (c, g) = (lane % 16, lane / 16) reads 8 e4m3 of key c and
-//   converts them with the key's tile scale (v_cvt_scalef32_pk_bf16_fp8;
-//   e4m3 x 2^k is exact in bf16).
-// * V^T operand: ds_read_b64_tr_b8 - within a 16-lane group, lane 8q + b
-//   receives byte b of the 8-byte segments addressed by lanes 2j + q,
-//   j = 0..7. Lanes 2j + q address key j at dims d0 + 8q, so lane i gets dim
-//   d0 + i of 8 keys: the A operand of O^T += V^T P^T after an unscaled
-//   conversion. The per-key scale of the wave's tile is folded into P
-//   (P x 2^k is exact in bf16), so the score waves write one P copy per dim
-//   tile.
-// bf16 records are DMA'd straight into rows whose 16-byte chunks are
-// XOR-swizzled by the key (chunk ^ (key & 15) for the latent, ^ (key & 7)
-// within the RoPE chunks); V^T then comes from ds_read_b64_tr_b16.
+//   buffered by block parity, behind the one barrier of the block.
+//
+// Records travel HBM -> registers -> LDS as bf16 rows. Lane (kk, j) of wave
+// w (kk = 8w + lane / 8, j = lane % 8) loads 1/8 of key kk's record of each
+// block with 16-byte loads two blocks ahead, and in the iteration before the
+// block is scored writes it into one of three row buffers (fp8 records
+// converted with their tile scales by v_cvt_scalef32_pk_bf16_fp8; e4m3 x 2^k
+// is exact in bf16). Conversion therefore happens once per key, not once
+// per wave that reads it, and the score and value phases read plain bf16:
+// * K operand: lane (c, g) = (lane % 16, lane / 16) reads 16 bytes of key
+//   16t + c per k-step.
+// * V^T operand: ds_read_b64_tr_b16 - lane 4 jj + qq of a 16-lane row group
+//   addresses key 4g + jj at dims d0 + 4qq and receives dim d0 + lane % 16
+//   of keys 4g .. 4g + 3 (a second read covers keys 16 + 4g ..).
+// A buffer written in iteration b - 1 is read by the scores of block b and,
+// after that block's barrier, by its PV product, hence three buffers.
 //
 // Key order inside a block: MFMA k-index 8g + j of the PV product is key
 // 16 (j / 4) + 4g + j % 4, which is where the S^T C layout of the two key
@@ -75,33 +69,28 @@ constexpr int kPageTokens = 64;
 constexpr float kRescaleThreshold = 8.0f;
 
 template <bool kFp8>
-struct Geometry {
+struct Format {
   static constexpr int kRecordBytes = kFp8 ? 656 : kQkDim * 2;
-  static constexpr int kChunks = kRecordBytes / 16;  // 41 or 72 per record
-  // fp8: record r at chunk 41 r, plus 8 chunks (128 bytes) for the second
-  // key half. 8-byte LDS reads are served 32 lanes at a time from 64 4-byte
-  // banks; with the 656-byte stride alone, keys r and r + 16 share banks, and
-  // the V^T reads of one cycle (keys 0-7 and 16-23, or 8-15 and 24-31) would
-  // conflict. The shift moves the second half onto the complementary banks.
-  // bf16: record r at chunk 72 r.
-  static constexpr int kHalfPad = kFp8 ? 8 : 0;
-  static constexpr int kStageChunks = kBlock * kChunks + kHalfPad;
-  static constexpr int kLoadsPerWave = (kStageChunks + kThreads - 1) / kThreads;  // 6 or 9
-  static constexpr int kStageBytes = kLoadsPerWave * kThreads * 16;
-  static constexpr int kRing = kFp8 ? 4 : 3;
-  static constexpr int kPVersions = kFp8 ? 4 : 1;  // P copies (one per V scale tile)
-  __device__ static constexpr uint32_t record_offset(int r) {
-    return 16u * (uint32_t)(kChunks * r + (r >= 16 ? kHalfPad : 0));
-  }
+  // 16-byte loads per lane per block: lane (key kk, part j) of the loader
+  // fetches 1/8 of its key's record (fp8: 4 latent + scales + RoPE; bf16:
+  // 8 latent + RoPE).
+  static constexpr int kLoads = kFp8 ? 6 : 9;
 };
 
-template <bool kFp8>
+// bf16 K/V rows of one block in LDS: key r at kRowBytes r, its 576 dims in
+// order. The 32-byte pad puts consecutive rows 40 banks apart (mod 64), which
+// keeps both the K reads (16 rows x 64 contiguous bytes per half-wave) and
+// the V^T transpose reads (8 rows x 32 bytes) free of bank conflicts.
+constexpr int kRowBytes = kQkDim * 2 + 32;
+constexpr int kBufBytes = kBlock * kRowBytes;
+constexpr int kBuffers = 3;  // written in iteration b - 1, read by S in b and by PV after its barrier
+
 struct __align__(16) Lds {
-  uint8_t ring[Geometry<kFp8>::kRing][Geometry<kFp8>::kStageBytes];  // raw records
-  // P^T in PV B-operand order, by block parity: [parity][version][head tile]
-  // [lane] 16 bytes, lane (c, g) of tile t holding head 16t + c, keys 4g + r
+  uint8_t kv[kBuffers][kBufBytes];
+  // P^T in PV B-operand order, by block parity: [parity][head tile][lane]
+  // 16 bytes, lane (c, g) of tile t holding head 16t + c, keys 4g + r
   // (r = 0..3) then 16 + 4g + r, bf16.
-  uint8_t p[2][Geometry<kFp8>::kPVersions][4][64][16];
+  uint8_t p[2][4][64][16];
   float alpha[2][kHeadsPerGroup];  // per-head rescale factor of the block, by parity
   float row_sum[kHeadsPerGroup];
   int32_t rows[kMaxSelected];  // physical record row per selected position, -1 = padding
@@ -152,17 +141,6 @@ __device__ __forceinline__ void mfma_drain(v4f& a, v4f& b, v4f& c, v4f& d) {
   asm volatile("s_nop 7\n\ts_nop 7" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
 }
 
-// 8 e4m3 (two dwords) x scale -> 8 bf16.
-__device__ __forceinline__ v8bf dequant8(v2u w, float scale) {
-  return as_v8bf(v4u{dequant_pair<false>(w.x, scale), dequant_pair<true>(w.x, scale),
-                     dequant_pair<false>(w.y, scale), dequant_pair<true>(w.y, scale)});
-}
-
-// Position of logical 16-byte chunk j (of 72) in bf16 record `key`.
-__device__ __forceinline__ int chunk_slot(int j, int key) {
-  return j < 64 ? (j ^ (key & 15)) : 64 + ((j - 64) ^ (key & 7));
-}
-
 typedef v2i __attribute__((address_space(3))) * lds_v2i;
 typedef v4s __attribute__((address_space(3))) * lds_v4s;
 
@@ -175,102 +153,16 @@ __device__ __forceinline__ void lds_store(uint32_t addr, T v) {
   *(T __attribute__((address_space(3)))*)(uintptr_t)addr = v;
 }
 
-// LDS barrier that does not wait for the in-flight DMA stages: finish this
-// wave's LDS traffic, then s_barrier. The memory clobber keeps the compiler
-// from moving LDS accesses across it.
+// LDS barrier: finish this wave's LDS traffic, then s_barrier. The memory
+// clobber keeps the compiler from moving memory accesses across it.
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-template <int kOutstanding>
-__device__ __forceinline__ void wait_dma() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kOutstanding) : "memory");
-}
-
-// One wave's LDS DMA for 64 consecutive 16-byte chunks of a raw stage: lane l
-// copies its chunk to lds_base + 16 l.
-__device__ __forceinline__ void dma16(const void* src, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-               ::"s"(lds_base), "v"(src) : "memory", "m0");
-}
-
-// Stage chunk -> (record slot r, logical chunk j) of the DMA source, or r = -1
-// for padding.
+// One block's share of a lane's record bytes, in flight or landed.
 template <bool kFp8>
-__device__ __forceinline__ void stage_chunk(int sc, int& r, int& j) {
-  using G = Geometry<kFp8>;
-  if (kFp8) {
-    constexpr int kHalf = 16 * G::kChunks;
-    int base = sc;
-    int r0 = 0;
-    if (sc >= kHalf) {
-      base = sc - kHalf - G::kHalfPad;
-      r0 = 16;
-    }
-    if (base < 0 || base >= kHalf) {
-      r = -1;
-      j = 0;
-      return;
-    }
-    const int rr = base / G::kChunks;
-    r = r0 + rr;
-    j = base - rr * G::kChunks;
-  } else {
-    if (sc >= G::kStageChunks) {
-      r = -1;
-      j = 0;
-      return;
-    }
-    r = sc / G::kChunks;
-    const int p = sc - r * G::kChunks;  // physical slot; the swizzle is an involution
-    j = chunk_slot(p, r);
-  }
-}
-
-// DMA plan of one lane: for each of its kLoadsPerWave loads per stage, the
-// record slot r (0xFFFF for padding) and the chunk's byte offset 16 j.
-template <bool kFp8>
-struct DmaPlan {
-  uint32_t rj[Geometry<kFp8>::kLoadsPerWave];  // (r << 16) | 16 j
-  int32_t row[Geometry<kFp8>::kLoadsPerWave];  // physical rows of the next block to issue
-
-  __device__ __forceinline__ void init() {
-    using G = Geometry<kFp8>;
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int k = 0; k < G::kLoadsPerWave; ++k) {
-      int r, j;
-      stage_chunk<kFp8>((k * kWaves + wave) * 64 + lane, r, j);
-      rj[k] = r < 0 ? 0xFFFF0000u : ((uint32_t)r << 16) | (uint32_t)(16 * j);
-    }
-  }
-  // Reads the physical rows of block `blk` (-1 where nothing is fetched).
-  __device__ __forceinline__ void load_rows(const int32_t* rows, int blk, int n_blocks) {
-    using G = Geometry<kFp8>;
-#pragma unroll
-    for (int k = 0; k < G::kLoadsPerWave; ++k) {
-      const uint32_t r = rj[k] >> 16;
-      const bool use = blk < n_blocks && r != 0xFFFF;
-      const int32_t v = rows[use ? blk * kBlock + (int)r : 0];
-      row[k] = use ? v : -1;
-    }
-  }
-  // Issues loads [k0, k1) of the block whose rows were loaded, into the stage
-  // at slot_base. Loads without a record read the zero record.
-  template <int k0, int k1>
-  __device__ __forceinline__ void issue(const uint8_t* __restrict__ kv, const uint8_t* zero,
-                                        uint32_t slot_base) const {
-    using G = Geometry<kFp8>;
-    const int wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int k = k0; k < k1; ++k) {
-      const bool use = row[k] >= 0;
-      const uint8_t* src = (use ? kv : zero) +
-                           (use ? (int64_t)row[k] * G::kRecordBytes + (rj[k] & 0xFFFF) : 0);
-      dma16(src, __builtin_amdgcn_readfirstlane(slot_base + (k * kWaves + wave) * 64 * 16));
-    }
-  }
+struct Staged {
+  v4u r[Format<kFp8>::kLoads];
 };
 
 template <bool kFp8>
@@ -279,8 +171,8 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
     const int32_t* __restrict__ page_table, int64_t n_tokens, int64_t pages,
     const int32_t* __restrict__ indices, int64_t heads, int64_t topk, float scale_log2,
     uint16_t* __restrict__ out) {
-  using G = Geometry<kFp8>;
-  __shared__ Lds<kFp8> lds;
+  using F = Format<kFp8>;
+  __shared__ Lds lds;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int g = lane >> 4;
@@ -289,10 +181,10 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
   const int64_t head0 = (int64_t)blockIdx.y * kHeadsPerGroup;
   const int32_t* ids = indices + row * topk;
   const float neg_inf = -__builtin_inff();
-  const int64_t iters = (topk + kBlock - 1) / kBlock;
+  const int n_blocks = (int)((topk + kBlock - 1) / kBlock);
 
   // Physical rows of every selected position.
-  for (int64_t i = threadIdx.x; i < iters * kBlock; i += kThreads) {
+  for (int i = threadIdx.x; i < n_blocks * kBlock; i += kThreads) {
     int32_t phys = -1;
     if (i < topk) {
       const int64_t id = ids[i];
@@ -324,70 +216,90 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
   float m_run = neg_inf;  // running max of head 16 wave + c
   float l_run = 0.0f;     // its row sum over this lane's keys
 
-  // All compiler-visible global loads must be complete before the DMA wait
-  // accounting starts; the builtin (vmcnt(0), expcnt/lgkmcnt untouched) also
-  // tells the compiler so, which keeps it from re-waiting inside the loop.
-  __builtin_amdgcn_s_waitcnt(0x0F70);
-  lds_barrier();
-  const uint8_t* zero = zero_record;
-  const uint32_t ring_base = (uint32_t)(uintptr_t)&lds.ring[0][0];
-  const int n_blocks = (int)iters;
-  constexpr int kL = G::kLoadsPerWave;
-  DmaPlan<kFp8> dma;
-  dma.init();
-#pragma unroll
-  for (int s = 0; s < G::kRing - 1; ++s) {
-    dma.load_rows(lds.rows, s, n_blocks);
-    dma.template issue<0, kL>(kv, zero, ring_base + s * G::kStageBytes);
-  }
-  dma.load_rows(lds.rows, G::kRing - 1, n_blocks);
-
-  const uint32_t p_base = (uint32_t)(uintptr_t)&lds.p[0][0][0][0][0];
+  // Loader role: key kk of each block, part j of its record.
+  const int kk = 8 * wave + (lane >> 3);
+  const int j = lane & 7;
   const uint32_t rows_base = (uint32_t)(uintptr_t)&lds.rows[0];
-  constexpr uint32_t kPParity = G::kPVersions * 4 * 64 * 16;
-  // V^T (tr8) rows: lane 2j + q of each 16-lane group reads key
-  // 16 (j / 4) + 4g + j % 4 at dims +8q.
-  const int vj = c >> 1;
-  const int vq = c & 1;
-  const int vkey = 16 * (vj >> 2) + 4 * g + (vj & 3);
+  const uint32_t kv_base = (uint32_t)(uintptr_t)&lds.kv[0][0];
+  const uint32_t p_base = (uint32_t)(uintptr_t)&lds.p[0][0][0][0];
 
-  // bf16 K operand of k-step ks: logical chunk 4 ks + g of key 16t + c sits
-  // at slot 16 (ks >> 2) + 4 ((ks & 3) ^ (c >> 2)) + (g ^ (c & 3)).
-  auto k_addr_bf16 = [&](uint32_t srec, int ks) -> uint32_t {
-    return ks < 16 ? srec + 256 * (ks >> 2) + 64 * ((ks & 3) ^ (c >> 2)) + 16 * (g ^ (c & 3))
-                   : srec + 16 * (64 + ((4 * (ks - 16) + g) ^ (c & 7)));
-  };
-  // Score operands of key tiles t = 0, 1 (keys 16t + c), loaded ahead (fp8:
-  // the key's tile scales and the first raw K chunks; bf16: the first chunks).
-  constexpr int kKAhead = kFp8 ? 4 : 2;
-  v4f ksc[2];
-  v2u raw[2][kKAhead];
-  v4u ka[2][kKAhead];
-  auto s_rec = [&](uint32_t stage_k, int t) -> uint32_t {
-    return stage_k + G::record_offset(16 * t + c) + (kFp8 ? 8 * g : 0);
-  };
-  auto prefetch_k = [&](uint32_t stage_k) {
+  // Block b's record bytes of this lane -> registers. Blocks past the end
+  // (and invalid ids) read the zero record, so the load count per block is
+  // fixed.
+  auto fetch = [&](Staged<kFp8>& st, int b) {
+    const int32_t phys = b < n_blocks ? lds_load<int32_t>(rows_base + 4 * (uint32_t)(b * kBlock + kk)) : -1;
+    const uint8_t* rec = phys >= 0 ? kv + (int64_t)phys * F::kRecordBytes : zero_record;
+    if (kFp8) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const uint32_t srec = s_rec(stage_k, t);
-      if (kFp8) {
-        ksc[t] = lds_load<v4f>(srec - 8 * g + kVDim);
+      for (int i = 0; i < 4; ++i) st.r[i] = *reinterpret_cast<const v4u*>(rec + 128 * i + 16 * j);
+      st.r[4] = *reinterpret_cast<const v4u*>(rec + kVDim);
+      st.r[5] = *reinterpret_cast<const v4u*>(rec + kVDim + 16 + 16 * j);
+    } else {
 #pragma unroll
-        for (int d = 0; d < kKAhead; ++d) raw[t][d] = lds_load<v2u>(srec + 32 * d);
-      } else {
-#pragma unroll
-        for (int d = 0; d < kKAhead; ++d) ka[t][d] = lds_load<v4u>(k_addr_bf16(srec, d));
-      }
+      for (int i = 0; i < 8; ++i) st.r[i] = *reinterpret_cast<const v4u*>(rec + 128 * i + 16 * j);
+      st.r[8] = *reinterpret_cast<const v4u*>(rec + 2 * kVDim + 16 * j);
     }
   };
-  wait_dma<kL * (G::kRing - 2)>();  // this wave's loads of block 0
-  lds_barrier();
-  prefetch_k(ring_base);
+  // Landed record bytes -> bf16 rows of a block buffer (fp8: e4m3 x tile
+  // scale, exact in bf16).
+  auto unpack = [&](const Staged<kFp8>& st, uint32_t buf) {
+    const uint32_t rec = buf + (uint32_t)kk * kRowBytes;
+    if (kFp8) {
+      const v4f sc = __builtin_bit_cast(v4f, st.r[4]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const v4u w = st.r[i];
+        const v4u lo{dequant_pair<false>(w.x, sc[i]), dequant_pair<true>(w.x, sc[i]),
+                     dequant_pair<false>(w.y, sc[i]), dequant_pair<true>(w.y, sc[i])};
+        const v4u hi{dequant_pair<false>(w.z, sc[i]), dequant_pair<true>(w.z, sc[i]),
+                     dequant_pair<false>(w.w, sc[i]), dequant_pair<true>(w.w, sc[i])};
+        lds_store<v4u>(rec + 256 * i + 32 * j, lo);
+        lds_store<v4u>(rec + 256 * i + 32 * j + 16, hi);
+      }
+      lds_store<v4u>(rec + 2 * kVDim + 16 * j, st.r[5]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) lds_store<v4u>(rec + 128 * i + 16 * j, st.r[i]);
+      lds_store<v4u>(rec + 2 * kVDim + 16 * j, st.r[8]);
+    }
+  };
 
-  int slot = 0;                  // ring slot of block it
-  int free_slot = G::kRing - 1;  // slot of block it - 1, refilled with block it + kRing - 1
-  for (int it = 0; it < n_blocks; ++it) {
-    const uint32_t stage = ring_base + (uint32_t)slot * G::kStageBytes;
+  // K operand of k-step ks for key 16t + c: dims 32 ks + 8g .. +8.
+  const uint32_t k_lane = (uint32_t)c * kRowBytes + 16 * g;
+  // Per-block base addresses are formed once and hidden from the optimizer:
+  // otherwise it hoists (lane offset + constant) out of the loop and pays an
+  // add per LDS access instead of using the instruction's offset field.
+  auto lane_base = [](uint32_t buf, uint32_t lane_off) -> uint32_t {
+    uint32_t a = buf + lane_off;
+    asm volatile("" : "+v"(a));
+    return a;
+  };
+  // V^T rows (ds_read_b64_tr_b16): lane 4 jj + qq of row group g addresses
+  // key vrow = 4g + jj (and 16 + vrow) at dims 128 wave + 16m + 4qq.
+  const int jj = c >> 2;
+  const int qq = c & 3;
+  const int vrow = 4 * g + jj;
+  const uint32_t v_lane = (uint32_t)vrow * kRowBytes + 256 * wave + 8 * qq;
+  constexpr uint32_t kHalf = 16 * kRowBytes;
+
+  // Prologue: blocks 0 and 1 in flight, block 0 unpacked, block 2 in flight.
+  Staged<kFp8> st0, st1;
+  __syncthreads();  // rows table
+  fetch(st0, 0);
+  fetch(st1, 1);
+  unpack(st0, kv_base);
+  fetch(st0, 2);
+  lds_barrier();
+
+  int buf_cur = 0;  // buffer of block it
+  // One block: scores, softmax and P of block it; unpack of block it + 1
+  // (landed two iterations ago in `st`) and refetch of block it + 3 into it;
+  // the barrier; then PV of block it.
+  auto step = [&](int it, Staged<kFp8>& st) {
+    const uint32_t buf = kv_base + (uint32_t)buf_cur * kBufBytes;
+    const uint32_t kbase = lane_base(buf, k_lane);
+    const int buf_next_i = buf_cur + 1 == kBuffers ? 0 : buf_cur + 1;
+    const uint32_t buf_next = kv_base + (uint32_t)buf_next_i * kBufBytes;
     const uint32_t parity = (uint32_t)(it & 1);
 
     // ---- S^T = K Q^T: keys 0..31 (two 16-key tiles) x heads 16 wave + c;
@@ -397,38 +309,22 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int u = 0; u < 2; ++u) sa[t][u] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    if (kFp8) {
-      v4u rope[2][2];
+    {
+      constexpr int kAhead = 3;
+      v4u ka[2][kAhead];
+      auto k_addr = [&](int t, int ks) -> uint32_t { return kbase + (uint32_t)(16 * t * kRowBytes + 64 * ks); };
+#pragma unroll
+      for (int d = 0; d < kAhead; ++d)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) ka[t][d] = lds_load<v4u>(k_addr(t, d));
 #pragma unroll
       for (int ks = 0; ks < kSteps; ++ks) {
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-          const uint32_t srec = s_rec(stage, t);
-          v8bf a;
-          if (ks < 16) {
-            a = dequant8(raw[t][ks % kKAhead], ksc[t][ks >> 2]);
-            if (ks + kKAhead < 16) {
-              raw[t][ks % kKAhead] = lds_load<v2u>(srec + 32 * (ks + kKAhead));
-            } else if (ks + kKAhead < 18) {
-              rope[t][ks + kKAhead - 16] = lds_load<v4u>(srec + 8 * g + kVDim + 16 + 64 * (ks + kKAhead - 16));
-            }
-          } else {
-            a = as_v8bf(rope[t][ks - 16]);
-          }
+          const v8bf a = as_v8bf(ka[t][ks % kAhead]);
+          if (ks + kAhead < kSteps) ka[t][ks % kAhead] = lds_load<v4u>(k_addr(t, ks + kAhead));
           mfma_qb(sa[t][ks & 1], a, qb[ks]);
         }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    } else {
-#pragma unroll
-      for (int ks = 0; ks < kSteps; ++ks) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const v8bf a = as_v8bf(ka[t][ks % kKAhead]);
-          if (ks + kKAhead < kSteps) ka[t][ks % kKAhead] = lds_load<v4u>(k_addr_bf16(s_rec(stage, t), ks + kKAhead));
-          mfma_qb(sa[t][ks & 1], a, qb[ks]);
-        }
-        __builtin_amdgcn_sched_barrier(0);
       }
     }
 
@@ -437,17 +333,10 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
 #pragma unroll
     for (int t = 0; t < 2; ++t)
       valid[t] = lds_load<v4i>(rows_base + 4 * (uint32_t)(it * kBlock + 16 * t + 4 * g));
-    v4f vsc[2][4];  // fp8: tile scales of keys 16t + 4g + r
-    if (kFp8) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) vsc[t][r] = lds_load<v4f>(stage + G::record_offset(16 * t + 4 * g + r) + kVDim);
-    }
     mfma_drain(sa[0][0], sa[0][1], sa[1][0], sa[1][1]);
 
-    // ---- online softmax of head 16 wave + c over the whole block (lane
-    // (c, g) holds keys 16t + 4g + r; the max over g uses the row-swap permutes).
+    // ---- online softmax of head 16 wave + c over the block (lane (c, g)
+    // holds keys 16t + 4g + r; the max over g uses the row-swap permutes).
     float x[2][4];
     float mx = neg_inf;
 #pragma unroll
@@ -475,34 +364,16 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
         l_run += p[t][r];
       }
     if (g == 0) lds.alpha[parity][16 * wave + c] = alpha;
-    // P^T -> LDS, one copy per V scale tile for fp8 (scaled by each key's
-    // scale of that tile; P x 2^k is exact in bf16).
-    const uint32_t p_own = p_base + parity * kPParity + (uint32_t)(wave * 64 + lane) * 16;
-    if (kFp8) {
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const v4u pk{pack_bf16(p[0][0] * vsc[0][0][v], p[0][1] * vsc[0][1][v]),
-                     pack_bf16(p[0][2] * vsc[0][2][v], p[0][3] * vsc[0][3][v]),
-                     pack_bf16(p[1][0] * vsc[1][0][v], p[1][1] * vsc[1][1][v]),
-                     pack_bf16(p[1][2] * vsc[1][2][v], p[1][3] * vsc[1][3][v])};
-        lds_store<v4u>(p_own + (uint32_t)v * 4096, pk);
-      }
-    } else {
-      const v4u pk{pack_bf16(p[0][0], p[0][1]), pack_bf16(p[0][2], p[0][3]),
-                   pack_bf16(p[1][0], p[1][1]), pack_bf16(p[1][2], p[1][3])};
-      lds_store<v4u>(p_own, pk);
-    }
+    lds_store<v4u>(p_base + parity * 4096 + (uint32_t)(wave * 64 + lane) * 16,
+                   v4u{pack_bf16(p[0][0], p[0][1]), pack_bf16(p[0][2], p[0][3]),
+                       pack_bf16(p[1][0], p[1][1]), pack_bf16(p[1][2], p[1][3])});
 
-    // Block it + 1's records: this wave's loads first, then the barrier
-    // makes everyone's visible, publishes P and alpha, and (every wave having
-    // finished PV of block it - 1) frees the slot of block it - 1.
-    wait_dma<kL * (G::kRing - 3)>();
-    lds_barrier();
-    const uint32_t fill = ring_base + (uint32_t)free_slot * G::kStageBytes;
-    dma.template issue<0, kL / 3>(kv, zero, fill);
-    slot = slot + 1 == G::kRing ? 0 : slot + 1;
-    free_slot = free_slot + 1 == G::kRing ? 0 : free_slot + 1;
-    if (it + 1 < n_blocks) prefetch_k(ring_base + (uint32_t)slot * G::kStageBytes);
+    // ---- block it + 1 -> bf16 rows; block it + 3 -> the freed registers.
+    // The buffer of block it + 1 last held block it - 2, whose readers all
+    // passed the previous barrier.
+    unpack(st, buf_next);
+    fetch(st, it + 3);
+    lds_barrier();  // P, alpha and block it + 1's rows visible
 
     // ---- O^T += V^T P^T for dims 128 wave + (0..127), all 64 heads.
     float al[4];
@@ -521,64 +392,37 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
     v8bf pb[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
-      pb[t] = as_v8bf(lds_load<v4u>(p_base + parity * kPParity +
-                                    (uint32_t)(((kFp8 ? wave : 0) * 4 + t) * 64 + lane) * 16));
-    if (kFp8) {
-      const uint32_t vaddr = stage + G::record_offset(vkey) + 128 * wave + 8 * vq;
-      constexpr int kAhead = 3;
-      v2u vr[kAhead];
+      pb[t] = as_v8bf(lds_load<v4u>(p_base + parity * 4096 + (uint32_t)(t * 64 + lane) * 16));
+    const uint32_t vbase = lane_base(buf, v_lane);
+    auto v_addr = [&](int m) -> uint32_t { return vbase + 32 * m; };
+    constexpr int kAhead = 3;
+    v4s vlo[kAhead], vhi[kAhead];
 #pragma unroll
-      for (int d = 0; d < kAhead; ++d)
-        vr[d] = __builtin_bit_cast(v2u, __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i)(uintptr_t)(vaddr + 16 * d)));
-#pragma unroll
-      for (int m = 0; m < 8; ++m) {
-        const v8bf a = dequant8(vr[m % kAhead], 1.0f);
-        if (m + kAhead < 8)
-          vr[m % kAhead] = __builtin_bit_cast(
-              v2u, __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i)(uintptr_t)(vaddr + 16 * (m + kAhead))));
-#pragma unroll
-        for (int t = 0; t < 4; ++t) o[t][m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[t], o[t][m], 0, 0, 0);
-        if (m == 2) dma.template issue<kL / 3, 2 * kL / 3>(kv, zero, fill);
-        if (m == 5) dma.template issue<2 * kL / 3, kL>(kv, zero, fill);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    } else {
-      // Dims 16 mg + 4 qq of rows vrow and 16 + vrow (vrow = 4g + jj): logical
-      // chunk 2 mg + (qq >> 1), slot 16 (mg >> 3) + 2 ((mg & 7) ^ (vrow >> 1)) +
-      // ((qq >> 1) ^ (vrow & 1)), with mg = 8 wave + m.
-      const int jj = c >> 2;
-      const int qq = c & 3;
-      const int vrow = 4 * g + jj;
-      const uint32_t vbase = stage + G::record_offset(vrow) + 256 * wave +
-                             16 * ((qq >> 1) ^ (vrow & 1)) + 8 * (qq & 1);
-      constexpr uint32_t kHalf = 16 * G::kRecordBytes;
-      auto v_addr = [&](int m) -> uint32_t { return vbase + 32 * (m ^ (vrow >> 1)); };
-      constexpr int kAhead = 3;
-      v4s vlo[kAhead], vhi[kAhead];
-#pragma unroll
-      for (int d = 0; d < kAhead; ++d) {
-        vlo[d] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)v_addr(d));
-        vhi[d] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)(v_addr(d) + kHalf));
-      }
-#pragma unroll
-      for (int m = 0; m < 8; ++m) {
-        const v8bf a = __builtin_bit_cast(
-            v8bf, __builtin_shufflevector(vlo[m % kAhead], vhi[m % kAhead], 0, 1, 2, 3, 4, 5, 6, 7));
-        if (m + kAhead < 8) {
-          vlo[m % kAhead] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)v_addr(m + kAhead));
-          vhi[m % kAhead] =
-              __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)(v_addr(m + kAhead) + kHalf));
-        }
-#pragma unroll
-        for (int t = 0; t < 4; ++t) o[t][m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[t], o[t][m], 0, 0, 0);
-        if (m == 2) dma.template issue<kL / 3, 2 * kL / 3>(kv, zero, fill);
-        if (m == 5) dma.template issue<2 * kL / 3, kL>(kv, zero, fill);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+    for (int d = 0; d < kAhead; ++d) {
+      vlo[d] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)v_addr(d));
+      vhi[d] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)(v_addr(d) + kHalf));
     }
-    dma.load_rows(lds.rows, it + G::kRing, n_blocks);  // rows of the next refill
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const v8bf a = __builtin_bit_cast(
+          v8bf, __builtin_shufflevector(vlo[m % kAhead], vhi[m % kAhead], 0, 1, 2, 3, 4, 5, 6, 7));
+      if (m + kAhead < 8) {
+        vlo[m % kAhead] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)v_addr(m + kAhead));
+        vhi[m % kAhead] =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)(v_addr(m + kAhead) + kHalf));
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) o[t][m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[t], o[t][m], 0, 0, 0);
+    }
+    buf_cur = buf_next_i;
+  };
+  // Two blocks per trip so that each register set stays a fixed register set.
+  for (int it = 0; it < n_blocks; it += 2) {
+    step(it, st1);
+    if (it + 1 < n_blocks) step(it + 1, st0);
   }
-  // Drain the DMA issued past the last block (padding loads) before exit.
+  // The fetches past the last block are never read; let them land before
+  // the registers are released.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // ---- row sums of all 64 heads, then O / l.
