@@ -11,14 +11,20 @@
 // Mapping (gfx950, wave64, v_mfma_f32_16x16x32_bf16). A work-group owns one
 // query row and 64 heads and walks the selection in blocks of 32 keys; its 4
 // waves (one per SIMD) split each block twice:
-// * Scores: wave w computes S^T = K Q^T for all 32 keys (two 16-key tiles)
-//   and its 16 heads 16 w .. 16 w + 15, keeping Q^T of those heads in AGPRs
-//   (72). The block max of a head is then a reduction inside the wave, and
-//   the wave owns the running max, rescale factor and row sum of its heads.
+// * Scores: wave w computes S^T = K Q^T for key half kh = w / 2 (16 keys)
+//   and head half hh = w % 2 (32 heads), keeping Q^T of its 32 heads in
+//   AGPRs (144); each K operand read from LDS feeds two MFMAs.
+// * Softmax without a max exchange in the common case: each wave computes
+//   P against the running max of its heads (known to every wave) and flags
+//   the block if any of its maxima rose by more than kRescaleThreshold. If
+//   no wave flagged it, P is final. Otherwise (the first block, and rarely
+//   later) every wave reads the other key half's block maxima after the
+//   barrier, recomputes its P against the new maxima, publishes the rescale
+//   factors, and a second barrier precedes the PV product.
 // * Values: wave w accumulates O^T for dims 128 w .. 128 w + 127 (one fp8
 //   scale tile) and all 64 heads (128 VGPRs). Each V operand feeds four MFMAs.
-// * The probabilities and per-head rescale factors go through LDS, double
-//   buffered by block parity, behind the one barrier of the block.
+// * The probabilities, block maxima and flags go through LDS, double
+//   buffered by block parity, behind the barrier of the block.
 //
 // Records travel HBM -> registers -> LDS as bf16 rows. Lane (kk, j) of wave
 // w (kk = 8w + lane / 8, j = lane % 8) loads 1/8 of key kk's record of each
@@ -28,7 +34,7 @@
 // is exact in bf16). Conversion therefore happens once per key, not once
 // per wave that reads it, and the score and value phases read plain bf16:
 // * K operand: lane (c, g) = (lane % 16, lane / 16) reads 16 bytes of key
-//   16t + c per k-step.
+//   16 kh + c per k-step.
 // * V^T operand: ds_read_b64_tr_b16 - lane 4 jj + qq of a 16-lane row group
 //   addresses key 4g + jj at dims d0 + 4qq and receives dim d0 + lane % 16
 //   of keys 4g .. 4g + 3 (a second read covers keys 16 + 4g ..).
@@ -37,7 +43,7 @@
 //
 // Key order inside a block: MFMA k-index 8g + j of the PV product is key
 // 16 (j / 4) + 4g + j % 4, which is where the S^T C layout of the two key
-// tiles puts them (lane (c, g) holds keys 4g + r of each tile, head c).
+// halves puts them (lane (c, g) holds keys 4g + r of its half, head c).
 //
 // Online softmax in log2 units with lazy rescaling (only when a block raises
 // the running max by more than 8, so p <= 2^8).
@@ -92,7 +98,9 @@ struct __align__(16) Lds {
   // (r = 0..3) then 16 + 4g + r, bf16.
   uint8_t p[2][4][64][16];
   float alpha[2][kHeadsPerGroup];  // per-head rescale factor of the block, by parity
-  float row_sum[kHeadsPerGroup];
+  float part_max[2][2][kHeadsPerGroup];  // [parity][key half] block max of each head
+  alignas(16) int32_t raise[2][4];  // [parity][wave]: the block raised a running max
+  float row_sum[2][kHeadsPerGroup];  // [key half]
   int32_t rows[kMaxSelected];  // physical record row per selected position, -1 = padding
 };
 
@@ -181,7 +189,9 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
   const int64_t head0 = (int64_t)blockIdx.y * kHeadsPerGroup;
   const int32_t* ids = indices + row * topk;
   const float neg_inf = -__builtin_inff();
-  const int n_blocks = (int)((topk + kBlock - 1) / kBlock);
+  // Blocks of 32 selected positions, rounded up to an even count (the loop
+  // takes two per trip; a padding block has no valid key and adds nothing).
+  const int n_blocks = (int)((topk + 2 * kBlock - 1) / (2 * kBlock)) * 2;
 
   // Physical rows of every selected position.
   for (int i = threadIdx.x; i < n_blocks * kBlock; i += kThreads) {
@@ -200,12 +210,17 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
     lds.rows[i] = phys;
   }
 
-  // Q^T operands of the score phase: head 16 wave + c, dims 32ks + 8g .. +8.
-  v8bf qb[kSteps];
-  {
-    const uint16_t* qrow = q + ((row * heads + head0 + 16 * wave + c) * kQkDim) + 8 * g;
+  // Score role: key half kh (keys 16 kh + c), head tiles 2 hh + u (heads
+  // 16 (2 hh + u) + c), u = 0, 1.
+  const int kh = wave >> 1;
+  const int hh = wave & 1;
+  // Q^T operands: head 16 (2 hh + u) + c, dims 32 ks + 8g .. +8.
+  v8bf qb[2][kSteps];
 #pragma unroll
-    for (int ks = 0; ks < kSteps; ++ks) qb[ks] = as_v8bf(*reinterpret_cast<const v4u*>(qrow + 32 * ks));
+  for (int u = 0; u < 2; ++u) {
+    const uint16_t* qrow = q + ((row * heads + head0 + 16 * (2 * hh + u) + c) * kQkDim) + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < kSteps; ++ks) qb[u][ks] = as_v8bf(*reinterpret_cast<const v4u*>(qrow + 32 * ks));
   }
   // O^T: head tile t (heads 16t + c), dims 128 wave + 16m + 4g + r.
   v4f o[4][8];
@@ -213,8 +228,10 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
   for (int t = 0; t < 4; ++t)
 #pragma unroll
     for (int m = 0; m < 8; ++m) o[t][m] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-  float m_run = neg_inf;  // running max of head 16 wave + c
-  float l_run = 0.0f;     // its row sum over this lane's keys
+  // Running max of heads 16 (2 hh + u) + c (the same in both key-half
+  // waves), and the row sum over this lane's keys.
+  float m_run[2] = {neg_inf, neg_inf};
+  float l_run[2] = {0.0f, 0.0f};
 
   // Loader role: key kk of each block, part j of its record.
   const int kk = 8 * wave + (lane >> 3);
@@ -264,8 +281,8 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
     }
   };
 
-  // K operand of k-step ks for key 16t + c: dims 32 ks + 8g .. +8.
-  const uint32_t k_lane = (uint32_t)c * kRowBytes + 16 * g;
+  // K operand of k-step ks for key 16 kh + c: dims 32 ks + 8g .. +8.
+  const uint32_t k_lane = (uint32_t)(16 * kh + c) * kRowBytes + 16 * g;
   // Per-block base addresses are formed once and hidden from the optimizer:
   // otherwise it hoists (lane offset + constant) out of the loop and pays an
   // add per LDS access instead of using the instruction's offset field.
@@ -302,93 +319,115 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
     const uint32_t buf_next = kv_base + (uint32_t)buf_next_i * kBufBytes;
     const uint32_t parity = (uint32_t)(it & 1);
 
-    // ---- S^T = K Q^T: keys 0..31 (two 16-key tiles) x heads 16 wave + c;
-    // two accumulators per tile (even / odd k-steps).
+    // ---- S^T = K Q^T: keys 16 kh .. +16 x heads of tiles 2 hh, 2 hh + 1;
+    // each K operand feeds both head tiles; two accumulators per tile (even /
+    // odd k-steps).
     v4f sa[2][2];
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int u = 0; u < 2; ++u)
 #pragma unroll
-      for (int u = 0; u < 2; ++u) sa[t][u] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int e = 0; e < 2; ++e) sa[u][e] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     {
-      constexpr int kAhead = 3;
-      v4u ka[2][kAhead];
-      auto k_addr = [&](int t, int ks) -> uint32_t { return kbase + (uint32_t)(16 * t * kRowBytes + 64 * ks); };
+      constexpr int kAhead = 4;
+      auto k_addr = [&](int ks) -> uint32_t { return kbase + (uint32_t)(64 * ks); };
+      v4u ka[kAhead];
 #pragma unroll
-      for (int d = 0; d < kAhead; ++d)
-#pragma unroll
-        for (int t = 0; t < 2; ++t) ka[t][d] = lds_load<v4u>(k_addr(t, d));
+      for (int d = 0; d < kAhead; ++d) ka[d] = lds_load<v4u>(k_addr(d));
 #pragma unroll
       for (int ks = 0; ks < kSteps; ++ks) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const v8bf a = as_v8bf(ka[t][ks % kAhead]);
-          if (ks + kAhead < kSteps) ka[t][ks % kAhead] = lds_load<v4u>(k_addr(t, ks + kAhead));
-          mfma_qb(sa[t][ks & 1], a, qb[ks]);
-        }
+        const v8bf a = as_v8bf(ka[ks % kAhead]);
+        if (ks + kAhead < kSteps) ka[ks % kAhead] = lds_load<v4u>(k_addr(ks + kAhead));
+        mfma_qb(sa[0][ks & 1], a, qb[0][ks]);
+        mfma_qb(sa[1][ks & 1], a, qb[1][ks]);
       }
     }
 
     // Operands of the softmax, issued before the MFMA results are read.
-    v4i valid[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-      valid[t] = lds_load<v4i>(rows_base + 4 * (uint32_t)(it * kBlock + 16 * t + 4 * g));
+    const v4i valid = lds_load<v4i>(rows_base + 4 * (uint32_t)(it * kBlock + 16 * kh + 4 * g));
     mfma_drain(sa[0][0], sa[0][1], sa[1][0], sa[1][1]);
 
-    // ---- online softmax of head 16 wave + c over the block (lane (c, g)
-    // holds keys 16t + 4g + r; the max over g uses the row-swap permutes).
+    // ---- softmax, speculatively against the running max: lane (c, g) holds
+    // keys 16 kh + 4g + r of heads 16 (2 hh + u) + c. If no wave sees a block
+    // max above its running max + kRescaleThreshold, the running maxima stand
+    // and P is final; otherwise every wave redoes its part after the barrier.
     float x[2][4];
-    float mx = neg_inf;
+    float mx[2];
+    bool raise = false;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const v4f sum = sa[t][0] + sa[t][1];
+    for (int u = 0; u < 2; ++u) {
+      const v4f sum = sa[u][0] + sa[u][1];
+      mx[u] = neg_inf;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        x[t][r] = valid[t][r] >= 0 ? sum[r] * scale_log2 : neg_inf;
-        mx = fmaxf(mx, x[t][r]);
+        x[u][r] = valid[r] >= 0 ? sum[r] * scale_log2 : neg_inf;
+        mx[u] = fmaxf(mx[u], x[u][r]);
       }
+      mx[u] = max_across_rows(mx[u]);
+      raise |= mx[u] > m_run[u] + kRescaleThreshold || (m_run[u] == neg_inf && mx[u] != neg_inf);
     }
-    mx = max_across_rows(mx);
-    const bool need = mx > m_run + kRescaleThreshold || (m_run == neg_inf && mx != neg_inf);
-    const float m_new = need ? fmaxf(m_run, mx) : m_run;
-    // exp2(-inf) = 0 covers the first valid block.
-    const float alpha = need ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
-    m_run = m_new;
-    l_run *= alpha;
-    float p[2][4];
+    const uint32_t p_own = p_base + parity * 4096 + (uint32_t)((2 * hh) * 64 + lane) * 16 + 8 * kh;
+    float block_sum[2];
+    auto write_p = [&](const float (&mref)[2]) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+      for (int u = 0; u < 2; ++u) {
+        float pu[4];
+        block_sum[u] = 0.0f;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        p[t][r] = m_run == neg_inf ? 0.0f : __builtin_amdgcn_exp2f(x[t][r] - m_run);
-        l_run += p[t][r];
+        for (int r = 0; r < 4; ++r) {
+          // exp2(-inf) = 0 covers invalid keys; a head with no valid key yet
+          // has p = 0.
+          pu[r] = mref[u] == neg_inf ? 0.0f : __builtin_amdgcn_exp2f(x[u][r] - mref[u]);
+          block_sum[u] += pu[r];
+        }
+        lds_store<v2u>(p_own + (uint32_t)u * 1024, v2u{pack_bf16(pu[0], pu[1]), pack_bf16(pu[2], pu[3])});
       }
-    if (g == 0) lds.alpha[parity][16 * wave + c] = alpha;
-    lds_store<v4u>(p_base + parity * 4096 + (uint32_t)(wave * 64 + lane) * 16,
-                   v4u{pack_bf16(p[0][0], p[0][1]), pack_bf16(p[0][2], p[0][3]),
-                       pack_bf16(p[1][0], p[1][1]), pack_bf16(p[1][2], p[1][3])});
+    };
+    write_p(m_run);
+    if (g == 0) {
+      lds.part_max[parity][kh][16 * (2 * hh) + c] = mx[0];
+      lds.part_max[parity][kh][16 * (2 * hh + 1) + c] = mx[1];
+    }
+    if (lane == 0) lds.raise[parity][wave] = __builtin_amdgcn_ballot_w64(raise) != 0;
 
     // ---- block it + 1 -> bf16 rows; block it + 3 -> the freed registers.
     // The buffer of block it + 1 last held block it - 2, whose readers all
     // passed the previous barrier.
     unpack(st, buf_next);
     fetch(st, it + 3);
-    lds_barrier();  // P, alpha and block it + 1's rows visible
+    lds_barrier();  // P, maxima, flags and block it + 1's rows visible
 
-    // ---- O^T += V^T P^T for dims 128 wave + (0..127), all 64 heads.
-    float al[4];
-    bool rescale = false;
+    // ---- a raised running max: new maxima from both key halves, P again,
+    // and the rescale factors of all 64 heads before the PV product.
+    const v4i raised = lds_load<v4i>((uint32_t)(uintptr_t)&lds.raise[parity][0]);
+    if ((raised.x | raised.y | raised.z | raised.w) != 0) {
+      float m_new[2], alpha[2];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      al[t] = lds.alpha[parity][16 * t + c];
-      rescale |= al[t] != 1.0f;
-    }
-    if (__builtin_amdgcn_ballot_w64(rescale)) {
+      for (int u = 0; u < 2; ++u) {
+        const float other = lds.part_max[parity][kh ^ 1][16 * (2 * hh + u) + c];
+        m_new[u] = fmaxf(m_run[u], fmaxf(mx[u], other));
+        // exp2(-inf) = 0 also covers the first block with a valid key.
+        alpha[u] = m_new[u] == neg_inf ? 1.0f : __builtin_amdgcn_exp2f(m_run[u] - m_new[u]);
+        m_run[u] = m_new[u];
+        l_run[u] *= alpha[u];
+      }
+      write_p(m_run);
+      if (kh == 0 && g == 0) {
+        lds.alpha[parity][16 * (2 * hh) + c] = alpha[0];
+        lds.alpha[parity][16 * (2 * hh + 1) + c] = alpha[1];
+      }
+      lds_barrier();
+      float al[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) al[t] = lds.alpha[parity][16 * t + c];
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int m = 0; m < 8; ++m) o[t][m] *= al[t];
     }
+    l_run[0] += block_sum[0];
+    l_run[1] += block_sum[1];
+
+    // ---- O^T += V^T P^T for dims 128 wave + (0..127), all 64 heads.
     v8bf pb[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -419,22 +458,25 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
   // Two blocks per trip so that each register set stays a fixed register set.
   for (int it = 0; it < n_blocks; it += 2) {
     step(it, st1);
-    if (it + 1 < n_blocks) step(it + 1, st0);
+    step(it + 1, st0);
   }
   // The fetches past the last block are never read; let them land before
   // the registers are released.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  // ---- row sums of all 64 heads, then O / l.
-  float l = l_run;
-  l += __shfl_xor(l, 16);
-  l += __shfl_xor(l, 32);
-  if (g == 0) lds.row_sum[16 * wave + c] = l;
+  // ---- row sums of all 64 heads (both key halves), then O / l.
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    float l = l_run[u];
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    if (g == 0) lds.row_sum[kh][16 * (2 * hh + u) + c] = l;
+  }
   __syncthreads();
   uint16_t* obase = out + ((row * heads + head0 + c) * kVDim) + 128 * wave + 4 * g;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    const float lt = lds.row_sum[16 * t + c];
+    const float lt = lds.row_sum[0][16 * t + c] + lds.row_sum[1][16 * t + c];
     const float inv_l = lt > 0.0f ? 1.0f / lt : 0.0f;
     uint16_t* orow = obase + (int64_t)16 * t * kVDim;
 #pragma unroll

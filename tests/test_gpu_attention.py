@@ -108,6 +108,25 @@ def test_empty_tiles_and_large_logits_keep_online_softmax_stable(gpu):
     assert torch.equal(actual, torch.full_like(actual, 2))
 
 
+def test_rising_and_falling_scores_across_blocks(gpu):
+    """RoPE norms grow along the selection (row 0) or shrink (row 1), so the
+    running maxima rise block after block in row 0 and only at the start in
+    row 1; the online-softmax rescaling must match the one-pass oracle. The
+    latent (value) part stays at unit scale."""
+    from cxldsagr_amd.attention import sparse_mla
+
+    torch.manual_seed(77)
+    n = 2048
+    kv = torch.randn(n, 576)
+    kv[:, 512:] *= torch.linspace(0.1, 24.0, n)[:, None]
+    kv = kv.to(device=gpu, dtype=torch.bfloat16)
+    q = torch.randn(2, 128, 576, device=gpu, dtype=torch.bfloat16)
+    ids = torch.arange(n, dtype=torch.int32).repeat(2, 1)
+    ids[1] = ids[1].flip(0)
+    ids = ids.to(gpu)
+    _assert_attention_close(sparse_mla(q, kv, ids, SCALE), _oracle(q, kv, ids, SCALE))
+
+
 def test_known_answers_duplicates_padding_and_rope(gpu):
     from cxldsagr_amd.attention import sparse_mla
 
