@@ -17,8 +17,10 @@
 // 3. the remaining digits (11/10/11/11/10 bits) are resolved on the LDS
 //    buffer; a bucket too large for LDS (huge ties, e.g. masked rows) falls
 //    back to further histogram passes over the row;
-// 4. bitonic sort of the <= 2048 selected keys in LDS, then values and
-//    indices are decoded from the keys.
+// 4. bitonic sort of the <= 2048 selected keys (two per thread; partners
+//    within a wave are exchanged with DPP / row-swap lane moves, only
+//    strides of 128 and more go through LDS), then values and indices are
+//    decoded from the keys.
 //
 // One 1024-thread work-group per row; the row is read twice from HBM/L2 in
 // the common case.
@@ -120,6 +122,36 @@ __device__ __forceinline__ uint32_t wave_slot(uint32_t* counter, bool take) {
   uint32_t base = 0;
   if ((int)(threadIdx.x & 63) == leader) base = atomicAdd(counter, (uint32_t)__builtin_popcountll(mask));
   return __builtin_amdgcn_readlane(base, leader) + lanes_below;
+}
+
+// Value of lane (lane ^ kM) for kM = 1 .. 32 with VALU-only lane moves:
+// quad permutes (DPP quad_perm) for 1 and 2; for 4 and 8 a quad reversal
+// (lane ^ 3) or row mirror (lane ^ 15) followed by a half-row mirror
+// (lane ^ 7); for 16 and 32 the gfx950 row-swap permutes, whose result
+// pair holds (even row, odd row) of each row pair.
+template <int kM>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
+  if constexpr (kM == 1) {
+    return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
+  } else if constexpr (kM == 2) {
+    return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);
+  } else if constexpr (kM == 4) {
+    return __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(v, 0x1B, 0xF, 0xF, false), 0x141, 0xF, 0xF, false);
+  } else if constexpr (kM == 8) {
+    return __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, false), 0x141, 0xF, 0xF, false);
+  } else if constexpr (kM == 16) {
+    const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (threadIdx.x & 16) ? p[0] : p[1];
+  } else {
+    static_assert(kM == 32, "lane distance");
+    const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (threadIdx.x & 32) ? p[0] : p[1];
+  }
+}
+
+template <int kM>
+__device__ __forceinline__ uint64_t lane_xor64(uint64_t v) {
+  return ((uint64_t)lane_xor<kM>((uint32_t)(v >> 32)) << 32) | lane_xor<kM>((uint32_t)v);
 }
 
 __device__ __forceinline__ void clear_hist(Shared& sh) {
@@ -402,47 +434,80 @@ __global__ __launch_bounds__(kThreads, 1) void topk_rows(const float* __restrict
   uint64_t x0 = active ? sh.sel[2 * tid] : 0;
   uint64_t x1 = active ? sh.sel[2 * tid + 1] : 0;
   const int p0 = 2 * tid;
-  // Keeps the larger key at the lower position inside descending blocks.
+  const int lane = tid & 63;
+  // Compare-exchange of a pair (lo at the lower position): the larger key
+  // goes first inside descending blocks.
   auto order = [](uint64_t& lo, uint64_t& hi, bool descending) {
-    const bool swap = descending ? lo < hi : lo > hi;
+    const bool swap = (lo < hi) == descending;
     const uint64_t a = lo, b = hi;
     lo = swap ? b : a;
     hi = swap ? a : b;
   };
-  auto shfl64 = [](uint64_t v, int mask) -> uint64_t {
-    const uint32_t lo = __shfl_xor((uint32_t)v, mask);
-    const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), mask);
-    return ((uint64_t)hi << 32) | lo;
+  // Strides 2..16: partner lane ^ kM (kM = stride / 2), fetched by DPP; the
+  // lane keeps the larger key iff it holds the lower position of a
+  // descending block (or the upper of an ascending one).
+  auto exchange_dpp = [&](auto m_tag, int size) {
+    constexpr int kM = decltype(m_tag)::value;
+    const bool desc = (p0 & size) == 0;
+    const bool keep_max = ((lane & kM) == 0) == desc;
+    const uint64_t y0 = lane_xor64<kM>(x0);
+    const uint64_t y1 = lane_xor64<kM>(x1);
+    x0 = ((x0 < y0) == keep_max) ? y0 : x0;
+    x1 = ((x1 < y1) == keep_max) ? y1 : x1;
+  };
+  // Strides 32 and 64 (lane ^ 16, lane ^ 32): one row-swap permute of (x0,
+  // x1) leaves every lane holding a whole pair - lanes with the distance bit
+  // clear get x0 of lanes l and l + kM, the others x1 of lanes l - kM and l -
+  // so the exchange happens in-lane and a second permute restores the layout.
+  auto exchange_swap = [&](auto m_tag, int size) {
+    constexpr int kM = decltype(m_tag)::value;
+    auto swap32 = [](uint32_t& a, uint32_t& b) {
+      const auto r = kM == 16 ? __builtin_amdgcn_permlane16_swap(a, b, false, false)
+                              : __builtin_amdgcn_permlane32_swap(a, b, false, false);
+      a = r[0];
+      b = r[1];
+    };
+    uint32_t a_lo = (uint32_t)x0, a_hi = (uint32_t)(x0 >> 32);
+    uint32_t b_lo = (uint32_t)x1, b_hi = (uint32_t)(x1 >> 32);
+    swap32(a_lo, b_lo);
+    swap32(a_hi, b_hi);
+    // The pair's lower position: 2l (x0 of lane l) or 2 (l - kM) + 1.
+    const int first = (lane & kM) ? 2 * ((tid & ~63) + lane - kM) + 1 : p0;
+    uint64_t lo = ((uint64_t)a_hi << 32) | a_lo;
+    uint64_t hi = ((uint64_t)b_hi << 32) | b_lo;
+    order(lo, hi, (first & size) == 0);
+    a_lo = (uint32_t)lo;
+    a_hi = (uint32_t)(lo >> 32);
+    b_lo = (uint32_t)hi;
+    b_hi = (uint32_t)(hi >> 32);
+    swap32(a_lo, b_lo);
+    swap32(a_hi, b_hi);
+    x0 = ((uint64_t)a_hi << 32) | a_lo;
+    x1 = ((uint64_t)b_hi << 32) | b_lo;
   };
   for (int size = 2; size <= padded; size <<= 1) {
-    const bool desc = (p0 & size) == 0;  // same for p0 and p0 + 1 (size >= 2)
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      if (stride == 1) {
-        order(x0, x1, desc);
-      } else if (stride <= 64) {
-        const int m = stride >> 1;  // partner lane distance
-        const uint64_t y0 = shfl64(x0, m);
-        const uint64_t y1 = shfl64(x1, m);
-        const bool lower = (p0 & stride) == 0;  // this lane holds the lower positions
-        // keep = the larger of the pair iff (lower == desc)
-        const bool keep_max = lower == desc;
-        x0 = keep_max ? (x0 > y0 ? x0 : y0) : (x0 < y0 ? x0 : y0);
-        x1 = keep_max ? (x1 > y1 ? x1 : y1) : (x1 < y1 ? x1 : y1);
-      } else {
-        if (active) {
-          sh.sel[p0] = x0;
-          sh.sel[p0 + 1] = x1;
-        }
-        __syncthreads();
-        const uint64_t y0 = active ? sh.sel[p0 ^ stride] : 0;
-        const uint64_t y1 = active ? sh.sel[(p0 + 1) ^ stride] : 0;
-        const bool lower = (p0 & stride) == 0;
-        const bool keep_max = lower == desc;
-        x0 = keep_max ? (x0 > y0 ? x0 : y0) : (x0 < y0 ? x0 : y0);
-        x1 = keep_max ? (x1 > y1 ? x1 : y1) : (x1 < y1 ? x1 : y1);
-        __syncthreads();
+    // Strides 128 .. size / 2 through LDS.
+    for (int stride = size >> 1; stride >= 128; stride >>= 1) {
+      const bool desc = (p0 & size) == 0;
+      if (active) {
+        sh.sel[p0] = x0;
+        sh.sel[p0 + 1] = x1;
       }
+      __syncthreads();
+      const uint64_t y0 = active ? sh.sel[p0 ^ stride] : 0;
+      const uint64_t y1 = active ? sh.sel[(p0 + 1) ^ stride] : 0;
+      const bool keep_max = ((p0 & stride) == 0) == desc;
+      x0 = ((x0 < y0) == keep_max) ? y0 : x0;
+      x1 = ((x1 < y1) == keep_max) ? y1 : x1;
+      __syncthreads();
     }
+    if (size >= 128) exchange_swap(std::integral_constant<int, 32>{}, size);
+    if (size >= 64) exchange_swap(std::integral_constant<int, 16>{}, size);
+    if (size >= 32) exchange_dpp(std::integral_constant<int, 8>{}, size);
+    if (size >= 16) exchange_dpp(std::integral_constant<int, 4>{}, size);
+    if (size >= 8) exchange_dpp(std::integral_constant<int, 2>{}, size);
+    if (size >= 4) exchange_dpp(std::integral_constant<int, 1>{}, size);
+    order(x0, x1, (p0 & size) == 0);
   }
   if (active) {
     sh.sel[p0] = x0;
