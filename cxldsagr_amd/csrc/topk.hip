@@ -300,12 +300,52 @@ __global__ __launch_bounds__(kThreads, 1) void topk_rows(const float* __restrict
     // ---- level 0 histogram over the row
     const bool resident = vec && cols <= kResidentCols;
     Resident res;
-    if (resident) res.load(row, cols);
+    uint32_t floor_key = 0;  // radix keys below it cannot be among the top `count`
+    // Resident slots e < n_valid hold row elements (columns grow with e).
+    int n_valid = 0;
+    if (resident) {
+      res.load(row, cols);
+#pragma unroll
+      for (int d = 0; d < kResidentVec; ++d) {
+        const int32_t left = (int32_t)cols - 4 * (d * kThreads + tid);
+        n_valid += left <= 0 ? 0 : (left >= 4 ? 4 : left);
+      }
+      // Values -> radix keys in place, and each thread's two largest keys.
+      // The 2048 >= count keys so found are a subset of the row, so their
+      // minimum is at most the count-th largest key: every key below it can
+      // be left out of the search (typically ~85-95 % of the row).
+      uint32_t t1 = 0, t2 = 0;
+#pragma unroll
+      for (int e = 0; e < 4 * kResidentVec; ++e) {
+        const uint32_t r = e < n_valid ? radix_key(res.v[e]) : 0u;
+        res.v[e] = __uint_as_float(r);
+        t2 = max(t2, min(t1, r));
+        t1 = max(t1, r);
+      }
+      t2 = min(t2, lane_xor<1>(t2));
+      t2 = min(t2, lane_xor<2>(t2));
+      t2 = min(t2, lane_xor<4>(t2));
+      t2 = min(t2, lane_xor<8>(t2));
+      t2 = min(t2, lane_xor<16>(t2));
+      t2 = min(t2, lane_xor<32>(t2));
+      if ((tid & 63) == 0) sh.wave_sums[tid >> 6] = t2;
+    }
     clear_hist(sh);
     __syncthreads();
     auto count_top = [&](float v, int64_t) { atomicAdd(&my_hist(sh)[radix_key(v) >> 21], 1u); };
-    if (resident) res.for_each(cols, count_top);
-    else for_each_element(row, cols, vec, count_top);
+    if (resident) {
+      floor_key = sh.wave_sums[0];
+#pragma unroll
+      for (int w = 1; w < kThreads / 64; ++w) floor_key = min(floor_key, sh.wave_sums[w]);
+      uint32_t* hist = my_hist(sh);
+#pragma unroll
+      for (int e = 0; e < 4 * kResidentVec; ++e) {
+        const uint32_t r = __float_as_uint(res.v[e]);
+        if (e < n_valid && r >= floor_key) atomicAdd(&hist[r >> 21], 1u);
+      }
+    } else {
+      for_each_element(row, cols, vec, count_top);
+    }
     __syncthreads();
     uint32_t remaining = (uint32_t)count;
     find_bucket(sh, remaining);
@@ -363,8 +403,80 @@ __global__ __launch_bounds__(kThreads, 1) void topk_rows(const float* __restrict
           }
         }
       };
-      if (resident) res.for_each_batch(cols, select_batch);
-      else for_each_batch(row, cols, vec, select_batch);
+      if (resident) {
+        // Survivor masks first (bit e % 32 of word e / 32 for resident value
+        // e, column 4 ((e / 4) kThreads + tid) + e % 4), then one pass over
+        // the set bits only: survivors are a few percent of the row.
+        constexpr int kValues = 4 * kResidentVec;
+        constexpr int kWords = (kValues + 31) / 32;
+        uint32_t m_sel[kWords], m_buf[kWords];
+#pragma unroll
+        for (int h = 0; h < kWords; ++h) {
+          m_sel[h] = 0;
+          m_buf[h] = 0;
+        }
+#pragma unroll
+        for (int e = 0; e < kValues; ++e) {
+          const uint32_t r = __float_as_uint(res.v[e]);  // radix key
+          const uint32_t dig = r >> 21;
+          const bool ok = e < n_valid;
+          m_sel[e >> 5] |= (ok && dig > d0_32) ? 1u << (e & 31) : 0u;
+          // Only keys the histogram counted (>= floor_key) enter the refinement.
+          m_buf[e >> 5] |= (ok && dig == d0_32 && r >= floor_key) ? 1u << (e & 31) : 0u;
+        }
+        uint32_t cnt_sel = 0, cnt_buf = 0;
+#pragma unroll
+        for (int h = 0; h < kWords; ++h) {
+          cnt_sel += (uint32_t)__builtin_popcount(m_sel[h]);
+          cnt_buf += (uint32_t)__builtin_popcount(m_buf[h]);
+        }
+        // Exclusive prefix over the wave from bit-plane ballots (counts <= 68).
+        uint32_t pre_sel = 0, pre_buf = 0, tot_sel = 0, tot_buf = 0;
+#pragma unroll 1
+        for (int bit = 0; bit < 7; ++bit) {
+          const uint64_t ms = __builtin_amdgcn_ballot_w64((cnt_sel >> bit) & 1u);
+          const uint64_t mb = __builtin_amdgcn_ballot_w64((cnt_buf >> bit) & 1u);
+          pre_sel += __builtin_amdgcn_mbcnt_hi((uint32_t)(ms >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)ms, 0)) << bit;
+          pre_buf += __builtin_amdgcn_mbcnt_hi((uint32_t)(mb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mb, 0)) << bit;
+          tot_sel += (uint32_t)__builtin_popcountll(ms) << bit;
+          tot_buf += (uint32_t)__builtin_popcountll(mb) << bit;
+        }
+        uint32_t base_sel = 0, base_buf = 0;
+        if (lane == 0) {
+          if (tot_sel) base_sel = atomicAdd(&sh.n_sel, tot_sel);
+          if (tot_buf) base_buf = atomicAdd(&sh.n_buf, tot_buf);
+        }
+        uint32_t at_sel = __builtin_amdgcn_readfirstlane(base_sel) + pre_sel;
+        uint32_t at_buf = __builtin_amdgcn_readfirstlane(base_buf) + pre_buf;
+        // Columns into the lists; the keys follow from the row (in L2).
+#pragma unroll
+        for (int h = 0; h < kWords; ++h) {
+          uint32_t m = m_sel[h] | m_buf[h];
+          while (m) {
+            const int e = __builtin_ctz(m);
+            m &= m - 1;
+            const int idx = 32 * h + e;
+            const uint32_t col = 4 * ((uint32_t)(idx >> 2) * kThreads + (uint32_t)tid) + (uint32_t)(idx & 3);
+            if ((m_sel[h] >> e) & 1u) {
+              if (at_sel < kMaxK) sh.sel[at_sel] = col;
+              ++at_sel;
+            } else {
+              if (at_buf < kRefineCap) sh.buf[at_buf] = col;
+              ++at_buf;
+            }
+          }
+        }
+        __syncthreads();
+        const uint32_t ns = sh.n_sel < kMaxK ? sh.n_sel : kMaxK;
+        const uint32_t nb = sh.n_buf < kRefineCap ? sh.n_buf : kRefineCap;
+        for (uint32_t i = tid; i < ns + nb; i += kThreads) {
+          uint64_t* slot = i < ns ? &sh.sel[i] : &sh.buf[i - ns];
+          const uint32_t col = (uint32_t)*slot;
+          *slot = composite(row[col], col);
+        }
+      } else {
+        for_each_batch(row, cols, vec, select_batch);
+      }
       __syncthreads();
       const uint32_t nbuf = sh.n_buf < kRefineCap ? sh.n_buf : kRefineCap;
       for (int level = 1; level < kLevels && !resolved; ++level) {
