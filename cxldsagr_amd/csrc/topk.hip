@@ -58,6 +58,9 @@ struct Shared {
   uint64_t sel[kMaxK];
   uint64_t buf[kRefineCap];
   uint32_t wave_sums[kThreads / 64];
+  uint64_t wave_max[kThreads / 64];
+  uint64_t wave_min[kThreads / 64];
+  uint32_t sort_fallback;
   uint32_t n_sel;
   uint32_t n_buf;
   uint32_t digit;
@@ -160,6 +163,96 @@ __device__ __forceinline__ void clear_hist(Shared& sh) {
 
 __device__ __forceinline__ uint32_t* my_hist(Shared& sh) { return sh.hist[(threadIdx.x >> 6) % kSubHists]; }
 
+// Counting sort of the unique keys sh.sel[0 .. count), descending: 2048
+// linear buckets over the keys' own range [smallest, largest] (so equal
+// values spread over their column bits), scatter, then place each key by its
+// rank inside its bucket. Returns false, leaving sh.sel as it was, when a bucket holds
+// more than kMaxBucket keys (the caller then runs the bitonic network).
+constexpr uint32_t kMaxBucket = 32;
+__device__ bool counting_sort(Shared& sh, int count) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  uint32_t* counts = sh.hist[0];
+  uint32_t* start = sh.hist[1];
+  uint32_t* cursor = sh.hist[2];
+  for (int i = tid; i < kBins; i += kThreads) counts[i] = 0;
+  if (tid == 0) sh.sort_fallback = 0;
+  uint64_t kmax = 0, kmin = ~0ull;
+  for (int i = tid; i < count; i += kThreads) {
+    const uint64_t key = sh.sel[i];
+    kmax = key > kmax ? key : kmax;
+    kmin = key < kmin ? key : kmin;
+  }
+  auto reduce = [&](auto m_tag) {
+    constexpr int kM = decltype(m_tag)::value;
+    const uint64_t a = lane_xor64<kM>(kmax), b = lane_xor64<kM>(kmin);
+    kmax = a > kmax ? a : kmax;
+    kmin = b < kmin ? b : kmin;
+  };
+  reduce(std::integral_constant<int, 1>{});
+  reduce(std::integral_constant<int, 2>{});
+  reduce(std::integral_constant<int, 4>{});
+  reduce(std::integral_constant<int, 8>{});
+  reduce(std::integral_constant<int, 16>{});
+  reduce(std::integral_constant<int, 32>{});
+  if (lane == 0) {
+    sh.wave_max[wave] = kmax;
+    sh.wave_min[wave] = kmin;
+  }
+  __syncthreads();
+  kmax = sh.wave_max[0];
+  kmin = sh.wave_min[0];
+#pragma unroll
+  for (int w = 1; w < kThreads / 64; ++w) {
+    kmax = sh.wave_max[w] > kmax ? sh.wave_max[w] : kmax;
+    kmin = sh.wave_min[w] < kmin ? sh.wave_min[w] : kmin;
+  }
+  // Linear buckets over [kmin, kmax]: the key distance from kmin, scaled to
+  // 11 bits (monotone in the key).
+  const uint64_t span = kmax - kmin;
+  const int bits = span == 0 ? 0 : 64 - __builtin_clzll(span);
+  const int shift = bits > 11 ? bits - 11 : 0;
+  auto digit = [kmin, shift](uint64_t key) -> uint32_t { return (uint32_t)((key - kmin) >> shift); };
+  for (int i = tid; i < count; i += kThreads) atomicAdd(&counts[digit(sh.sel[i])], 1u);
+  __syncthreads();
+  // Bucket starts in descending digit order; thread t owns bins 2t, 2t + 1.
+  const uint32_t h0 = counts[2 * tid], h1 = counts[2 * tid + 1];
+  uint32_t incl = h0 + h1;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t o = __shfl_up(incl, d);
+    if (lane >= d) incl += o;
+  }
+  if (lane == 63) sh.wave_sums[wave] = incl;
+  if (h0 > kMaxBucket || h1 > kMaxBucket) sh.sort_fallback = 1;
+  __syncthreads();
+  uint32_t before = 0;
+  for (int w = 0; w < wave; ++w) before += sh.wave_sums[w];
+  const uint32_t above_pair = (uint32_t)count - (incl + before);
+  start[2 * tid + 1] = above_pair;
+  cursor[2 * tid + 1] = above_pair;
+  start[2 * tid] = above_pair + h1;
+  cursor[2 * tid] = above_pair + h1;
+  __syncthreads();
+  if (sh.sort_fallback) return false;
+  for (int i = tid; i < count; i += kThreads) {
+    const uint64_t key = sh.sel[i];
+    sh.buf[atomicAdd(&cursor[digit(key)], 1u)] = key;
+  }
+  __syncthreads();
+  for (int i = tid; i < count; i += kThreads) {
+    const uint64_t key = sh.buf[i];
+    const uint32_t d = digit(key);
+    const uint32_t b0 = start[d], n = counts[d];
+    uint32_t rank = 0;
+    for (uint32_t j = b0; j < b0 + n; ++j) rank += sh.buf[j] > key ? 1u : 0u;
+    sh.sel[b0 + rank] = key;
+  }
+  __syncthreads();
+  return true;
+}
+
 // Calls f(value, column) for every element of the row, each thread with four
 // 16-byte loads in flight.
 template <typename F>
@@ -228,9 +321,14 @@ __device__ __forceinline__ void for_each_batch(const float* row, int64_t cols, b
 // A row of up to kResident * kThreads elements is read from memory once and
 // kept in registers (thread t: float4 slots d * kThreads + t) for both the
 // histogram and the selection pass.
-constexpr int kResidentVec = 17;
-constexpr int64_t kResidentCols = 4 * kResidentVec * kThreads;  // 69632
+// Register capacities: 17 float4 per thread (69,632 columns) for whole rows,
+// 9 (36,864) for the halves of split rows, so a thread walks only slots that
+// can hold row elements.
+constexpr int kResidentVecLarge = 17;
+constexpr int kResidentVecSmall = 9;
+constexpr int64_t resident_cols(int vecs) { return 4 * (int64_t)vecs * kThreads; }
 
+template <int kResidentVec>
 struct Resident {
   float v[4 * kResidentVec];
   __device__ __forceinline__ void load(const float* row, int64_t cols) {
@@ -279,14 +377,27 @@ struct Resident {
   }
 };
 
+// Work-group (r, h) of a grid (rows, parts) selects and sorts the top
+// min(count, columns of its part) keys of row r's part h. With one part that
+// is the answer. With two (columns split at a multiple of 4 near the middle),
+// each part stores its sorted keys in the workspace and topk_merge, launched
+// next on the same stream, merges them.
+template <int kResidentVec>
 __global__ __launch_bounds__(kThreads, 1) void topk_rows(const float* __restrict__ scores,
-                                                        int64_t cols, int64_t ld, int count,
+                                                        int64_t all_cols, int64_t ld, int total_count,
                                                         float* __restrict__ values,
                                                         int32_t* __restrict__ ids,
-                                                        int64_t out_ld) {
+                                                        int64_t out_ld, uint64_t* ws_keys) {
   __shared__ Shared sh;
   const int tid = threadIdx.x;
-  const float* row = scores + (int64_t)blockIdx.x * ld;
+  const int64_t r = blockIdx.x;
+  const int part = blockIdx.y;
+  const int parts = gridDim.y;
+  const int64_t part_cols = parts == 1 ? all_cols : ((((all_cols + 1) >> 1) + 3) & ~(int64_t)3);
+  const int64_t col0 = part * part_cols;
+  const int64_t cols = part_cols < all_cols - col0 ? part_cols : all_cols - col0;
+  const int count = total_count < cols ? total_count : (int)cols;
+  const float* row = scores + r * ld + col0;
   const bool vec = ((reinterpret_cast<uintptr_t>(row) & 15) == 0);
 
   if (tid == 0) {
@@ -298,8 +409,8 @@ __global__ __launch_bounds__(kThreads, 1) void topk_rows(const float* __restrict
     for (int64_t i = tid; i < cols; i += kThreads) sh.sel[i] = composite(row[i], i);
   } else {
     // ---- level 0 histogram over the row
-    const bool resident = vec && cols <= kResidentCols;
-    Resident res;
+    const bool resident = vec && cols <= resident_cols(kResidentVec);
+    Resident<kResidentVec> res;
     uint32_t floor_key = 0;  // radix keys below it cannot be among the top `count`
     // Resident slots e < n_valid hold row elements (columns grow with e).
     int n_valid = 0;
@@ -534,10 +645,11 @@ __global__ __launch_bounds__(kThreads, 1) void topk_rows(const float* __restrict
   }
   __syncthreads();
 
-  // ---- bitonic sort of `count` keys, descending (padding keys are 0).
-  // Thread t holds positions 2t and 2t + 1 in registers. Partners at stride
-  // 1 are in the same thread, strides 2..64 in the same wave (lane ^ s/2,
-  // exchanged with lane shuffles); only strides >= 128 go through LDS.
+  // ---- sort `count` keys, descending: counting sort, or when a bucket is
+  // crowded, a bitonic network (padding keys are 0). Thread t holds
+  // positions 2t and 2t + 1 in registers; partners at stride 1 are in the
+  // same thread, strides 2..64 in the same wave, strides >= 128 in LDS.
+  if (!counting_sort(sh, count)) {
   int padded = 2;
   while (padded < count) padded <<= 1;
   for (int i = count + tid; i < padded; i += kThreads) sh.sel[i] = 0;
@@ -626,15 +738,73 @@ __global__ __launch_bounds__(kThreads, 1) void topk_rows(const float* __restrict
     sh.sel[p0 + 1] = x1;
   }
   __syncthreads();
+  }
 
-  float* vout = values + (int64_t)blockIdx.x * out_ld;
-  int32_t* iout = ids + (int64_t)blockIdx.x * out_ld;
-  for (int i = tid; i < count; i += kThreads) {
-    const uint64_t key = sh.sel[i];
+  float* vout = values + r * out_ld;
+  int32_t* iout = ids + r * out_ld;
+  auto emit = [&](int i, uint64_t key) {
     const uint32_t bits = key_bits((uint32_t)(key >> 32));
     vout[i] = __uint_as_float(bits);
     const bool finite = (bits & 0x7F800000u) != 0x7F800000u;
     iout[i] = finite ? (int32_t)(~(uint32_t)key) : -1;
+  };
+  if (parts == 1) {
+    for (int i = tid; i < count; i += kThreads) emit(i, sh.sel[i]);
+    return;
+  }
+
+  // ---- two parts: this part's sorted list (row-global columns) goes to the
+  // workspace; topk_merge combines the two lists of each row.
+  uint64_t* mine = ws_keys + (r * 2 + part) * kMaxK;
+  for (int i = tid; i < count; i += kThreads) {
+    const uint64_t key = sh.sel[i];
+    const uint32_t col = ~(uint32_t)key + (uint32_t)col0;
+    mine[i] = (key & 0xFFFFFFFF00000000ull) | (uint64_t)(~col);
+  }
+}
+
+// Merge path over the two descending key lists of a row (keys are unique):
+// thread t emits outputs 2t and 2t + 1 of the top `count`.
+__global__ __launch_bounds__(kThreads, 1) void topk_merge(const uint64_t* __restrict__ ws_keys,
+                                                         int64_t all_cols, int count,
+                                                         float* __restrict__ values,
+                                                         int32_t* __restrict__ ids, int64_t out_ld) {
+  __shared__ uint64_t A[kMaxK];
+  __shared__ uint64_t B[kMaxK];
+  const int tid = threadIdx.x;
+  const int64_t r = blockIdx.x;
+  const int64_t part_cols = (((all_cols + 1) >> 1) + 3) & ~(int64_t)3;
+  const int n_a = count < part_cols ? count : (int)part_cols;
+  const int64_t rest = all_cols - part_cols;
+  const int n_b = count < rest ? count : (int)rest;
+  const uint64_t* src = ws_keys + r * 2 * kMaxK;
+  for (int i = tid; i < n_a; i += kThreads) A[i] = src[i];
+  for (int i = tid; i < n_b; i += kThreads) B[i] = src[kMaxK + i];
+  __syncthreads();
+  float* vout = values + r * out_ld;
+  int32_t* iout = ids + r * out_ld;
+  const int p = 2 * tid;
+  if (p >= count) return;
+  int lo = p - n_b > 0 ? p - n_b : 0;
+  int hi = p < n_a ? p : n_a;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (A[mid] > B[p - 1 - mid]) lo = mid + 1;
+    else hi = mid;
+  }
+  int i = lo, j = p - lo;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    if (p + q < count) {
+      const bool take_a = i < n_a && (j >= n_b || A[i] > B[j]);
+      const uint64_t key = take_a ? A[i] : B[j];
+      if (take_a) ++i;
+      else ++j;
+      const uint32_t bits = key_bits((uint32_t)(key >> 32));
+      vout[p + q] = __uint_as_float(bits);
+      const bool finite = (bits & 0x7F800000u) != 0x7F800000u;
+      iout[p + q] = finite ? (int32_t)(~(uint32_t)key) : -1;
+    }
   }
 }
 
@@ -654,8 +824,54 @@ extern "C" int dsa_topk_radix(const float* scores, int64_t rows, int64_t columns
   if (rows == 0) return kOk;
   DSA_CHECK_ARG(scores && values && indices, "null pointer");
   DSA_CHECK_ARG(rows < 0x7FFFFFFF, "too many rows");
-  hipLaunchKernelGGL(topk_rows, dim3((unsigned)rows), dim3(kThreads), 0, stream, scores, columns,
-                     ld, (int)count, values, indices, out_ld);
+  auto kernel = columns <= resident_cols(kResidentVecSmall) ? topk_rows<kResidentVecSmall>
+                                                             : topk_rows<kResidentVecLarge>;
+  hipLaunchKernelGGL(kernel, dim3((unsigned)rows, 1), dim3(kThreads), 0, stream, scores, columns,
+                     ld, (int)count, values, indices, out_ld, nullptr);
+  DSA_CHECK_LAUNCH("exact top-k");
+  return kOk;
+}
+
+namespace dsa {
+namespace {
+int64_t topk_workspace_bytes(int64_t rows) { return rows * 2 * kMaxK * 8; }
+}  // namespace
+}  // namespace dsa
+
+extern "C" int dsa_topk_workspace_bytes(int64_t rows, int64_t* bytes) {
+  using namespace dsa;
+  DSA_CHECK_ARG(rows >= 0 && rows < 0x7FFFFFFF && bytes != nullptr, "invalid top-k workspace query");
+  *bytes = topk_workspace_bytes(rows);
+  return kOk;
+}
+
+extern "C" int dsa_topk_radix_split(const float* scores, int64_t rows, int64_t columns, int64_t ld,
+                                    int64_t k, float* values, int32_t* indices, int64_t out_ld,
+                                    void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  using namespace dsa;
+  DSA_CHECK_ARG(columns >= 1, "scores must have nonempty visible tokens");
+  DSA_CHECK_ARG(k >= 1 && k <= kMaxK, "k must be an integer in [1, 2048]");
+  DSA_CHECK_ARG(ld >= columns && rows >= 0, "invalid score layout");
+  DSA_CHECK_ARG(columns < (int64_t)0x7FFFFFFF, "column count must fit int32");
+  const int64_t count = k < columns ? k : columns;
+  DSA_CHECK_ARG(out_ld >= count, "output row stride too small");
+  if (rows == 0) return kOk;
+  DSA_CHECK_ARG(scores && values && indices, "null pointer");
+  DSA_CHECK_ARG(rows < 0x7FFFFFFF, "too many rows");
+  // Rows too short to be worth two work-groups take the one-part kernel.
+  if (columns < 4 * kMaxK) return dsa_topk_radix(scores, rows, columns, ld, k, values, indices, out_ld, stream);
+  DSA_CHECK_ARG(workspace != nullptr && workspace_bytes >= topk_workspace_bytes(rows),
+                "top-k workspace too small");
+  DSA_CHECK_ARG(reinterpret_cast<uintptr_t>(workspace) % 8 == 0, "workspace must be 8-byte aligned");
+  uint64_t* keys = static_cast<uint64_t*>(workspace);
+  const int64_t part_cols = (((columns + 1) >> 1) + 3) & ~(int64_t)3;
+  auto kernel = part_cols <= resident_cols(kResidentVecSmall) ? topk_rows<kResidentVecSmall>
+                                                               : topk_rows<kResidentVecLarge>;
+  hipLaunchKernelGGL(kernel, dim3((unsigned)rows, 2), dim3(kThreads), 0, stream, scores, columns,
+                     ld, (int)count, values, indices, out_ld, keys);
+  DSA_CHECK_LAUNCH("exact top-k");
+  hipLaunchKernelGGL(topk_merge, dim3((unsigned)rows), dim3(kThreads), 0, stream, keys, columns,
+                     (int)count, values, indices, out_ld);
   DSA_CHECK_LAUNCH("exact top-k");
   return kOk;
 }

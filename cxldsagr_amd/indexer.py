@@ -14,6 +14,8 @@ All work runs in hand-written gfx950 kernels (``csrc/quantize.hip``,
 no host synchronisation.
 """
 
+import ctypes
+
 import torch
 
 from cxldsagr_amd import _native
@@ -207,8 +209,10 @@ def exact_topk(scores, k):
     if scores.stride(1) != 1 or scores.stride(0) < columns:
         scores = scores.contiguous()
     with torch.cuda.device(device):
+        stream = _native.stream_of(device)
+        workspace = _topk_workspace(device, stream, rows)
         _native.call(
-            "dsa_topk_radix",
+            "dsa_topk_radix_split",
             _native.ptr(scores),
             rows,
             columns,
@@ -217,6 +221,24 @@ def exact_topk(scores, k):
             _native.ptr(values),
             _native.ptr(indices),
             count,
-            _native.stream_of(device),
+            _native.ptr(workspace),
+            workspace.numel(),
+            stream,
         )
     return values, indices
+
+
+# Per (device, stream) workspace of the two-part top-k (the sorted half lists
+# of every row), reused by all stream-ordered calls on that stream.
+_TOPK_WORKSPACES = {}
+
+
+def _topk_workspace(device, stream, rows):
+    key = (device.index, stream.value)
+    workspace = _TOPK_WORKSPACES.get(key)
+    needed = ctypes.c_int64()
+    _native.call("dsa_topk_workspace_bytes", rows, ctypes.byref(needed))
+    if workspace is None or workspace.numel() < needed.value:
+        workspace = torch.empty(needed.value, dtype=torch.uint8, device=device)
+        _TOPK_WORKSPACES[key] = workspace
+    return workspace

@@ -82,6 +82,22 @@ int dsa_indexer_logits_fp8(const void* q, const void* k, const float* weights,
 int dsa_topk_radix(const float* scores, int64_t rows, int64_t columns, int64_t ld, int64_t k,
                    float* values, int32_t* indices, int64_t out_ld, hipStream_t stream);
 
+/*
+ * A6, same contract and results as dsa_topk_radix, with each row of 8192 or
+ * more columns split over two work-groups (each selects and sorts the top
+ * min(k, half) keys of its half into the workspace; a second launch on the
+ * same stream merges the two lists of every row), so that a launch of Q rows
+ * occupies 2Q compute units. Replaces the same exact_topk
+ * (selection.py:62-113). workspace: device memory of the size
+ * dsa_topk_workspace_bytes(rows, &bytes) stores, 8-byte aligned, no
+ * initialisation needed; calls that overlap on different streams need
+ * distinct workspaces. Shorter rows run the one-work-group kernel.
+ */
+int dsa_topk_workspace_bytes(int64_t rows, int64_t* bytes);
+int dsa_topk_radix_split(const float* scores, int64_t rows, int64_t columns, int64_t ld, int64_t k,
+                         float* values, int32_t* indices, int64_t out_ld, void* workspace,
+                         int64_t workspace_bytes, hipStream_t stream);
+
 
 /*
  * A8 producer - pack bf16 [tokens, 576] (512 latent + 64 RoPE) into the

@@ -59,3 +59,13 @@ def test_operators_refuse_cpu_tensors():
         indexer.quantize_index(torch.ones(2, 128, dtype=torch.bfloat16))
     with pytest.raises(ValueError, match="CUDA Q"):
         indexer.logits(torch.zeros(1, 64, 128), torch.zeros(8, 128), None, None, 7)
+
+
+def test_topk_workspace_query_without_gpu():
+    import ctypes
+
+    size = ctypes.c_int64()
+    _native.call("dsa_topk_workspace_bytes", 128, ctypes.byref(size))
+    assert size.value == 128 * 2 * 2048 * 8
+    with pytest.raises(ValueError, match="workspace query"):
+        _native.call("dsa_topk_workspace_bytes", -1, ctypes.byref(size))

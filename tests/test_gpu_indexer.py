@@ -223,6 +223,42 @@ def test_topk_bit_exact_with_causal_masks(gpu, rows, columns, k):
     torch.testing.assert_close(values, reference.values, atol=0, rtol=0)
 
 
+@pytest.mark.parametrize("rows,columns,k", [(3, 8191, 2048), (5, 8193, 2048), (7, 40001, 777),
+                                             (2, 139264, 2048), (9, 65664, 2048)])
+def test_topk_two_part_rows_equal_one_part_kernel(gpu, rows, columns, k):
+    """The split entry (two work-groups per row, merged through the workspace)
+    returns exactly what the one-work-group entry returns, call after call."""
+    from cxldsagr_amd import _native
+    from cxldsagr_amd.indexer import exact_topk
+
+    generator = torch.Generator(device="cuda").manual_seed(columns)
+    scores = torch.randn(rows, columns, device=gpu, generator=generator)
+    scores[0, ::3] = 0.5  # ties across the two halves
+    count = min(k, columns)
+    values = torch.empty(rows, count, device=gpu)
+    indices = torch.empty(rows, count, device=gpu, dtype=torch.int32)
+    with torch.cuda.device(gpu):
+        _native.call("dsa_topk_radix", _native.ptr(scores), rows, columns, scores.stride(0), k,
+                     _native.ptr(values), _native.ptr(indices), count, _native.stream_of(gpu))
+    for _ in range(3):
+        split_values, split_indices = exact_topk(scores, k)
+        assert torch.equal(split_values.view(torch.int32), values.view(torch.int32))
+        assert torch.equal(split_indices, indices)
+
+
+def test_topk_split_rejects_a_short_workspace(gpu):
+    from cxldsagr_amd import _native
+
+    scores = torch.randn(4, 9000, device=gpu)
+    values = torch.empty(4, 2048, device=gpu)
+    indices = torch.empty(4, 2048, device=gpu, dtype=torch.int32)
+    workspace = torch.zeros(1024, dtype=torch.uint8, device=gpu)
+    with pytest.raises(ValueError, match="workspace too small"):
+        _native.call("dsa_topk_radix_split", _native.ptr(scores), 4, 9000, 9000, 2048,
+                     _native.ptr(values), _native.ptr(indices), 2048, _native.ptr(workspace),
+                     workspace.numel(), _native.stream_of(gpu))
+
+
 def test_topk_misaligned_rows_stream_from_memory(gpu):
     """Rows that do not start on a 16-byte boundary take the scalar streaming path."""
     generator = torch.Generator(device="cuda").manual_seed(7)
