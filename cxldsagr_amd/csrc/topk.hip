@@ -11,19 +11,27 @@
 // the reference spells out in indexer/csrc/q1_topk_sort.cu:24-42). Selecting
 // the top `count` composite keys therefore needs no tie handling at all:
 //
-// 1. histogram of the top 11 bits over the row (global memory, 1 pass);
-// 2. second pass: keys above the threshold bucket go straight to the
-//    selected set in LDS, keys in the bucket go to an LDS refine buffer;
+// 1. the row (or its half, below) is read once into registers as radix
+//    keys; each thread's two largest keys bound the count-th largest from
+//    below, and only keys at or above that bound are histogrammed on their
+//    top 11 bits;
+// 2. a pass over the registers sends keys above the threshold bucket to the
+//    selected set in LDS and keys in the bucket to an LDS refine buffer;
 // 3. the remaining digits (11/10/11/11/10 bits) are resolved on the LDS
 //    buffer; a bucket too large for LDS (huge ties, e.g. masked rows) falls
 //    back to further histogram passes over the row;
-// 4. bitonic sort of the <= 2048 selected keys (two per thread; partners
-//    within a wave are exchanged with DPP / row-swap lane moves, only
-//    strides of 128 and more go through LDS), then values and indices are
-//    decoded from the keys.
+// 4. the <= 2048 selected keys are sorted: a counting sort into 2048 linear
+//    buckets over their own key range plus in-bucket ranks, or, when a
+//    bucket holds more than 32 keys, a bitonic network (two keys per thread;
+//    partners within a wave exchanged with DPP / row-swap lane moves, only
+//    strides of 128 and more through LDS); values and indices are decoded
+//    from the keys.
 //
-// One 1024-thread work-group per row; the row is read twice from HBM/L2 in
-// the common case.
+// One 1024-thread work-group per row, or, for rows of 8192 columns and more
+// through dsa_topk_radix_split, one per half-row: each half selects and
+// sorts its own top min(count, half) keys into a workspace and a second
+// launch merges the two sorted lists of every row (merge path), so Q rows
+// occupy 2Q compute units.
 #include "dsa_common.h"
 #include "../../include/dsa_gfx950.h"
 
