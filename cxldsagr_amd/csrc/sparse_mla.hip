@@ -319,6 +319,13 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
     const uint32_t buf_next = kv_base + (uint32_t)buf_next_i * kBufBytes;
     const uint32_t parity = (uint32_t)(it & 1);
 
+    // ---- block it + 1 -> bf16 rows (first, so that the row writes drain
+    // during the score MFMAs); block it + 3 -> the freed registers. The
+    // buffer of block it + 1 last held block it - 2, whose readers all passed
+    // the previous barrier.
+    unpack(st, buf_next);
+    fetch(st, it + 3);
+
     // ---- S^T = K Q^T: keys 16 kh .. +16 x heads of tiles 2 hh, 2 hh + 1;
     // each K operand feeds both head tiles; two accumulators per tile (even /
     // odd k-steps).
@@ -389,11 +396,6 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
     }
     if (lane == 0) lds.raise[parity][wave] = __builtin_amdgcn_ballot_w64(raise) != 0;
 
-    // ---- block it + 1 -> bf16 rows; block it + 3 -> the freed registers.
-    // The buffer of block it + 1 last held block it - 2, whose readers all
-    // passed the previous barrier.
-    unpack(st, buf_next);
-    fetch(st, it + 3);
     lds_barrier();  // P, maxima, flags and block it + 1's rows visible
 
     // ---- a raised running max: new maxima from both key halves, P again,
