@@ -36,8 +36,8 @@ PEAKS = {  # MI355X published dense peaks
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--history", type=int, default=65536)
     p.add_argument("--queries", type=int, default=128)
     p.add_argument("--seed", type=int, default=947)
@@ -54,6 +54,20 @@ def parse_args():
                         "over a pinned-host token pool; 4: long-context stress, fp8 and bf16 KV")
     p.add_argument("--users", type=int, default=16, help="config 3: users")
     return p.parse_args()
+
+
+def spin_up(torch, fn, seconds=0.2):
+    """Run fn() (untimed) for a fixed wall time before the warm-up steps: the
+    GPU needs some tens of milliseconds of load to reach its steady clock, and
+    a handful of warm-up steps alone leave the first timed steps ~8 % slow."""
+    import time
+
+    torch.cuda.synchronize()
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for _ in range(16):
+            fn()
+        torch.cuda.synchronize()
 
 
 def event_time_us(torch, fn, iters):
@@ -152,15 +166,14 @@ def main():
 
     # Intermediates for per-stage timing (same values the step produces).
     out, selection = step()
-    q8, q_scale = indexer.quantize_index(index_q)
-    w_eff = (weights * q_scale[..., 0]).contiguous()
+    q8, _, w_eff = indexer.quantize_index_folded(index_q, weights)
     keys, kscale = layer.index_keys[:tokens], layer.index_scales[:tokens]
     scores = indexer.logits(q8, keys, w_eff, kscale, history, _pad_to_stride=True)
     _, ids = indexer.exact_topk(scores, topk)
     torch.cuda.synchronize()
 
     stages = {
-        "quantize_q": lambda: indexer.quantize_index(index_q),
+        "quantize_q": lambda: indexer.quantize_index_folded(index_q, weights),
         "logits": lambda: indexer.logits(q8, keys, w_eff, kscale, history, _pad_to_stride=True),
         "topk": lambda: indexer.exact_topk(scores, topk),
         "pack_kv": lambda: attention.pack_kv_fp8(kv_new, layer.kv_cache, layer.page_table,
@@ -182,6 +195,7 @@ def main():
         print(json.dumps({"only": args.only, "us": round(us, 2), "steps": args.steps}))
         return
 
+    spin_up(torch, step)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -294,11 +308,11 @@ def bench_config4(args):
             return layer.forward(index_q, index_k_new, weights, mla_q, kv_new)
 
         out, selection = step()
+        spin_up(torch, step)
         for _ in range(args.warmup):
             step()
         layer_us = event_time_us(torch, step, args.steps)
-        q8, q_scale = indexer.quantize_index(index_q)
-        w_eff = (weights * q_scale[..., 0]).contiguous()
+        q8, _, w_eff = indexer.quantize_index_folded(index_q, weights)
         keys, kscale = layer.index_keys[:tokens], layer.index_scales[:tokens]
         scores = indexer.logits(q8, keys, w_eff, kscale, history, _pad_to_stride=True)
         ids = selection.token_ids
@@ -366,8 +380,7 @@ def bench_config3(args):
 
     def run_user(u, x, timing):
         st = state[u]
-        q8, q_scale = indexer.quantize_index(x["index_q"])
-        w_eff = (x["weights"] * q_scale[..., 0]).contiguous()
+        q8, _, w_eff = indexer.quantize_index_folded(x["index_q"], x["weights"])
         indexer.quantize_into(x["index_k"], st["keys"][history:], st["scales"][history:])
         scores = indexer.logits(q8, st["keys"], w_eff, st["scales"], history, _pad_to_stride=True)
         _, ids = indexer.exact_topk(scores, topk)

@@ -24,6 +24,8 @@ SIGNATURES = {
     "dsa_last_error": [ctypes.c_char_p, ctypes.c_size_t],
     "dsa_abi_version": [],
     "dsa_quantize_fp8_rows": [_ptr, _int, _i64, _i64, _i64, _ptr, _ptr, _int, _ptr],
+    "dsa_quantize_fp8_rows_fold": [_ptr, _int, _i64, _i64, _i64, _ptr, _ptr, _int, _ptr, _ptr,
+                                   _ptr],
     "dsa_indexer_logits_fp8": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _ptr,
                                _ptr],
     "dsa_topk_radix": [_ptr, _i64, _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr],

@@ -51,7 +51,9 @@ __device__ __forceinline__ uint32_t quantize_one(float v, float scale, float inv
 __global__ __launch_bounds__(256) void quantize_bf16_d128(const uint16_t* __restrict__ x,
                                                           int64_t rows, int64_t row_stride,
                                                           uint8_t* __restrict__ y,
-                                                          float* __restrict__ scales, int ue8m0) {
+                                                          float* __restrict__ scales, int ue8m0,
+                                                          const float* __restrict__ fold_in,
+                                                          float* __restrict__ fold_out) {
   const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;
   const int part = threadIdx.x & 15;
   const bool live = row < rows;
@@ -80,7 +82,10 @@ __global__ __launch_bounds__(256) void quantize_bf16_d128(const uint16_t* __rest
 #pragma unroll
   for (int i = 0; i < 4; ++i) hi |= quantize_one(v[4 + i], scale, inverse, ue8m0 != 0) << (8 * i);
   *reinterpret_cast<uint2*>(y + row * 128 + part * 8) = make_uint2(lo, hi);
-  if (part == 0) scales[row] = scale;
+  if (part == 0) {
+    scales[row] = scale;
+    if (fold_out) fold_out[row] = fold_in[row] * scale;
+  }
 }
 
 template <typename T>
@@ -103,7 +108,9 @@ template <typename T>
 __global__ __launch_bounds__(256) void quantize_generic(const T* __restrict__ x, int64_t rows,
                                                         int64_t dim, int64_t row_stride,
                                                         uint8_t* __restrict__ y,
-                                                        float* __restrict__ scales, int ue8m0) {
+                                                        float* __restrict__ scales, int ue8m0,
+                                                        const float* __restrict__ fold_in,
+                                                        float* __restrict__ fold_out) {
   const int64_t row = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
@@ -118,16 +125,15 @@ __global__ __launch_bounds__(256) void quantize_generic(const T* __restrict__ x,
   const float inverse = 1.0f / scale;
   for (int64_t i = lane; i < dim; i += 64)
     y[row * dim + i] = (uint8_t)quantize_one(load_as_f32<T>(src + i), scale, inverse, ue8m0 != 0);
-  if (lane == 0) scales[row] = scale;
+  if (lane == 0) {
+    scales[row] = scale;
+    if (fold_out) fold_out[row] = fold_in[row] * scale;
+  }
 }
 
-}  // namespace
-}  // namespace dsa
-
-extern "C" int dsa_quantize_fp8_rows(const void* x, int dtype, int64_t rows, int64_t dim,
-                                     int64_t row_stride, void* out_codes, float* out_scales,
-                                     int ue8m0, hipStream_t stream) {
-  using namespace dsa;
+int quantize_rows(const void* x, int dtype, int64_t rows, int64_t dim, int64_t row_stride,
+                  void* out_codes, float* out_scales, int ue8m0, const float* fold_in,
+                  float* fold_out, hipStream_t stream) {
   DSA_CHECK_ARG(rows >= 0 && dim >= 1 && row_stride >= dim, "invalid quantize shape");
   DSA_CHECK_ARG(dtype == DSA_DTYPE_BF16 || dtype == DSA_DTYPE_F16 || dtype == DSA_DTYPE_F32,
                 "quantize supports bf16, fp16 and fp32 inputs");
@@ -140,23 +146,45 @@ extern "C" int dsa_quantize_fp8_rows(const void* x, int dtype, int64_t rows, int
     const int64_t threads = rows * 16;
     const int64_t blocks = (threads + 255) / 256;
     hipLaunchKernelGGL(quantize_bf16_d128, dim3((unsigned)blocks), dim3(256), 0, stream,
-                       static_cast<const uint16_t*>(x), rows, row_stride, y, out_scales, ue8m0);
+                       static_cast<const uint16_t*>(x), rows, row_stride, y, out_scales, ue8m0,
+                       fold_in, fold_out);
   } else {
     const int64_t blocks = (rows + 3) / 4;
     if (dtype == DSA_DTYPE_BF16)
       hipLaunchKernelGGL(quantize_generic<uint16_t>, dim3((unsigned)blocks), dim3(256), 0, stream,
                          static_cast<const uint16_t*>(x), rows, dim, row_stride, y, out_scales,
-                         ue8m0);
+                         ue8m0, fold_in, fold_out);
     else if (dtype == DSA_DTYPE_F16)
       hipLaunchKernelGGL(quantize_generic<_Float16>, dim3((unsigned)blocks), dim3(256), 0, stream,
                          static_cast<const _Float16*>(x), rows, dim, row_stride, y, out_scales,
-                         ue8m0);
+                         ue8m0, fold_in, fold_out);
     else
       hipLaunchKernelGGL(quantize_generic<float>, dim3((unsigned)blocks), dim3(256), 0, stream,
-                         static_cast<const float*>(x), rows, dim, row_stride, y, out_scales, ue8m0);
+                         static_cast<const float*>(x), rows, dim, row_stride, y, out_scales, ue8m0,
+                         fold_in, fold_out);
   }
   DSA_CHECK_LAUNCH("quantize");
   return kOk;
+}
+
+}  // namespace
+}  // namespace dsa
+
+extern "C" int dsa_quantize_fp8_rows(const void* x, int dtype, int64_t rows, int64_t dim,
+                                     int64_t row_stride, void* out_codes, float* out_scales,
+                                     int ue8m0, hipStream_t stream) {
+  return dsa::quantize_rows(x, dtype, rows, dim, row_stride, out_codes, out_scales, ue8m0, nullptr,
+                            nullptr, stream);
+}
+
+extern "C" int dsa_quantize_fp8_rows_fold(const void* x, int dtype, int64_t rows, int64_t dim,
+                                          int64_t row_stride, void* out_codes, float* out_scales,
+                                          int ue8m0, const float* weights, float* weights_out,
+                                          hipStream_t stream) {
+  using namespace dsa;
+  DSA_CHECK_ARG(rows <= 0 || (weights && weights_out), "null weights");
+  return quantize_rows(x, dtype, rows, dim, row_stride, out_codes, out_scales, ue8m0, weights,
+                       weights_out, stream);
 }
 
 namespace dsa {

@@ -45,6 +45,30 @@ def quantize_index(x, scale_fmt="ue8m0"):
     ``clamp(x / scale, -448, 448)``. Accepts bf16, fp16 and fp32 in any layout
     (non-unit last-dim strides are copied first).
     """
+    data, scales, _ = _quantize(x, scale_fmt, None)
+    return data, scales
+
+
+def quantize_index_folded(x, weights, scale_fmt="ue8m0"):
+    """``quantize_index(x)`` plus the indexer weight fold in the same pass.
+
+    Returns ``(data, scales, folded)`` with ``folded = weights * scales[..., 0]``
+    computed in fp32 by the quantiser (the fold of
+    ``models/deepseek_v32/projections.py:241-244``). ``weights`` is FP32 with
+    the shape ``x.shape[:-1]``.
+    """
+    if (
+        not isinstance(weights, torch.Tensor)
+        or weights.dtype != torch.float32
+        or not isinstance(x, torch.Tensor)
+        or tuple(weights.shape) != tuple(x.shape[:-1])
+        or weights.device != x.device
+    ):
+        raise ValueError("weights must be FP32 with the shape of x without its last dimension")
+    return _quantize(x, scale_fmt, weights)
+
+
+def _quantize(x, scale_fmt, weights):
     if scale_fmt not in ("ue8m0", None):
         raise ValueError("Unsupported indexer quantization scale format")
     if not isinstance(x, torch.Tensor) or x.ndim == 0:
@@ -57,9 +81,38 @@ def quantize_index(x, scale_fmt="ue8m0"):
         raise ValueError("quantize_index needs a nonempty last dimension")
     data = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=x.device)
     scales = torch.empty((*x.shape[:-1], 1), dtype=torch.float32, device=x.device)
+    folded = None
+    if weights is not None:
+        weights = weights.contiguous()
+        folded = torch.empty_like(weights)
     rows = x.numel() // dim
     if rows == 0:
-        return data, scales
+        return data, scales, folded
+    # Rows must sit at a uniform stride with unit element stride; other
+    # layouts are copied on the device first.
+    if x.is_contiguous():
+        source, row_stride = x, dim
+    elif x.ndim == 2 and x.stride(1) == 1:
+        source, row_stride = x, x.stride(0)
+    else:
+        source, row_stride = x.contiguous(), dim
+    common = (
+        _native.ptr(source),
+        _native.DTYPE_CODES[x.dtype],
+        rows,
+        dim,
+        row_stride,
+        _native.ptr(data),
+        _native.ptr(scales),
+        1 if scale_fmt == "ue8m0" else 0,
+    )
+    with torch.cuda.device(x.device):
+        if weights is None:
+            _native.call("dsa_quantize_fp8_rows", *common, _native.stream_of(x.device))
+        else:
+            _native.call("dsa_quantize_fp8_rows_fold", *common, _native.ptr(weights),
+                         _native.ptr(folded), _native.stream_of(x.device))
+    return data, scales, folded
     # Rows must sit at a uniform stride with unit element stride; other
     # layouts are copied on the device first.
     if x.is_contiguous():

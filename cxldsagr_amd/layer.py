@@ -4,7 +4,7 @@ Follows the stage order of the reference's ``EchoAttentionRunner._forward``
 (``models/deepseek_v32/attention.py:276-425``) for the hot path:
 
 1. quantise the indexer Q (A1) and fold ``q_scale`` into the head weights
-   (``models/deepseek_v32/projections.py:241-244``; A2);
+   in the same kernel (``models/deepseek_v32/projections.py:241-244``; A2);
 2. quantise the new tokens' index K straight into the resident index cache
    (``attention.py:323-326``; A3);
 3. fp8 logits with the causal ``-inf`` tail over the aligned score storage
@@ -104,8 +104,7 @@ class DSALayer:
         end = position + rows
         if end > self.capacity:
             raise ValueError("query batch exceeds the layer capacity")
-        q8, q_scale = indexer.quantize_index(index_q)
-        weights = (weights * q_scale[..., 0]).contiguous()
+        q8, _, weights = indexer.quantize_index_folded(index_q, weights)
         indexer.quantize_into(index_k, self.index_keys[position:end],
                               self.index_scales[position:end])
         scores = indexer.logits(q8, self.index_keys[:end], weights, self.index_scales[:end],
@@ -117,18 +116,35 @@ class DSALayer:
         """Main attention: append the new KV, then sparse MLA over the selection."""
         end = position + len(q)
         self._append_kv(kv, position)
-        ids = selection.token_ids
+        return self._attend(q, selection.token_ids, end)
+
+    def _attend(self, q, ids, end):
         if self.kv_format == "fp8_paged":
             return attention.sparse_mla_fp8_paged(q, self.kv_cache, self.page_table, ids,
                                                   self.scale, n_tokens=end)
         return attention.sparse_mla(q, self.records[:end], ids, self.scale)
 
     def forward(self, index_q, index_k, weights, q, kv):
-        """Run one query batch at ``position = self.written``; returns (out, selection)."""
+        """Run one query batch at ``position = self.written``; returns (out, selection).
+
+        The stages of ``index`` then ``consume`` in one call (the KV append
+        placed after the top-k, where the runner's ``consume`` does it).
+        """
         position = self.written
-        selection = self.index(index_q, index_k, weights, position)
-        out = self.consume(q, selection, kv, position)
-        self.written = position + len(q)
+        rows = len(index_q)
+        end = position + rows
+        if end > self.capacity or len(q) != rows or len(kv) != rows or len(index_k) != rows:
+            raise ValueError("query batch exceeds the layer capacity or inputs disagree in length")
+        indexer.quantize_into(index_k, self.index_keys[position:end],
+                              self.index_scales[position:end])
+        q8, _, folded = indexer.quantize_index_folded(index_q, weights)
+        scores = indexer.logits(q8, self.index_keys[:end], folded, self.index_scales[:end],
+                                position, _pad_to_stride=end >= self.topk)
+        _, ids = indexer.exact_topk(scores, self.topk)
+        selection = TokenSelection(ids)
+        self._append_kv(kv, position)
+        out = self._attend(q, ids, end)
+        self.written = end
         return out, selection
 
 

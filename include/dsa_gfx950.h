@@ -57,6 +57,18 @@ int dsa_quantize_fp8_rows(const void* x, int dtype, int64_t rows, int64_t dim,
                           hipStream_t stream);
 
 /*
+ * A1 + A2 - the same quantisation with the q-scale folded into the indexer
+ * head weights in the same pass: weights_out[i] = weights[i] * out_scales[i]
+ * (fp32 multiply) for every row i. Rows are (query, head) pairs in order, so
+ * weights / weights_out are the contiguous f32 [queries, heads] matrices.
+ * Replaces quantize_index (quantization.py:63-88) followed by the weight fold
+ * `weights * q_scale[..., 0]` of models/deepseek_v32/projections.py:241-244.
+ */
+int dsa_quantize_fp8_rows_fold(const void* x, int dtype, int64_t rows, int64_t dim,
+                               int64_t row_stride, void* out_codes, float* out_scales, int ue8m0,
+                               const float* weights, float* weights_out, hipStream_t stream);
+
+/*
  * A4 - fp8 MQA indexer logits with the causal -inf tail.
  * Replaces the resident branch of logits(),
  * operators/deepseek_v32/indexer/echo.py:299-410 (DeepGEMM

@@ -207,6 +207,25 @@ def _topk_check(scores, k):
     return values, indices
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_quantize_with_folded_weights(gpu, dtype):
+    """The fused weight fold equals quantize_index followed by the fp32 product."""
+    from cxldsagr_amd.indexer import quantize_index, quantize_index_folded
+
+    generator = torch.Generator(device="cuda").manual_seed(31)
+    x = (torch.randn(37, 64, 128, device=gpu, generator=generator) * 3).to(dtype)
+    x[3, 5] = float("nan")
+    weights = torch.randn(37, 64, device=gpu, generator=generator)
+    data, scales = quantize_index(x)
+    fdata, fscales, folded = quantize_index_folded(x, weights)
+    assert torch.equal(fdata.view(torch.uint8), data.view(torch.uint8))
+    assert torch.equal(fscales.view(torch.int32), scales.view(torch.int32))
+    expected = weights * scales[..., 0]
+    assert torch.equal(folded.view(torch.int32), expected.view(torch.int32))
+    with pytest.raises(ValueError, match="weights must be FP32"):
+        quantize_index_folded(x, weights[:, :32])
+
+
 @pytest.mark.parametrize(
     "rows,columns,k",
     [(1, 1, 1), (3, 17, 2048), (5, 257, 32), (32, 4099, 1024), (64, 1024, 2048),
