@@ -335,7 +335,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
 #pragma unroll
       for (int e = 0; e < 2; ++e) sa[u][e] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     {
-      constexpr int kAhead = 4;
+      constexpr int kAhead = 8;  // K reads in flight (LDS latency under load)
       auto k_addr = [&](int ks) -> uint32_t { return kbase + (uint32_t)(64 * ks); };
       v4u ka[kAhead];
 #pragma unroll
@@ -436,7 +436,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
       pb[t] = as_v8bf(lds_load<v4u>(p_base + parity * 4096 + (uint32_t)(t * 64 + lane) * 16));
     const uint32_t vbase = lane_base(buf, v_lane);
     auto v_addr = [&](int m) -> uint32_t { return vbase + 32 * m; };
-    constexpr int kAhead = 3;
+    constexpr int kAhead = 4;
     v4s vlo[kAhead], vhi[kAhead];
 #pragma unroll
     for (int d = 0; d < kAhead; ++d) {
