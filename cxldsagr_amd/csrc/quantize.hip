@@ -47,14 +47,15 @@ __device__ __forceinline__ uint32_t quantize_one(float v, float scale, float inv
   return f32_to_e4m3fn(y);
 }
 
-// 16 lanes per 128-wide bf16 row; each lane owns 8 consecutive values.
-__global__ __launch_bounds__(256) void quantize_bf16_d128(const uint16_t* __restrict__ x,
-                                                          int64_t rows, int64_t row_stride,
-                                                          uint8_t* __restrict__ y,
-                                                          float* __restrict__ scales, int ue8m0,
-                                                          const float* __restrict__ fold_in,
-                                                          float* __restrict__ fold_out) {
-  const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;
+// 16 lanes per 128-wide bf16 row; each lane owns 8 consecutive values. Block
+// `block` of 256 threads covers rows 16 block .. 16 block + 15.
+__device__ __forceinline__ void quantize_rows_d128(int64_t block, const uint16_t* __restrict__ x,
+                                                   int64_t rows, int64_t row_stride,
+                                                   uint8_t* __restrict__ y,
+                                                   float* __restrict__ scales, int ue8m0,
+                                                   const float* __restrict__ fold_in,
+                                                   float* __restrict__ fold_out) {
+  const int64_t row = (block * 256 + threadIdx.x) >> 4;
   const int part = threadIdx.x & 15;
   const bool live = row < rows;
   uint4 raw = make_uint4(0, 0, 0, 0);
@@ -86,6 +87,15 @@ __global__ __launch_bounds__(256) void quantize_bf16_d128(const uint16_t* __rest
     scales[row] = scale;
     if (fold_out) fold_out[row] = fold_in[row] * scale;
   }
+}
+
+__global__ __launch_bounds__(256) void quantize_bf16_d128(const uint16_t* __restrict__ x,
+                                                          int64_t rows, int64_t row_stride,
+                                                          uint8_t* __restrict__ y,
+                                                          float* __restrict__ scales, int ue8m0,
+                                                          const float* __restrict__ fold_in,
+                                                          float* __restrict__ fold_out) {
+  quantize_rows_d128(blockIdx.x, x, rows, row_stride, y, scales, ue8m0, fold_in, fold_out);
 }
 
 template <typename T>
@@ -194,12 +204,13 @@ namespace {
 // fp8 paged record. One wave per token: lane l quantises 8 values of latent
 // tile l/16 (the A1 rule, UE8M0 scale per 128-value tile); lanes 0-7 copy the
 // 64 RoPE bf16 values.
-__global__ __launch_bounds__(256) void kv_pack_fp8(const uint16_t* __restrict__ kv,
-                                                   int64_t tokens, int64_t token_offset,
-                                                   const int32_t* __restrict__ page_table,
-                                                   int64_t pages, uint8_t* __restrict__ cache,
-                                                   int32_t* __restrict__ status) {
-  const int64_t token = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+// Tokens 4 block .. 4 block + 3, one wave each.
+__device__ __forceinline__ void pack_tokens(int64_t block, const uint16_t* __restrict__ kv,
+                                            int64_t tokens, int64_t token_offset,
+                                            const int32_t* __restrict__ page_table,
+                                            int64_t pages, uint8_t* __restrict__ cache,
+                                            int32_t* __restrict__ status) {
+  const int64_t token = block * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (token >= tokens) return;
   const int64_t logical = token_offset + token;
@@ -241,6 +252,36 @@ __global__ __launch_bounds__(256) void kv_pack_fp8(const uint16_t* __restrict__ 
         *reinterpret_cast<const uint4*>(src + 512 + lane * 8);
 }
 
+__global__ __launch_bounds__(256) void kv_pack_fp8(const uint16_t* __restrict__ kv,
+                                                   int64_t tokens, int64_t token_offset,
+                                                   const int32_t* __restrict__ page_table,
+                                                   int64_t pages, uint8_t* __restrict__ cache,
+                                                   int32_t* __restrict__ status) {
+  pack_tokens(blockIdx.x, kv, tokens, token_offset, page_table, pages, cache, status);
+}
+
+// The three small stages of a layer step in one launch: blocks [0, nq) quantise
+// the indexer Q rows and fold their scales into the head weights, blocks
+// [nq, nq + nk) quantise the new index-K rows into the resident cache, and the
+// rest pack the new KV tokens into the fp8 paged cache. All three are
+// independent of each other.
+__global__ __launch_bounds__(256) void layer_prologue(
+    const uint16_t* __restrict__ q, int64_t q_rows, const float* __restrict__ weights,
+    uint8_t* __restrict__ q_codes, float* __restrict__ q_scales, float* __restrict__ w_folded,
+    const uint16_t* __restrict__ k, int64_t k_rows, uint8_t* __restrict__ k_codes,
+    float* __restrict__ k_scales, const uint16_t* __restrict__ kv, int64_t tokens,
+    int64_t token_offset, const int32_t* __restrict__ page_table, int64_t pages,
+    uint8_t* __restrict__ cache, int32_t* __restrict__ status, int64_t nq, int64_t nk) {
+  const int64_t b = blockIdx.x;
+  if (b < nq) {
+    quantize_rows_d128(b, q, q_rows, 128, q_codes, q_scales, 1, weights, w_folded);
+  } else if (b < nq + nk) {
+    quantize_rows_d128(b - nq, k, k_rows, 128, k_codes, k_scales, 1, nullptr, nullptr);
+  } else {
+    pack_tokens(b - nq - nk, kv, tokens, token_offset, page_table, pages, cache, status);
+  }
+}
+
 }  // namespace
 }  // namespace dsa
 
@@ -259,5 +300,41 @@ extern "C" int dsa_kv_pack_fp8(const void* kv, int64_t tokens, int64_t token_off
                      static_cast<const uint16_t*>(kv), tokens, token_offset, page_table, pages,
                      static_cast<uint8_t*>(cache), status);
   DSA_CHECK_LAUNCH("fp8 KV pack");
+  return kOk;
+}
+
+extern "C" int dsa_layer_prologue_fp8(const void* q, int64_t q_rows, const float* weights,
+                                      void* q_codes, float* q_scales, float* w_folded,
+                                      const void* k, int64_t k_rows, void* k_codes,
+                                      float* k_scales, const void* kv, int64_t tokens,
+                                      int64_t token_offset, const int32_t* page_table,
+                                      int64_t pages, void* cache, int32_t* status,
+                                      hipStream_t stream) {
+  using namespace dsa;
+  DSA_CHECK_ARG(q_rows >= 0 && k_rows >= 0 && tokens >= 0 && token_offset >= 0 && pages >= 0,
+                "invalid prologue shape");
+  DSA_CHECK_ARG(token_offset + tokens <= pages * 64, "tokens exceed the paged cache");
+  DSA_CHECK_ARG((q_rows == 0 || (q && weights && q_codes && q_scales && w_folded)) &&
+                    (k_rows == 0 || (k && k_codes && k_scales)) &&
+                    (tokens == 0 || (kv && page_table && cache)),
+                "null pointer");
+  DSA_CHECK_ARG(reinterpret_cast<uintptr_t>(q) % 16 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(kv) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(cache) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(q_codes) % 8 == 0 &&
+                    reinterpret_cast<uintptr_t>(k_codes) % 8 == 0,
+                "prologue inputs must be 16-byte and code outputs 8-byte aligned");
+  const int64_t nq = (q_rows * 16 + 255) / 256;
+  const int64_t nk = (k_rows * 16 + 255) / 256;
+  const int64_t nt = (tokens + 3) / 4;
+  if (nq + nk + nt == 0) return kOk;
+  DSA_CHECK_ARG(nq + nk + nt < 0x7FFFFFFF, "prologue too large for one launch");
+  hipLaunchKernelGGL(layer_prologue, dim3((unsigned)(nq + nk + nt)), dim3(256), 0, stream,
+                     static_cast<const uint16_t*>(q), q_rows, weights,
+                     static_cast<uint8_t*>(q_codes), q_scales, w_folded,
+                     static_cast<const uint16_t*>(k), k_rows, static_cast<uint8_t*>(k_codes),
+                     k_scales, static_cast<const uint16_t*>(kv), tokens, token_offset, page_table,
+                     pages, static_cast<uint8_t*>(cache), status, nq, nk);
+  DSA_CHECK_LAUNCH("layer prologue");
   return kOk;
 }

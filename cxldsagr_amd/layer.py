@@ -21,7 +21,7 @@ stream without host synchronisation.
 
 import torch
 
-from cxldsagr_amd import attention, indexer
+from cxldsagr_amd import _native, attention, indexer
 from cxldsagr_amd.contracts import AttentionContext, TokenSelection
 
 PAGE_TOKENS = 64
@@ -118,6 +118,41 @@ class DSALayer:
         self._append_kv(kv, position)
         return self._attend(q, selection.token_ids, end)
 
+    def _fused_prologue_applies(self, index_q, index_k, weights, kv):
+        """The one-launch prologue covers the model shapes on the fp8 paged cache."""
+        rows = len(index_q)
+        return (self.kv_format == "fp8_paged" and index_q.dtype == torch.bfloat16
+                and index_q.ndim == 3 and index_q.shape[1:] == (64, 128)
+                and index_k.dtype == torch.bfloat16 and tuple(index_k.shape) == (rows, 128)
+                and weights.dtype == torch.float32 and tuple(weights.shape) == (rows, 64)
+                and kv.dtype == torch.bfloat16 and tuple(kv.shape) == (rows, attention.QK_DIM)
+                and all(t.device == self.device for t in (index_q, index_k, weights, kv)))
+
+    def _prologue(self, index_q, index_k, weights, kv, position):
+        """Q quantisation + weight fold, new index K into the cache and the new
+        KV records into the fp8 paged cache, in one launch
+        (``dsa_layer_prologue_fp8``; the same bits as the three separate
+        operators)."""
+        rows = len(index_q)
+        end = position + rows
+        index_q, index_k, weights, kv = (t.contiguous() for t in (index_q, index_k, weights, kv))
+        index_q, index_k, kv = (attention._aligned(t) for t in (index_q, index_k, kv))
+        q8 = torch.empty(index_q.shape, dtype=torch.float8_e4m3fn, device=self.device)
+        q_scales = torch.empty((*index_q.shape[:-1], 1), dtype=torch.float32, device=self.device)
+        folded = torch.empty_like(weights)
+        with torch.cuda.device(self.device):
+            _native.call(
+                "dsa_layer_prologue_fp8",
+                _native.ptr(index_q), rows * 64, _native.ptr(weights), _native.ptr(q8),
+                _native.ptr(q_scales), _native.ptr(folded),
+                _native.ptr(index_k), rows, _native.ptr(self.index_keys[position:end]),
+                _native.ptr(self.index_scales[position:end]),
+                _native.ptr(kv), rows, position, _native.ptr(self.page_table),
+                self.kv_cache.shape[0], _native.ptr(self.kv_cache), None,
+                _native.stream_of(self.device),
+            )
+        return q8, folded
+
     def _attend(self, q, ids, end):
         if self.kv_format == "fp8_paged":
             return attention.sparse_mla_fp8_paged(q, self.kv_cache, self.page_table, ids,
@@ -135,14 +170,17 @@ class DSALayer:
         end = position + rows
         if end > self.capacity or len(q) != rows or len(kv) != rows or len(index_k) != rows:
             raise ValueError("query batch exceeds the layer capacity or inputs disagree in length")
-        indexer.quantize_into(index_k, self.index_keys[position:end],
-                              self.index_scales[position:end])
-        q8, _, folded = indexer.quantize_index_folded(index_q, weights)
+        if self._fused_prologue_applies(index_q, index_k, weights, kv):
+            q8, folded = self._prologue(index_q, index_k, weights, kv, position)
+        else:
+            indexer.quantize_into(index_k, self.index_keys[position:end],
+                                  self.index_scales[position:end])
+            q8, _, folded = indexer.quantize_index_folded(index_q, weights)
+            self._append_kv(kv, position)
         scores = indexer.logits(q8, self.index_keys[:end], folded, self.index_scales[:end],
                                 position, _pad_to_stride=end >= self.topk)
         _, ids = indexer.exact_topk(scores, self.topk)
         selection = TokenSelection(ids)
-        self._append_kv(kv, position)
         out = self._attend(q, ids, end)
         self.written = end
         return out, selection

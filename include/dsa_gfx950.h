@@ -125,6 +125,23 @@ int dsa_kv_pack_fp8(const void* kv, int64_t tokens, int64_t token_offset,
                     hipStream_t stream);
 
 /*
+ * Layer-step prologue in one launch: the fold variant of the A1 quantiser on
+ * q_rows contiguous bf16 [q_rows, 128] indexer-Q rows (UE8M0; q_codes e4m3
+ * [q_rows, 128], q_scales f32 [q_rows], w_folded = weights * q_scales), the
+ * A3 quantiser on k_rows bf16 [k_rows, 128] new index-K rows into k_codes /
+ * k_scales, and dsa_kv_pack_fp8 of `tokens` new bf16 [tokens, 576] KV
+ * records. No reference counterpart as one entry: it replaces the three
+ * launches of models/deepseek_v32/projections.py:241-244 +
+ * quantization.py:63-88, attention.py:323-326 and attention.py:400-401 in a
+ * layer step. Results equal those three entry points bit for bit.
+ */
+int dsa_layer_prologue_fp8(const void* q, int64_t q_rows, const float* weights, void* q_codes,
+                           float* q_scales, float* w_folded, const void* k, int64_t k_rows,
+                           void* k_codes, float* k_scales, const void* kv, int64_t tokens,
+                           int64_t token_offset, const int32_t* page_table, int64_t pages,
+                           void* cache, int32_t* status, hipStream_t stream);
+
+/*
  * A7 - sparse MLA over flat bf16 records. Replaces sparse_mla /
  * sparse_mla_from_pool (FlashMLA flash_mla_sparse_fwd),
  * operators/deepseek_v32/attention/device_only/mla.py:156-181 and

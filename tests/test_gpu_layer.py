@@ -115,3 +115,31 @@ def test_layer_selection_is_sorted_and_causal(gpu):
         assert len(torch.unique(row)) == TOPK
         vals = scores[r, row.long()]
         assert bool((vals[:-1] >= vals[1:]).all())
+
+
+def test_fused_prologue_equals_the_separate_stages(gpu):
+    """dsa_layer_prologue_fp8 (Q quantise + weight fold, index-K quantise, KV
+    pack in one launch) writes the same bits as the three operators."""
+    from cxldsagr_amd import attention, indexer
+    from cxldsagr_amd.layer import DSALayer
+    from cxldsagr_amd.workloads import make_layer_inputs
+
+    history, queries = 1000, 77
+    inputs = make_layer_inputs(history, queries, seed=3)
+    tokens = history + queries
+    fused = DSALayer(tokens, device=gpu, kv_format="fp8_paged", page_table=inputs.page_table)
+    plain = DSALayer(tokens, device=gpu, kv_format="fp8_paged", page_table=inputs.page_table)
+    index_q, weights = inputs.index_q.to(gpu), inputs.weights.to(gpu)
+    index_k, kv = inputs.index_k[history:].to(gpu), inputs.kv[history:].to(gpu)
+    index_q[5, 7, 3] = float("nan")
+    assert fused._fused_prologue_applies(index_q, index_k, weights, kv)
+    q8, folded = fused._prologue(index_q, index_k, weights, kv, history)
+    ref_q8, _, ref_folded = indexer.quantize_index_folded(index_q, weights)
+    indexer.quantize_into(index_k, plain.index_keys[history:tokens], plain.index_scales[history:tokens])
+    attention.pack_kv_fp8(kv, plain.kv_cache, plain.page_table, token_offset=history)
+    torch.cuda.synchronize()
+    assert torch.equal(q8.view(torch.uint8), ref_q8.view(torch.uint8))
+    assert torch.equal(folded.view(torch.int32), ref_folded.view(torch.int32))
+    assert torch.equal(fused.index_keys.view(torch.uint8), plain.index_keys.view(torch.uint8))
+    assert torch.equal(fused.index_scales.view(torch.int32), plain.index_scales.view(torch.int32))
+    assert torch.equal(fused.kv_cache, plain.kv_cache)
