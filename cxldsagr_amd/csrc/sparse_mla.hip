@@ -8,45 +8,36 @@
 // a record; P = softmax(q[r,h] . rec * scale); out[r,h] = P @ rec[:512],
 // rounded to bf16; a row with no valid id is zero.
 //
-// Mapping (gfx950, wave64, v_mfma_f32_16x16x32_bf16). A work-group owns one
-// query row and 64 heads and walks the selection in blocks of 32 keys; its 4
-// waves (one per SIMD) split each block twice:
-// * Scores: wave w computes S^T = K Q^T for key half kh = w / 2 (16 keys)
-//   and head half hh = w % 2 (32 heads), keeping Q^T of its 32 heads in
-//   AGPRs (144); each K operand read from LDS feeds two MFMAs.
-// * Softmax without a max exchange in the common case: each wave computes
-//   P against the running max of its heads (known to every wave) and flags
-//   the block if any of its maxima rose by more than kRescaleThreshold. If
-//   no wave flagged it, P is final. Otherwise (the first block, and rarely
-//   later) every wave reads the other key half's block maxima after the
-//   barrier, recomputes its P against the new maxima, publishes the rescale
-//   factors, and a second barrier precedes the PV product.
-// * Values: wave w accumulates O^T for dims 128 w .. 128 w + 127 (one fp8
-//   scale tile) and all 64 heads (128 VGPRs). Each V operand feeds four MFMAs.
-// * The probabilities, block maxima and flags go through LDS, double
-//   buffered by block parity, behind the barrier of the block.
-//
-// Records travel HBM -> registers -> LDS as bf16 rows. Lane (kk, j) of wave
-// w (kk = 8w + lane / 8, j = lane % 8) loads 1/8 of key kk's record of each
-// block with 16-byte loads two blocks ahead, and in the iteration before the
-// block is scored writes it into one of three row buffers (fp8 records
-// converted with their tile scales by v_cvt_scalef32_pk_bf16_fp8; e4m3 x 2^k
-// is exact in bf16). Conversion therefore happens once per key, not once
-// per wave that reads it, and the score and value phases read plain bf16:
-// * K operand: lane (c, g) = (lane % 16, lane / 16) reads 16 bytes of key
-//   16 kh + c per k-step.
-// * V^T operand: ds_read_b64_tr_b16 - lane 4 jj + qq of a 16-lane row group
-//   addresses key 4g + jj at dims d0 + 4qq and receives dim d0 + lane % 16
-//   of keys 4g .. 4g + 3 (a second read covers keys 16 + 4g ..).
-// A buffer written in iteration b - 1 is read by the scores of block b and,
-// after that block's barrier, by its PV product, hence three buffers.
-//
-// Key order inside a block: MFMA k-index 8g + j of the PV product is key
-// 16 (j / 4) + 4g + j % 4, which is where the S^T C layout of the two key
-// halves puts them (lane (c, g) holds keys 4g + r of its half, head c).
+// Mapping (gfx950, wave64). A work-group owns one query row and 64 heads
+// and walks the selection in blocks of 32 keys with 4 waves, one per SIMD,
+// in two roles, so that the matrix work of one role runs beside the
+// conversion and LDS stores of the other (MFMA and VALU work of one wave
+// serialise on its SIMD):
+// * Score waves 0 and 1 compute S^T = K Q^T for all 32 keys and heads
+//   32 sw .. 32 sw + 31 with v_mfma_f32_32x32x16_bf16 (Q^T of their 32 heads
+//   stays in AGPRs, 144 registers), then the online softmax of their heads,
+//   writing P^T (bf16) and the per-head rescale factors to LDS.
+// * Load waves 2 and 3 stage the records: lane (kk, j) (kk = 16 (w - 2) +
+//   lane / 4, j = lane % 4) loads a quarter of key kk's record with 16-byte
+//   loads, kLookahead blocks ahead, and converts it into bf16 rows of one of
+//   three LDS buffers the step before the block is scored (fp8 records by
+//   v_cvt_scalef32_pk_bf16_fp8 with their tile scales; e4m3 x 2^k is exact in
+//   bf16). Conversion happens once per key, not once per wave that reads it.
+// * After the block's barrier all four waves accumulate O^T += V^T P^T
+//   (v_mfma_f32_16x16x32_bf16) over all 64 heads: score waves for 64 dims
+//   each, load waves for 192 each, which evens out the two roles' time per
+//   block. V^T comes from ds_read_b64_tr_b16: lane 4 jj + qq of row group g
+//   addresses key 2 jj + 8 (g & 1) + (g >> 1) (and + 16) at dims d0 + 4 qq.
+// * Row sums come out of the same MFMA pipe: wave w adds P^T of head tile w
+//   against a row of ones, so l sums exactly the bf16 P the product used.
+// A buffer written in step b - 1 is read by the scores of block b and,
+// after that block's barrier, by its PV product, hence three buffers; P and
+// the rescale factors are double buffered by block parity.
 //
 // Online softmax in log2 units with lazy rescaling (only when a block raises
-// the running max by more than 8, so p <= 2^8).
+// a head's running max by more than 8, so p <= 2^8).
+#include <type_traits>
+
 #include "dsa_common.h"
 #include "../../include/dsa_gfx950.h"
 
@@ -59,17 +50,13 @@ typedef float v2f __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
-typedef int32_t v2i __attribute__((ext_vector_type(2)));
-typedef int32_t v4i __attribute__((ext_vector_type(4)));
 typedef short v4s __attribute__((ext_vector_type(4)));
 
 constexpr int kQkDim = 576;
 constexpr int kVDim = 512;
 constexpr int kHeadsPerGroup = 64;
 constexpr int kBlock = 32;            // keys per block
-constexpr int kSteps = kQkDim / 32;   // 18 k-steps of 32 dims
 constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
 constexpr int kMaxSelected = 4096;    // rows table capacity per query row
 constexpr int kPageTokens = 64;
 constexpr float kRescaleThreshold = 8.0f;
@@ -77,32 +64,41 @@ constexpr float kRescaleThreshold = 8.0f;
 template <bool kFp8>
 struct Format {
   static constexpr int kRecordBytes = kFp8 ? 656 : kQkDim * 2;
-  // 16-byte loads per lane per block: lane (key kk, part j) of the loader
-  // fetches 1/8 of its key's record (fp8: 4 latent + scales + RoPE; bf16:
-  // 8 latent + RoPE).
-  static constexpr int kLoads = kFp8 ? 6 : 9;
+  // 16-byte loads per lane per block: the two load waves fetch 16 keys each,
+  // four lanes per key (fp8: 8 latent + scales + 2 RoPE; bf16: 16 + 2).
+  static constexpr int kLoads = kFp8 ? 11 : 18;
 };
 
 // bf16 K/V rows of one block in LDS: key r at kRowBytes r, its 576 dims in
-// order. The 32-byte pad puts consecutive rows 40 banks apart (mod 64), which
-// keeps both the K reads (16 rows x 64 contiguous bytes per half-wave) and
-// the V^T transpose reads (8 rows x 32 bytes) free of bank conflicts.
-constexpr int kRowBytes = kQkDim * 2 + 32;
+// order. 1168 bytes = 292 dwords = 36 (mod 64): the 16 keys read by a 16-lane
+// group of the score operands land on 16 distinct 4-bank groups, and the 8
+// even (or odd) keys of a V^T transpose read on disjoint 8-bank windows.
+constexpr int kRowBytes = kQkDim * 2 + 16;
 constexpr int kBufBytes = kBlock * kRowBytes;
-constexpr int kBuffers = 3;  // written in iteration b - 1, read by S in b and by PV after its barrier
+constexpr int kBuffers = 3;
+// 16-dim tiles of O^T per score wave and per load wave (two of each).
+constexpr int kScoreDimTiles = 4;
+constexpr int kLoadDimTiles = (kVDim / 16 - 2 * kScoreDimTiles) / 2;
 
 struct __align__(16) Lds {
   uint8_t kv[kBuffers][kBufBytes];
   // P^T in PV B-operand order, by block parity: [parity][head tile][lane]
-  // 16 bytes, lane (c, g) of tile t holding head 16t + c, keys 4g + r
-  // (r = 0..3) then 16 + 4g + r, bf16.
+  // 16 bytes: lane (c, g) of tile t holds head 16t + c, k-index j = key
+  // 2(j & 3) + 8(g & 1) + (g >> 1) + 16(j >> 2), bf16.
   uint8_t p[2][4][64][16];
   float alpha[2][kHeadsPerGroup];  // per-head rescale factor of the block, by parity
-  float part_max[2][2][kHeadsPerGroup];  // [parity][key half] block max of each head
-  alignas(16) int32_t raise[2][4];  // [parity][wave]: the block raised a running max
-  float row_sum[2][kHeadsPerGroup];  // [key half]
+  float row_sum[kHeadsPerGroup];
   int32_t rows[kMaxSelected];  // physical record row per selected position, -1 = padding
 };
+
+// Key order inside a block. Row m = 8a + 4h + i of the 32x32 score tile holds
+// key 2i + 8(a & 1) + h + 16(a >> 1); k-index j of the PV operands of lane
+// row-group g is key 2(j & 3) + 8(g & 1) + (g >> 1) + 16(j >> 2). With these,
+// the four results a score lane holds in registers 4a'..4a'+3 are exactly
+// the four consecutive k-indices 4(a' >> 1) .. +3 of one PV operand slot.
+__device__ __forceinline__ int score_key(int m) {
+  return 2 * (m & 3) + 8 * ((m >> 3) & 1) + ((m >> 2) & 1) + 16 * (m >> 4);
+}
 
 // Source of padding slots and invalid ids: a zero record (zero scales), so
 // that their V^T operands are zeros rather than whatever the cache holds.
@@ -120,36 +116,26 @@ __device__ __forceinline__ uint32_t dequant_pair(uint32_t word, float scale) {
   return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(word, scale, kHigh));
 }
 
-// acc += a b for the score MFMAs, with b (Q^T) pinned to AGPRs: Q^T of 32
-// heads (144 registers) and the O accumulators (128) do not both fit the 256
-// VGPRs, and as a compiler-chosen spill Q^T is copied back into an aligned
-// tuple before every use. As inline assembly the MFMA is invisible to the
-// hazard recognizer, so it covers its own wait states: the leading s_nop 1
-// gives the 2 required after a VALU write of `a` or `acc`; the reader of the
-// final accumulators waits with mfma_drain().
-__device__ __forceinline__ void mfma_qb(v4f& acc, v8bf a, v8bf b) {
-  asm volatile("s_nop 1\n\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "a"(b));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// acc += a b with the 32x32x16 bf16 MFMA, b (Q^T) pinned to AGPRs: Q^T of 32
+// heads (144 registers) does not fit the VGPRs beside the O accumulators, and
+// as a compiler-chosen spill it is copied back into an aligned tuple before
+// every use. As inline assembly the MFMA is invisible to the hazard
+// recognizer, so it covers its own wait states: the leading s_nop 1 gives the
+// 2 required after a VALU write of `a` or `acc`; back-to-back MFMAs into the
+// same accumulator need none; the reader of the final accumulator waits with
+// mfma_drain32().
+__device__ __forceinline__ void mfma32_qb(v16f& acc, v8bf a, v8bf b) {
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "a"(b));
+}
+// Wait states between the last inline-assembly MFMA and any read of its
+// results (more than the 18 a 16-pass XDL op needs). The accumulator is an
+// operand, so no read of it can be scheduled above the wait.
+__device__ __forceinline__ void mfma_drain32(v16f& a) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(a));
 }
 
-// Max over the four 16-lane rows (lanes l, l ^ 16, l ^ 32, l ^ 48) with the
-// gfx950 row-swap permutes instead of LDS-routed shuffles.
-__device__ __forceinline__ float max_across_rows(float v) {
-  const uint32_t u = __float_as_uint(v);
-  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-  const float m = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  const uint32_t w = __float_as_uint(m);
-  const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-
-// Wait states between the last inline-assembly MFMAs and any read of their
-// results (more than the 11 an 8-pass XDL op needs). The accumulators are
-// operands, so no read of them can be scheduled above the wait.
-__device__ __forceinline__ void mfma_drain(v4f& a, v4f& b, v4f& c, v4f& d) {
-  asm volatile("s_nop 7\n\ts_nop 7" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
-}
-
-typedef v2i __attribute__((address_space(3))) * lds_v2i;
 typedef v4s __attribute__((address_space(3))) * lds_v4s;
 
 template <typename T>
@@ -166,12 +152,6 @@ __device__ __forceinline__ void lds_store(uint32_t addr, T v) {
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
-
-// One block's share of a lane's record bytes, in flight or landed.
-template <bool kFp8>
-struct Staged {
-  v4u r[Format<kFp8>::kLoads];
-};
 
 template <bool kFp8>
 __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
@@ -210,79 +190,37 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
     lds.rows[i] = phys;
   }
 
-  // Score role: key half kh (keys 16 kh + c), head tiles 2 hh + u (heads
-  // 16 (2 hh + u) + c), u = 0, 1.
-  const int kh = wave >> 1;
-  const int hh = wave & 1;
-  // Q^T operands: head 16 (2 hh + u) + c, dims 32 ks + 8g .. +8.
-  v8bf qb[2][kSteps];
+  // Roles: waves 0 and 1 score (32 heads each, all 32 keys of a block, with
+  // 32x32x16 MFMAs) and run the softmax; waves 2 and 3 stage the records of
+  // the next block (HBM -> registers -> bf16 rows in LDS). All four then
+  // accumulate O^T for their share of the 512 dims over all 64 heads.
+  const bool scorer = wave < 2;
+  const int sw = wave & 1;           // score wave: heads 32 sw .. + 31
+  const int n = lane & 31;           // score lane: head 32 sw + n
+  const int h = lane >> 5;           // score lane: row half
+  // One register pool serves both roles, so that the allocator can give
+  // the two roles the same registers: Q^T operands on score waves (k-step
+  // ks: dims 16 ks + 8h), staged record bytes on load waves (fp8: two sets
+  // of kLoads at 0 and kLoads, bf16: one set).
+  constexpr int kPool = kQkDim / 16;
+  static_assert((kFp8 ? 2 : 1) * F::kLoads <= kPool, "staging does not fit the pool");
+  v4u pool[kPool];
+  if (scorer) {
+    const uint16_t* qrow = q + ((row * heads + head0 + 32 * sw + n) * kQkDim) + 8 * h;
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const uint16_t* qrow = q + ((row * heads + head0 + 16 * (2 * hh + u) + c) * kQkDim) + 8 * g;
-#pragma unroll
-    for (int ks = 0; ks < kSteps; ++ks) qb[u][ks] = as_v8bf(*reinterpret_cast<const v4u*>(qrow + 32 * ks));
+    for (int ks = 0; ks < kPool; ++ks) pool[ks] = *reinterpret_cast<const v4u*>(qrow + 16 * ks);
   }
-  // O^T: head tile t (heads 16t + c), dims 128 wave + 16m + 4g + r.
-  v4f o[4][8];
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-#pragma unroll
-    for (int m = 0; m < 8; ++m) o[t][m] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-  // Running max of heads 16 (2 hh + u) + c (the same in both key-half
-  // waves), and the row sum over this lane's keys.
-  float m_run[2] = {neg_inf, neg_inf};
-  float l_run[2] = {0.0f, 0.0f};
+  float m_run = neg_inf;  // score lane: running max of its head (scaled)
+  // Row sums of heads 16 wave + c (P^T against ones; every row alike).
+  v4f l_acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // Loader role: key kk of each block, part j of its record.
-  const int kk = 8 * wave + (lane >> 3);
-  const int j = lane & 7;
+  // Load role: key kk of each block, quarter j of its record.
+  const int kk = 16 * (wave & 1) + (lane >> 2);
+  const int j = lane & 3;
   const uint32_t rows_base = (uint32_t)(uintptr_t)&lds.rows[0];
   const uint32_t kv_base = (uint32_t)(uintptr_t)&lds.kv[0][0];
   const uint32_t p_base = (uint32_t)(uintptr_t)&lds.p[0][0][0][0];
 
-  // Block b's record bytes of this lane -> registers. Blocks past the end
-  // (and invalid ids) read the zero record, so the load count per block is
-  // fixed.
-  auto fetch = [&](Staged<kFp8>& st, int b) {
-    const int32_t phys = b < n_blocks ? lds_load<int32_t>(rows_base + 4 * (uint32_t)(b * kBlock + kk)) : -1;
-    const uint8_t* rec = phys >= 0 ? kv + (int64_t)phys * F::kRecordBytes : zero_record;
-    if (kFp8) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) st.r[i] = *reinterpret_cast<const v4u*>(rec + 128 * i + 16 * j);
-      st.r[4] = *reinterpret_cast<const v4u*>(rec + kVDim);
-      st.r[5] = *reinterpret_cast<const v4u*>(rec + kVDim + 16 + 16 * j);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) st.r[i] = *reinterpret_cast<const v4u*>(rec + 128 * i + 16 * j);
-      st.r[8] = *reinterpret_cast<const v4u*>(rec + 2 * kVDim + 16 * j);
-    }
-  };
-  // Landed record bytes -> bf16 rows of a block buffer (fp8: e4m3 x tile
-  // scale, exact in bf16).
-  auto unpack = [&](const Staged<kFp8>& st, uint32_t buf) {
-    const uint32_t rec = buf + (uint32_t)kk * kRowBytes;
-    if (kFp8) {
-      const v4f sc = __builtin_bit_cast(v4f, st.r[4]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const v4u w = st.r[i];
-        const v4u lo{dequant_pair<false>(w.x, sc[i]), dequant_pair<true>(w.x, sc[i]),
-                     dequant_pair<false>(w.y, sc[i]), dequant_pair<true>(w.y, sc[i])};
-        const v4u hi{dequant_pair<false>(w.z, sc[i]), dequant_pair<true>(w.z, sc[i]),
-                     dequant_pair<false>(w.w, sc[i]), dequant_pair<true>(w.w, sc[i])};
-        lds_store<v4u>(rec + 256 * i + 32 * j, lo);
-        lds_store<v4u>(rec + 256 * i + 32 * j + 16, hi);
-      }
-      lds_store<v4u>(rec + 2 * kVDim + 16 * j, st.r[5]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) lds_store<v4u>(rec + 128 * i + 16 * j, st.r[i]);
-      lds_store<v4u>(rec + 2 * kVDim + 16 * j, st.r[8]);
-    }
-  };
-
-  // K operand of k-step ks for key 16 kh + c: dims 32 ks + 8g .. +8.
-  const uint32_t k_lane = (uint32_t)(16 * kh + c) * kRowBytes + 16 * g;
   // Per-block base addresses are formed once and hidden from the optimizer:
   // otherwise it hoists (lane offset + constant) out of the loop and pays an
   // add per LDS access instead of using the instruction's offset field.
@@ -291,149 +229,194 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
     asm volatile("" : "+v"(a));
     return a;
   };
+  // Block b's record bytes of this lane -> registers. Blocks past the end
+  // (and invalid ids) read the zero record, so the load count per block is
+  // fixed. fp8 latent loads i cover record bytes 64i + 16j (64 contiguous
+  // bytes per key and instruction); bf16 loads 2i + u cover 128i + 32j + 16u.
+  auto fetch = [&](auto set, int b) __attribute__((always_inline)) {
+    v4u* st = pool + decltype(set)::value;
+    const int32_t phys = b < n_blocks ? lds_load<int32_t>(rows_base + 4 * (uint32_t)(b * kBlock + kk)) : -1;
+    const uint8_t* rec = phys >= 0 ? kv + (int64_t)phys * F::kRecordBytes : zero_record;
+    if (kFp8) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) st[i] = *reinterpret_cast<const v4u*>(rec + 64 * i + 16 * j);
+      st[8] = *reinterpret_cast<const v4u*>(rec + kVDim);
+      st[9] = *reinterpret_cast<const v4u*>(rec + kVDim + 16 + 32 * j);
+      st[10] = *reinterpret_cast<const v4u*>(rec + kVDim + 32 + 32 * j);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        st[i] = *reinterpret_cast<const v4u*>(rec + 128 * (i >> 1) + 32 * j + 16 * (i & 1));
+      st[16] = *reinterpret_cast<const v4u*>(rec + 2 * kVDim + 32 * j);
+      st[17] = *reinterpret_cast<const v4u*>(rec + 2 * kVDim + 16 + 32 * j);
+    }
+  };
+  // Landed record bytes -> bf16 rows of a block buffer (fp8: e4m3 x tile
+  // scale, exact in bf16).
+  auto unpack = [&](auto set, uint32_t buf) __attribute__((always_inline)) {
+    const v4u* st = pool + decltype(set)::value;
+    const uint32_t rec = lane_base(buf, (uint32_t)kk * kRowBytes + 32 * j);
+    if (kFp8) {
+      const v4f sc = __builtin_bit_cast(v4f, st[8]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float s_i = sc[i >> 1];
+        const v4u w = st[i];
+        const v4u lo{dequant_pair<false>(w.x, s_i), dequant_pair<true>(w.x, s_i),
+                     dequant_pair<false>(w.y, s_i), dequant_pair<true>(w.y, s_i)};
+        const v4u hi{dequant_pair<false>(w.z, s_i), dequant_pair<true>(w.z, s_i),
+                     dequant_pair<false>(w.w, s_i), dequant_pair<true>(w.w, s_i)};
+        lds_store<v4u>(rec + 128 * i, lo);
+        lds_store<v4u>(rec + 128 * i + 16, hi);
+      }
+      lds_store<v4u>(rec + 2 * kVDim, st[9]);
+      lds_store<v4u>(rec + 2 * kVDim + 16, st[10]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) lds_store<v4u>(rec + 128 * (i >> 1) + 16 * (i & 1), st[i]);
+      lds_store<v4u>(rec + 2 * kVDim, st[16]);
+      lds_store<v4u>(rec + 2 * kVDim + 16, st[17]);
+    }
+  };
+
+  // Score A operand (K): lane l reads key score_key(l % 32), dims 16 ks + 8h.
+  const uint32_t k_lane = (uint32_t)score_key(n) * kRowBytes + 16 * h;
+  // O^T dims of the wave: score waves take fewer (they also run S and the
+  // softmax), so that both roles spend about the same time per block.
+  const int dim0 = scorer ? 16 * kScoreDimTiles * sw : 16 * (2 * kScoreDimTiles + kLoadDimTiles * (wave & 1));
   // V^T rows (ds_read_b64_tr_b16): lane 4 jj + qq of row group g addresses
-  // key vrow = 4g + jj (and 16 + vrow) at dims 128 wave + 16m + 4qq.
+  // key 2 jj + 8 (g & 1) + (g >> 1) (and + 16) at dims dim0 + 16m + 4qq.
   const int jj = c >> 2;
   const int qq = c & 3;
-  const int vrow = 4 * g + jj;
-  const uint32_t v_lane = (uint32_t)vrow * kRowBytes + 256 * wave + 8 * qq;
+  const int vkey = 2 * jj + 8 * (g & 1) + (g >> 1);
+  const uint32_t v_lane = (uint32_t)vkey * kRowBytes + 2 * dim0 + 8 * qq;
   constexpr uint32_t kHalf = 16 * kRowBytes;
 
-  // Prologue: blocks 0 and 1 in flight, block 0 unpacked, block 2 in flight.
-  Staged<kFp8> st0, st1;
+  // Record loads run kLookahead blocks ahead of the block being scored: two
+  // register sets for fp8 (blocks it + 2 and it + 3 in flight), one for the
+  // bf16 record, whose two sets would not fit beside O^T.
+  constexpr int kLookahead = kFp8 ? 3 : 2;
+  using Set0 = std::integral_constant<int, 0>;
+  using Set1 = std::integral_constant<int, kFp8 ? F::kLoads : 0>;
   __syncthreads();  // rows table
-  fetch(st0, 0);
-  fetch(st1, 1);
-  unpack(st0, kv_base);
-  fetch(st0, 2);
+  if (!scorer) {
+    fetch(Set0{}, 0);
+    if (kFp8) fetch(Set1{}, 1);
+    unpack(Set0{}, kv_base);
+    fetch(Set0{}, kLookahead - 1);
+  }
   lds_barrier();
 
   int buf_cur = 0;  // buffer of block it
-  // One block: scores, softmax and P of block it; unpack of block it + 1
-  // (landed two iterations ago in `st`) and refetch of block it + 3 into it;
-  // the barrier; then PV of block it.
-  auto step = [&](int it, Staged<kFp8>& st) {
+  // kScore is the wave's role, a compile-time constant of each of the two
+  // loops below: with one loop per role the wait-count pass sees only that
+  // role's loads and waits for exactly the set being unpacked.
+  auto step = [&](int it, auto set, auto role, auto& o) __attribute__((always_inline)) {
+    constexpr bool kScore = decltype(role)::value;
+    constexpr int kM = kScore ? kScoreDimTiles : kLoadDimTiles;
     const uint32_t buf = kv_base + (uint32_t)buf_cur * kBufBytes;
-    const uint32_t kbase = lane_base(buf, k_lane);
     const int buf_next_i = buf_cur + 1 == kBuffers ? 0 : buf_cur + 1;
-    const uint32_t buf_next = kv_base + (uint32_t)buf_next_i * kBufBytes;
     const uint32_t parity = (uint32_t)(it & 1);
 
-    // ---- block it + 1 -> bf16 rows (first, so that the row writes drain
-    // during the score MFMAs); block it + 3 -> the freed registers. The
-    // buffer of block it + 1 last held block it - 2, whose readers all passed
-    // the previous barrier.
-    unpack(st, buf_next);
-    fetch(st, it + 3);
-
-    // ---- S^T = K Q^T: keys 16 kh .. +16 x heads of tiles 2 hh, 2 hh + 1;
-    // each K operand feeds both head tiles; two accumulators per tile (even /
-    // odd k-steps).
-    v4f sa[2][2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-      for (int e = 0; e < 2; ++e) sa[u][e] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    {
-      constexpr int kAhead = 8;  // K reads in flight (LDS latency under load)
-      auto k_addr = [&](int ks) -> uint32_t { return kbase + (uint32_t)(64 * ks); };
+    if constexpr (kScore) {
+      // ---- S^T = K Q^T: 32 keys x heads 32 sw .. + 31, 36 k-steps of 16
+      // dims accumulated back to back.
+      v16f sa = {};
+      const uint32_t kbase = lane_base(buf, k_lane);
+      constexpr int kAhead = 8;
       v4u ka[kAhead];
 #pragma unroll
-      for (int d = 0; d < kAhead; ++d) ka[d] = lds_load<v4u>(k_addr(d));
+      for (int d = 0; d < kAhead; ++d) ka[d] = lds_load<v4u>(kbase + 32 * d);
 #pragma unroll
-      for (int ks = 0; ks < kSteps; ++ks) {
+      for (int ks = 0; ks < kQkDim / 16; ++ks) {
         const v8bf a = as_v8bf(ka[ks % kAhead]);
-        if (ks + kAhead < kSteps) ka[ks % kAhead] = lds_load<v4u>(k_addr(ks + kAhead));
-        mfma_qb(sa[0][ks & 1], a, qb[0][ks]);
-        mfma_qb(sa[1][ks & 1], a, qb[1][ks]);
+        if (ks + kAhead < kQkDim / 16) ka[ks % kAhead] = lds_load<v4u>(kbase + 32 * (ks + kAhead));
+        mfma32_qb(sa, a, as_v8bf(pool[ks]));
       }
-    }
+      // Valid keys of the block (bit = key).
+      const int32_t prow = lds_load<int32_t>(rows_base + 4 * (uint32_t)(it * kBlock + n));
+      const uint32_t vmask = (uint32_t)__builtin_amdgcn_ballot_w64(h == 0 && prow >= 0);
+      mfma_drain32(sa);
 
-    // Operands of the softmax, issued before the MFMA results are read.
-    const v4i valid = lds_load<v4i>(rows_base + 4 * (uint32_t)(it * kBlock + 16 * kh + 4 * g));
-    mfma_drain(sa[0][0], sa[0][1], sa[1][0], sa[1][1]);
-
-    // ---- softmax, speculatively against the running max: lane (c, g) holds
-    // keys 16 kh + 4g + r of heads 16 (2 hh + u) + c. If no wave sees a block
-    // max above its running max + kRescaleThreshold, the running maxima stand
-    // and P is final; otherwise every wave redoes its part after the barrier.
-    float x[2][4];
-    float mx[2];
-    bool raise = false;
+      // ---- online softmax of head 32 sw + n over the block: this lane holds
+      // keys score_key(8(r / 4) + 4h + r % 4), the other half (lane ^ 32)
+      // the rest. Maxima are taken on raw scores (scale_log2 > 0) and invalid
+      // keys become -inf, so p = exp2(s * scale_log2 - m) is one FMA and one
+      // exp2. Row sums are not formed here: the PV product adds P^T against a
+      // row of ones (the same bf16 P, so O / l is a weighted mean of V).
+      float sc[16];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const v4f sum = sa[u][0] + sa[u][1];
-      mx[u] = neg_inf;
+      for (int r = 0; r < 16; ++r) sc[r] = sa[r];
+      if (vmask != 0xFFFFFFFFu) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        x[u][r] = valid[r] >= 0 ? sum[r] * scale_log2 : neg_inf;
-        mx[u] = fmaxf(mx[u], x[u][r]);
-      }
-      mx[u] = max_across_rows(mx[u]);
-      raise |= mx[u] > m_run[u] + kRescaleThreshold || (m_run[u] == neg_inf && mx[u] != neg_inf);
-    }
-    const uint32_t p_own = p_base + parity * 4096 + (uint32_t)((2 * hh) * 64 + lane) * 16 + 8 * kh;
-    float block_sum[2];
-    auto write_p = [&](const float (&mref)[2]) {
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        float pu[4];
-        block_sum[u] = 0.0f;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          // exp2(-inf) = 0 covers invalid keys; a head with no valid key yet
-          // has p = 0.
-          pu[r] = mref[u] == neg_inf ? 0.0f : __builtin_amdgcn_exp2f(x[u][r] - mref[u]);
-          block_sum[u] += pu[r];
+        for (int r = 0; r < 16; ++r) {
+          const int key = score_key(8 * (r >> 2) + 4 * h + (r & 3));
+          sc[r] = (vmask >> key) & 1u ? sc[r] : neg_inf;
         }
-        lds_store<v2u>(p_own + (uint32_t)u * 1024, v2u{pack_bf16(pu[0], pu[1]), pack_bf16(pu[2], pu[3])});
       }
-    };
-    write_p(m_run);
-    if (g == 0) {
-      lds.part_max[parity][kh][16 * (2 * hh) + c] = mx[0];
-      lds.part_max[parity][kh][16 * (2 * hh + 1) + c] = mx[1];
+      float mx = fmaxf(fmaxf(sc[0], sc[1]), sc[2]);
+#pragma unroll
+      for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, sc[r]), sc[r + 1]);
+      mx = fmaxf(mx, sc[15]);
+      {
+        const uint32_t u = __float_as_uint(mx);
+        const auto sw32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        mx = fmaxf(__uint_as_float(sw32[0]), __uint_as_float(sw32[1])) * scale_log2;
+      }
+      const bool need = mx > m_run + kRescaleThreshold || (m_run == neg_inf && mx != neg_inf);
+      const float m_new = need ? fmaxf(m_run, mx) : m_run;
+      // exp2(-inf) = 0 covers the first valid block.
+      const float alpha = need ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+      m_run = m_new;
+      // With no valid key so far every score is -inf and p = exp2(-inf) = 0.
+      const float neg_m = m_run == neg_inf ? 0.0f : -m_run;
+      uint32_t pk[8];
+#pragma unroll
+      for (int r = 0; r < 16; r += 2)
+        pk[r / 2] = pack_bf16(__builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], scale_log2, neg_m)),
+                              __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r + 1], scale_log2, neg_m)));
+      if (h == 0) lds.alpha[parity][32 * sw + n] = alpha;
+      // P^T -> LDS: registers 4a' .. 4a' + 3 are k-indices 4(a' >> 1) .. +3 of
+      // operand slot (c = n % 16, g = 2h + (a' & 1)) of head tile 2 sw + n / 16.
+      const uint32_t p_tile = p_base + parity * 4096 + (uint32_t)((2 * sw + (n >> 4)) * 64 + (n & 15)) * 16;
+#pragma unroll
+      for (int ap = 0; ap < 4; ++ap) {
+        const int gg = 2 * h + (ap & 1);
+        lds_store<v2u>(p_tile + (uint32_t)gg * 256 + 8 * (ap >> 1), v2u{pk[2 * ap], pk[2 * ap + 1]});
+      }
+    } else {
+      // ---- block it + 1 -> bf16 rows (its buffer last held block it - 2,
+      // whose readers all passed the previous barrier); block
+      // it + kLookahead -> the freed registers.
+      unpack(set, kv_base + (uint32_t)buf_next_i * kBufBytes);
+      fetch(set, it + kLookahead);
     }
-    if (lane == 0) lds.raise[parity][wave] = __builtin_amdgcn_ballot_w64(raise) != 0;
+    lds_barrier();  // P, alpha and block it + 1's rows visible
 
-    lds_barrier();  // P, maxima, flags and block it + 1's rows visible
-
-    // ---- a raised running max: new maxima from both key halves, P again,
-    // and the rescale factors of all 64 heads before the PV product.
-    const v4i raised = lds_load<v4i>((uint32_t)(uintptr_t)&lds.raise[parity][0]);
-    if ((raised.x | raised.y | raised.z | raised.w) != 0) {
-      float m_new[2], alpha[2];
+    // ---- O^T += V^T P^T for dims dim0 .. dim0 + 16 kM - 1, all 64 heads.
+    float al[4];
+    bool rescale = false;
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const float other = lds.part_max[parity][kh ^ 1][16 * (2 * hh + u) + c];
-        m_new[u] = fmaxf(m_run[u], fmaxf(mx[u], other));
-        // exp2(-inf) = 0 also covers the first block with a valid key.
-        alpha[u] = m_new[u] == neg_inf ? 1.0f : __builtin_amdgcn_exp2f(m_run[u] - m_new[u]);
-        m_run[u] = m_new[u];
-        l_run[u] *= alpha[u];
-      }
-      write_p(m_run);
-      if (kh == 0 && g == 0) {
-        lds.alpha[parity][16 * (2 * hh) + c] = alpha[0];
-        lds.alpha[parity][16 * (2 * hh + 1) + c] = alpha[1];
-      }
-      lds_barrier();
-      float al[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) al[t] = lds.alpha[parity][16 * t + c];
+    for (int t = 0; t < 4; ++t) {
+      al[t] = lds.alpha[parity][16 * t + c];
+      rescale |= al[t] != 1.0f;
+    }
+    if (__builtin_amdgcn_ballot_w64(rescale)) {
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int m = 0; m < 8; ++m) o[t][m] *= al[t];
+        for (int m = 0; m < kM; ++m) o[t][m] *= al[t];
+      l_acc *= lds.alpha[parity][16 * wave + c];
     }
-    l_run[0] += block_sum[0];
-    l_run[1] += block_sum[1];
-
-    // ---- O^T += V^T P^T for dims 128 wave + (0..127), all 64 heads.
     v8bf pb[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
       pb[t] = as_v8bf(lds_load<v4u>(p_base + parity * 4096 + (uint32_t)(t * 64 + lane) * 16));
+    {
+      const v8bf p_own = as_v8bf(lds_load<v4u>(p_base + parity * 4096 + (uint32_t)(wave * 64 + lane) * 16));
+      const v4u ones = v4u{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+      l_acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(ones), p_own, l_acc, 0, 0, 0);
+    }
     const uint32_t vbase = lane_base(buf, v_lane);
     auto v_addr = [&](int m) -> uint32_t { return vbase + 32 * m; };
     constexpr int kAhead = 4;
@@ -444,10 +427,10 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
       vhi[d] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)(v_addr(d) + kHalf));
     }
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
+    for (int m = 0; m < kM; ++m) {
       const v8bf a = __builtin_bit_cast(
           v8bf, __builtin_shufflevector(vlo[m % kAhead], vhi[m % kAhead], 0, 1, 2, 3, 4, 5, 6, 7));
-      if (m + kAhead < 8) {
+      if (m + kAhead < kM) {
         vlo[m % kAhead] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)v_addr(m + kAhead));
         vhi[m % kAhead] =
             __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)(v_addr(m + kAhead) + kHalf));
@@ -458,35 +441,40 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
     buf_cur = buf_next_i;
   };
   // Two blocks per trip so that each register set stays a fixed register set.
-  for (int it = 0; it < n_blocks; it += 2) {
-    step(it, st1);
-    step(it + 1, st0);
-  }
-  // The fetches past the last block are never read; let them land before
-  // the registers are released.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  auto run = [&](auto role) __attribute__((always_inline)) {
+    constexpr int kM = decltype(role)::value ? kScoreDimTiles : kLoadDimTiles;
+    // O^T: head tile t (heads 16t + c), dims dim0 + 16m + 4g + r.
+    v4f o[4][kM];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int m = 0; m < kM; ++m) o[t][m] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int it = 0; it < n_blocks; it += 2) {
+      step(it, Set1{}, role, o);
+      step(it + 1, Set0{}, role, o);
+    }
+    // The fetches past the last block are never read; let them land before
+    // the registers are released.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  // ---- row sums of all 64 heads (both key halves), then O / l.
+    // ---- row sums of all 64 heads, then O / l.
+    if (g == 0) lds.row_sum[16 * wave + c] = l_acc[0];
+    __syncthreads();
+    uint16_t* obase = out + ((row * heads + head0 + c) * kVDim) + dim0 + 4 * g;
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    float l = l_run[u];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
-    if (g == 0) lds.row_sum[kh][16 * (2 * hh + u) + c] = l;
-  }
-  __syncthreads();
-  uint16_t* obase = out + ((row * heads + head0 + c) * kVDim) + 128 * wave + 4 * g;
+    for (int t = 0; t < 4; ++t) {
+      const float lt = lds.row_sum[16 * t + c];
+      const float inv_l = lt > 0.0f ? 1.0f / lt : 0.0f;
+      uint16_t* orow = obase + (int64_t)16 * t * kVDim;
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const float lt = lds.row_sum[0][16 * t + c] + lds.row_sum[1][16 * t + c];
-    const float inv_l = lt > 0.0f ? 1.0f / lt : 0.0f;
-    uint16_t* orow = obase + (int64_t)16 * t * kVDim;
-#pragma unroll
-    for (int m = 0; m < 8; ++m)
-      *reinterpret_cast<uint2*>(orow + 16 * m) =
-          make_uint2(pack_bf16(o[t][m][0] * inv_l, o[t][m][1] * inv_l),
-                     pack_bf16(o[t][m][2] * inv_l, o[t][m][3] * inv_l));
-  }
+      for (int m = 0; m < kM; ++m)
+        *reinterpret_cast<uint2*>(orow + 16 * m) =
+            make_uint2(pack_bf16(o[t][m][0] * inv_l, o[t][m][1] * inv_l),
+                       pack_bf16(o[t][m][2] * inv_l, o[t][m][3] * inv_l));
+    }
+  };
+  if (scorer) run(std::true_type{});
+  else run(std::false_type{});
 }
 
 template <bool kFp8>
