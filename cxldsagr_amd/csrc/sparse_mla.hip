@@ -24,8 +24,8 @@
 //   v_cvt_scalef32_pk_bf16_fp8 with their tile scales; e4m3 x 2^k is exact in
 //   bf16). Conversion happens once per key, not once per wave that reads it.
 // * After the block's barrier all four waves accumulate O^T += V^T P^T
-//   (v_mfma_f32_16x16x32_bf16) over all 64 heads: score waves for 64 dims
-//   each, load waves for 192 each, which evens out the two roles' time per
+//   (v_mfma_f32_16x16x32_bf16) over all 64 heads: score waves for 48 dims
+//   each, load waves for 208 each, which evens out the two roles' time per
 //   block. V^T comes from ds_read_b64_tr_b16: lane 4 jj + qq of row group g
 //   addresses key 2 jj + 8 (g & 1) + (g >> 1) (and + 16) at dims d0 + 4 qq.
 // * Row sums come out of the same MFMA pipe: wave w adds P^T of head tile w
@@ -77,7 +77,7 @@ constexpr int kRowBytes = kQkDim * 2 + 16;
 constexpr int kBufBytes = kBlock * kRowBytes;
 constexpr int kBuffers = 3;
 // 16-dim tiles of O^T per score wave and per load wave (two of each).
-constexpr int kScoreDimTiles = 4;
+constexpr int kScoreDimTiles = 3;
 constexpr int kLoadDimTiles = (kVDim / 16 - 2 * kScoreDimTiles) / 2;
 
 struct __align__(16) Lds {
@@ -173,8 +173,9 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
   // takes two per trip; a padding block has no valid key and adds nothing).
   const int n_blocks = (int)((topk + 2 * kBlock - 1) / (2 * kBlock)) * 2;
 
-  // Physical rows of every selected position.
-  for (int i = threadIdx.x; i < n_blocks * kBlock; i += kThreads) {
+  // Physical record row of selected position i; -1 for padding, an id
+  // outside [0, n_tokens) or a page outside the cache.
+  auto phys_of = [&](int i) -> int32_t {
     int32_t phys = -1;
     if (i < topk) {
       const int64_t id = ids[i];
@@ -187,8 +188,8 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
         }
       }
     }
-    lds.rows[i] = phys;
-  }
+    return phys;
+  };
 
   // Roles: waves 0 and 1 score (32 heads each, all 32 keys of a block, with
   // 32x32x16 MFMAs) and run the softmax; waves 2 and 3 stage the records of
@@ -233,9 +234,11 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
   // (and invalid ids) read the zero record, so the load count per block is
   // fixed. fp8 latent loads i cover record bytes 64i + 16j (64 contiguous
   // bytes per key and instruction); bf16 loads 2i + u cover 128i + 32j + 16u.
-  auto fetch = [&](auto set, int b) __attribute__((always_inline)) {
+  auto row_of = [&](int b) -> int32_t {
+    return b < n_blocks ? lds_load<int32_t>(rows_base + 4 * (uint32_t)(b * kBlock + kk)) : -1;
+  };
+  auto fetch = [&](auto set, int32_t phys) __attribute__((always_inline)) {
     v4u* st = pool + decltype(set)::value;
-    const int32_t phys = b < n_blocks ? lds_load<int32_t>(rows_base + 4 * (uint32_t)(b * kBlock + kk)) : -1;
     const uint8_t* rec = phys >= 0 ? kv + (int64_t)phys * F::kRecordBytes : zero_record;
     if (kFp8) {
 #pragma unroll
@@ -298,12 +301,18 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
   constexpr int kLookahead = kFp8 ? 3 : 2;
   using Set0 = std::integral_constant<int, 0>;
   using Set1 = std::integral_constant<int, kFp8 ? F::kLoads : 0>;
+  // Prologue: the rows table of all positions, blocks 0 .. kLookahead - 1
+  // requested and block 0 converted. In the loop the row of the next block
+  // to fetch is read from the table one step ahead.
+  for (int i = threadIdx.x; i < n_blocks * kBlock; i += kThreads) lds.rows[i] = phys_of(i);
   __syncthreads();  // rows table
+  int32_t phys_next = -1;
   if (!scorer) {
-    fetch(Set0{}, 0);
-    if (kFp8) fetch(Set1{}, 1);
+    fetch(Set0{}, row_of(0));
+    if (kFp8) fetch(Set1{}, row_of(1));
     unpack(Set0{}, kv_base);
-    fetch(Set0{}, kLookahead - 1);
+    fetch(Set0{}, row_of(kLookahead - 1));
+    phys_next = row_of(kLookahead);
   }
   lds_barrier();
 
@@ -311,7 +320,16 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
   // kScore is the wave's role, a compile-time constant of each of the two
   // loops below: with one loop per role the wait-count pass sees only that
   // role's loads and waits for exactly the set being unpacked.
-  auto step = [&](int it, auto set, auto role, auto& o) __attribute__((always_inline)) {
+  // ka: the first kAheadK K operands of block it, read before the step (in
+  // the previous step's PV phase: block it + 1's rows are complete once
+  // block it's barrier has passed).
+  constexpr int kAheadK = 6;
+  auto k_prefetch = [&](v4u (&ka)[kAheadK], uint32_t buf) __attribute__((always_inline)) {
+    const uint32_t kbase = lane_base(buf, k_lane);
+#pragma unroll
+    for (int d = 0; d < kAheadK; ++d) ka[d] = lds_load<v4u>(kbase + 32 * d);
+  };
+  auto step = [&](int it, auto set, auto role, auto& o, v4u (&ka)[kAheadK]) __attribute__((always_inline)) {
     constexpr bool kScore = decltype(role)::value;
     constexpr int kM = kScore ? kScoreDimTiles : kLoadDimTiles;
     const uint32_t buf = kv_base + (uint32_t)buf_cur * kBufBytes;
@@ -321,20 +339,16 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
     if constexpr (kScore) {
       // ---- S^T = K Q^T: 32 keys x heads 32 sw .. + 31, 36 k-steps of 16
       // dims accumulated back to back.
+      // Valid keys of the block (bit = key), read ahead of the MFMAs.
+      const int32_t prow = lds_load<int32_t>(rows_base + 4 * (uint32_t)(it * kBlock + n));
       v16f sa = {};
       const uint32_t kbase = lane_base(buf, k_lane);
-      constexpr int kAhead = 8;
-      v4u ka[kAhead];
-#pragma unroll
-      for (int d = 0; d < kAhead; ++d) ka[d] = lds_load<v4u>(kbase + 32 * d);
 #pragma unroll
       for (int ks = 0; ks < kQkDim / 16; ++ks) {
-        const v8bf a = as_v8bf(ka[ks % kAhead]);
-        if (ks + kAhead < kQkDim / 16) ka[ks % kAhead] = lds_load<v4u>(kbase + 32 * (ks + kAhead));
+        const v8bf a = as_v8bf(ka[ks % kAheadK]);
+        if (ks + kAheadK < kQkDim / 16) ka[ks % kAheadK] = lds_load<v4u>(kbase + 32 * (ks + kAheadK));
         mfma32_qb(sa, a, as_v8bf(pool[ks]));
       }
-      // Valid keys of the block (bit = key).
-      const int32_t prow = lds_load<int32_t>(rows_base + 4 * (uint32_t)(it * kBlock + n));
       const uint32_t vmask = (uint32_t)__builtin_amdgcn_ballot_w64(h == 0 && prow >= 0);
       mfma_drain32(sa);
 
@@ -389,18 +403,38 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
       // whose readers all passed the previous barrier); block
       // it + kLookahead -> the freed registers.
       unpack(set, kv_base + (uint32_t)buf_next_i * kBufBytes);
-      fetch(set, it + kLookahead);
+      fetch(set, phys_next);
+      phys_next = row_of(it + kLookahead + 1);
+    }
+    // The first V^T operands of this block (its rows are complete since the
+    // previous barrier) are read before the barrier.
+    const uint32_t vbase = lane_base(buf, v_lane);
+    auto v_addr = [&](int m) -> uint32_t { return vbase + 32 * m; };
+    constexpr int kAhead = 2;
+    v4s vlo[kAhead], vhi[kAhead];
+#pragma unroll
+    for (int d = 0; d < kAhead; ++d) {
+      vlo[d] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)v_addr(d));
+      vhi[d] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)(v_addr(d) + kHalf));
     }
     lds_barrier();  // P, alpha and block it + 1's rows visible
 
     // ---- O^T += V^T P^T for dims dim0 .. dim0 + 16 kM - 1, all 64 heads.
+    // Reads first (rescale factors, P^T, then the score waves' first K
+    // operands of block it + 1), then the rescale of O^T if any head's
+    // running max rose.
     float al[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) al[t] = lds.alpha[parity][16 * t + c];
+    v8bf pb[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      pb[t] = as_v8bf(lds_load<v4u>(p_base + parity * 4096 + (uint32_t)(t * 64 + lane) * 16));
+    const v8bf p_own = as_v8bf(lds_load<v4u>(p_base + parity * 4096 + (uint32_t)(wave * 64 + lane) * 16));
+    if constexpr (kScore) k_prefetch(ka, kv_base + (uint32_t)buf_next_i * kBufBytes);
     bool rescale = false;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      al[t] = lds.alpha[parity][16 * t + c];
-      rescale |= al[t] != 1.0f;
-    }
+    for (int t = 0; t < 4; ++t) rescale |= al[t] != 1.0f;
     if (__builtin_amdgcn_ballot_w64(rescale)) {
 #pragma unroll
       for (int t = 0; t < 4; ++t)
@@ -408,23 +442,9 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
         for (int m = 0; m < kM; ++m) o[t][m] *= al[t];
       l_acc *= lds.alpha[parity][16 * wave + c];
     }
-    v8bf pb[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-      pb[t] = as_v8bf(lds_load<v4u>(p_base + parity * 4096 + (uint32_t)(t * 64 + lane) * 16));
     {
-      const v8bf p_own = as_v8bf(lds_load<v4u>(p_base + parity * 4096 + (uint32_t)(wave * 64 + lane) * 16));
       const v4u ones = v4u{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
       l_acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(ones), p_own, l_acc, 0, 0, 0);
-    }
-    const uint32_t vbase = lane_base(buf, v_lane);
-    auto v_addr = [&](int m) -> uint32_t { return vbase + 32 * m; };
-    constexpr int kAhead = 4;
-    v4s vlo[kAhead], vhi[kAhead];
-#pragma unroll
-    for (int d = 0; d < kAhead; ++d) {
-      vlo[d] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)v_addr(d));
-      vhi[d] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)(v_addr(d) + kHalf));
     }
 #pragma unroll
     for (int m = 0; m < kM; ++m) {
@@ -449,9 +469,11 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int m = 0; m < kM; ++m) o[t][m] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    v4u ka[kAheadK];
+    if constexpr (decltype(role)::value) k_prefetch(ka, kv_base);
     for (int it = 0; it < n_blocks; it += 2) {
-      step(it, Set1{}, role, o);
-      step(it + 1, Set0{}, role, o);
+      step(it, Set1{}, role, o, ka);
+      step(it + 1, Set0{}, role, o, ka);
     }
     // The fetches past the last block are never read; let them land before
     // the registers are released.
