@@ -11,10 +11,14 @@
 //   (resident in VGPRs for the whole key loop) and B = 128 dims x 16 keys
 //   read from LDS; one instruction is a full 128-deep dot product.
 // * C layout: lane l, register r -> head 16t + 4(l/16) + r, key l%16. The
-//   head-weighted ReLU sum is 16 in-lane (max, fma) pairs per key per query;
-//   the four lane rows are then combined with a reduce-scatter on the gfx950
-//   row-swap permutes (v_permlane32_swap, v_permlane16_swap) so lane l ends
-//   with key l of a 64-key stage: one coalesced 256-byte row store.
+//   head-weighted ReLU sum uses relu(s) = (s + |s|) / 2: the |s| half is 16
+//   in-lane FMAs per key per query (|s| is a free source modifier), and the
+//   linear half, sum_h w_h s_h / 2 = k . q' with q' = sum_h w_h q_h / 2, is
+//   one more MFMA per 16 keys for all four queries of a wave, with q' held
+//   as four e4m3 digits (q' to ~2^-17 of its largest element). The four lane
+//   rows are then combined with a reduce-scatter on the gfx950 row-swap
+//   permutes (v_permlane32_swap, v_permlane16_swap) so lane l ends with key
+//   l of a 64-key stage: one coalesced 256-byte row store.
 // * The epilogue of one (query, 16-key) unit runs while the four MFMAs of the
 //   next unit execute (explicitly interleaved).
 // * Work-group: 4 waves (one per SIMD, so Q of 4 queries stays in registers
@@ -28,6 +32,8 @@
 //   pending it no longer says which loads are done. Wave 0 issues every DMA
 //   (and waits on vmcnt for them) but stores nothing; its rows go through LDS
 //   to waves 1-3, which store their own rows and wave 0's in turn.
+#include <utility>
+
 #include "dsa_common.h"
 #include "../../include/dsa_gfx950.h"
 
@@ -35,6 +41,7 @@ namespace dsa {
 namespace {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v2f __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
@@ -49,7 +56,14 @@ constexpr int kRing = 4;
 constexpr int kKBytes = kStageKeys * kDim;         // 8 KB of keys per stage
 constexpr int kKLoads = kKBytes / (64 * 16);       // DMA instructions for the keys (wave 0)
 constexpr int kStageBytes = kKBytes + 64 * 4;      // + the stage's 64 key scales
+constexpr int kDigits = 4;                         // e4m3 digits of the folded query
 
+
+// f(integral_constant<int, I>) for every I of the sequence, in order.
+template <typename F, int... I>
+__device__ __forceinline__ void for_each_index(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
 
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -147,13 +161,100 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
     for (int t = 0; t < 4; ++t) {
       const v4f wv = *reinterpret_cast<const v4f*>(w + qc * kHeads + 16 * t + 4 * group);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) wt[j][4 * t + r] = live ? wv[r] : 0.0f;
+      for (int r = 0; r < 4; ++r) wt[j][4 * t + r] = live ? 0.5f * wv[r] : 0.0f;
     }
     // A dead query gets an empty visible range; its stores are skipped anyway.
     int64_t e = ends ? (int64_t)ends[qc] : query_start + qc + 1;
     if (e > columns) e = columns;
     qs[j] = live ? (starts ? starts[qc] : 0) : 0;
     qe[j] = live ? (int32_t)e : 0;
+  }
+
+  // Linear half of the head sum: sum_h (w_h / 2) s_h = k . q' with
+  // q' = sum_h (w_h / 2) q_h, formed here in fp32 (lane 16j + c: query j,
+  // dims 8c .. 8c + 7) and written as kDigits e4m3 digits, digit d at scale
+  // 2^(E_j - 4d) (|q'| < 2^(E_j + 8)): each digit holds the residual of the
+  // ones before it to within half an e4m3 ulp, so the four carry q' to about
+  // 2^-17 of its largest element. In the MFMA operand, row 4d + j is digit d
+  // of query j; its C row then sits in lane group d, register j, so the
+  // reduction over lane groups that sums head partials also sums the digits.
+  __shared__ __align__(16) uint8_t digits[kWaves][kQueriesPerWave][kDigits][kDim];
+  v8i qd;
+  float fl[kQueriesPerWave];
+  {
+    const int j = lane >> 4;
+    const int c = lane & 15;
+    const int64_t qi = qw + j;
+    const bool live = qi < rows;
+    const int64_t qc = live ? qi : 0;
+    const uint8_t* qrow = q + qc * kHeads * kDim + 8 * c;
+    // All 64 heads' codes in flight at once; the weights of heads 4c .. 4c + 3
+    // per lane, each head's weight broadcast along the 16-lane row by DPP
+    // (row_newbcast).
+    uint2 codes[kHeads];
+#pragma unroll
+    for (int h = 0; h < kHeads; ++h) codes[h] = *reinterpret_cast<const uint2*>(qrow + h * kDim);
+    const v4f w4 = *reinterpret_cast<const v4f*>(w + qc * kHeads + 4 * c);
+    float qp[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    auto add_head = [&](auto head) {
+      constexpr int h = decltype(head)::value;
+      const float wb = __int_as_float(
+          __builtin_amdgcn_update_dpp(0, __float_as_int(w4[h & 3]), 0x150 + (h >> 2), 0xF, 0xF, false));
+      const float wh = live ? 0.5f * wb : 0.0f;
+      const v2f x0 = __builtin_amdgcn_cvt_pk_f32_fp8(codes[h].x, false);
+      const v2f x1 = __builtin_amdgcn_cvt_pk_f32_fp8(codes[h].x, true);
+      const v2f x2 = __builtin_amdgcn_cvt_pk_f32_fp8(codes[h].y, false);
+      const v2f x3 = __builtin_amdgcn_cvt_pk_f32_fp8(codes[h].y, true);
+      qp[0] = fmaf(wh, x0[0], qp[0]);
+      qp[1] = fmaf(wh, x0[1], qp[1]);
+      qp[2] = fmaf(wh, x1[0], qp[2]);
+      qp[3] = fmaf(wh, x1[1], qp[3]);
+      qp[4] = fmaf(wh, x2[0], qp[4]);
+      qp[5] = fmaf(wh, x2[1], qp[5]);
+      qp[6] = fmaf(wh, x3[0], qp[6]);
+      qp[7] = fmaf(wh, x3[1], qp[7]);
+    };
+    for_each_index(add_head, std::make_integer_sequence<int, kHeads>{});
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(qp[i]));
+#pragma unroll
+    for (int m = 8; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 16));
+    int ex = 0;
+    (void)frexpf(amax, &ex);  // amax < 2^ex (ex = 0 for amax = 0)
+    const int e0 = ex - 8;
+#pragma unroll
+    for (int d = 0; d < kDigits; ++d) {
+      const int e = e0 - 4 * d;
+      uint32_t lo = 0, hi = 0;
+      lo = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(qp[0], -e), ldexpf(qp[1], -e), lo, false);
+      lo = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(qp[2], -e), ldexpf(qp[3], -e), lo, true);
+      hi = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(qp[4], -e), ldexpf(qp[5], -e), hi, false);
+      hi = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(qp[6], -e), ldexpf(qp[7], -e), hi, true);
+      *reinterpret_cast<uint2*>(&digits[wave][j][d][8 * c]) = make_uint2(lo, hi);
+      const v2f y0 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
+      const v2f y1 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
+      const v2f y2 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
+      const v2f y3 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+      qp[0] -= ldexpf(y0[0], e);
+      qp[1] -= ldexpf(y0[1], e);
+      qp[2] -= ldexpf(y1[0], e);
+      qp[3] -= ldexpf(y1[1], e);
+      qp[4] -= ldexpf(y2[0], e);
+      qp[5] -= ldexpf(y2[1], e);
+      qp[6] -= ldexpf(y3[0], e);
+      qp[7] -= ldexpf(y3[1], e);
+    }
+    // A operand: lane l holds row l % 16 = 4d + j', dims 32 (l / 16) .. + 31.
+    const int jr = lane & 3, dr = (lane & 15) >> 2, blk = lane >> 4;
+    const v4u lo = *reinterpret_cast<const v4u*>(&digits[wave][jr][dr][32 * blk]);
+    const v4u hi = *reinterpret_cast<const v4u*>(&digits[wave][jr][dr][32 * blk + 16]);
+    qd = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    // C rows of lane group g = digit g: register r (query r) is scaled by
+    // 2^(E_r - 4g).
+#pragma unroll
+    for (int r = 0; r < kQueriesPerWave; ++r)
+      fl[r] = ldexpf(1.0f, __builtin_amdgcn_readlane(e0, 16 * r) - 4 * group);
   }
 
   // DMA plan (wave 0 only): K chunk p = 64 i + lane of a stage (load i) is
@@ -225,25 +326,31 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
     b[0] = load_b(0);
     b[1] = load_b(1);
     v4f acc[2][4];
+    v4f acc_lin[2];  // linear half of key group u (parity u & 1), all four queries
     auto mfmas = [&](int i) {
       const int u = i / kQueriesPerWave, j = i % kQueriesPerWave;
 #pragma unroll
       for (int t = 0; t < 4; ++t)
         acc[i & 1][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
             qa[j][t], b[u & 1], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0, 0, 0, 0);
+      if (j == 0)
+        acc_lin[u & 1] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+            qd, b[u & 1], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0, 0, 0, 0);
     };
     auto epilogue = [&](int i) {
       const int u = i / kQueriesPerWave, j = i % kQueriesPerWave;
-      // Four independent chains (one per head tile), so no fma waits on the
-      // previous one.
+      // relu(s) w = (|s| + s) w / 2: the |s| half here, one FMA per head
+      // (wt holds w / 2), four independent chains (one per head tile); the
+      // s half is the linear MFMA's share of this lane.
       float pt[4];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) pt[t] = fmaxf(acc[i & 1][t][0], 0.0f) * wt[j][4 * t];
+      for (int t = 0; t < 4; ++t) pt[t] = fabsf(acc[i & 1][t][0]) * wt[j][4 * t];
 #pragma unroll
       for (int r = 1; r < 4; ++r)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) pt[t] = fmaf(fmaxf(acc[i & 1][t][r], 0.0f), wt[j][4 * t + r], pt[t]);
+        for (int t = 0; t < 4; ++t) pt[t] = fmaf(fabsf(acc[i & 1][t][r]), wt[j][4 * t + r], pt[t]);
       float p = (pt[0] + pt[1]) + (pt[2] + pt[3]);
+      p = fmaf(acc_lin[u & 1][j], fl[j], p);
       // Pins the epilogue here: otherwise instruction selection sinks it below
       // every MFMA of the stage and all 64 results stay live.
       asm volatile("" : "+v"(p));
@@ -258,14 +365,19 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
       const bool refill = i % kQueriesPerWave == kQueriesPerWave - 1 && i / kQueriesPerWave + 2 < 4;
       if (refill) b[(i / kQueriesPerWave) & 1] = load_b(i / kQueriesPerWave + 2);
       epilogue(i - 1);
-      // One MFMA, then the (max, fma) pairs of one accumulator of the
-      // previous unit, four times: the results read were issued a full unit
-      // earlier, and the VALU work runs under the MFMAs.
+      // One MFMA, then the FMAs of one accumulator of the previous unit,
+      // four times (five MFMAs with a key group's linear one): the results
+      // read were issued a full unit earlier, and the VALU work runs under
+      // the MFMAs.
       if (refill) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      if (i % kQueriesPerWave == 0) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+      }
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 9, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
