@@ -28,12 +28,14 @@ SIGNATURES = {
                                    _ptr],
     "dsa_indexer_logits_fp8": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _ptr,
                                _ptr],
+    "dsa_indexer_logits_fp8_folded": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64,
+                                      _ptr, _ptr, _ptr],
     "dsa_topk_radix": [_ptr, _i64, _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr],
     "dsa_topk_workspace_bytes": [_i64, ctypes.POINTER(ctypes.c_int64)],
     "dsa_topk_radix_split": [_ptr, _i64, _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr, _i64, _ptr],
     "dsa_kv_pack_fp8": [_ptr, _i64, _i64, _ptr, _i64, _ptr, _ptr, _ptr],
-    "dsa_layer_prologue_fp8": [_ptr, _i64, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _ptr, _ptr, _ptr,
-                               _i64, _i64, _ptr, _i64, _ptr, _ptr, _ptr],
+    "dsa_layer_prologue_fp8": [_ptr, _i64, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _ptr, _ptr,
+                               _ptr, _i64, _i64, _ptr, _i64, _ptr, _ptr, _ptr],
     "dsa_sparse_mla_bf16": [_ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _f32, _ptr, _ptr],
     "dsa_sparse_mla_fp8_paged": [_ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i64, _f32,
                                  _ptr, _ptr],

@@ -113,7 +113,7 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
     const uint8_t* __restrict__ q, const uint8_t* __restrict__ k, const float* __restrict__ w,
     const float* __restrict__ kscale, const int32_t* __restrict__ starts,
     const int32_t* __restrict__ ends, int64_t query_start, int64_t rows, int64_t columns,
-    int64_t ldo, int64_t keys_per_split, float* __restrict__ out) {
+    int64_t ldo, int64_t keys_per_split, const float* __restrict__ q_fold, float* __restrict__ out) {
   __shared__ __align__(16) uint8_t ring[kRing][kStageBytes];
 
   const int tid = threadIdx.x;
@@ -187,34 +187,59 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
     const int64_t qi = qw + j;
     const bool live = qi < rows;
     const int64_t qc = live ? qi : 0;
-    const uint8_t* qrow = q + qc * kHeads * kDim + 8 * c;
-    // All 64 heads' codes in flight at once; the weights of heads 4c .. 4c + 3
-    // per lane, each head's weight broadcast along the 16-lane row by DPP
-    // (row_newbcast).
-    uint2 codes[kHeads];
+    // q' in four partial sums over heads 16g .. 16g + 15 (each one fmaf chain
+    // from 0 in increasing head order), then 0.5 (((p0 + p1) + p2) + p3): the
+    // same bits whether the partials come from the layer prologue (q_fold,
+    // [rows][4][128]) or are formed here.
+    float pg[4][8];
+    if (q_fold) {
 #pragma unroll
-    for (int h = 0; h < kHeads; ++h) codes[h] = *reinterpret_cast<const uint2*>(qrow + h * kDim);
-    const v4f w4 = *reinterpret_cast<const v4f*>(w + qc * kHeads + 4 * c);
-    float qp[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-    auto add_head = [&](auto head) {
-      constexpr int h = decltype(head)::value;
-      const float wb = __int_as_float(
-          __builtin_amdgcn_update_dpp(0, __float_as_int(w4[h & 3]), 0x150 + (h >> 2), 0xF, 0xF, false));
-      const float wh = live ? 0.5f * wb : 0.0f;
-      const v2f x0 = __builtin_amdgcn_cvt_pk_f32_fp8(codes[h].x, false);
-      const v2f x1 = __builtin_amdgcn_cvt_pk_f32_fp8(codes[h].x, true);
-      const v2f x2 = __builtin_amdgcn_cvt_pk_f32_fp8(codes[h].y, false);
-      const v2f x3 = __builtin_amdgcn_cvt_pk_f32_fp8(codes[h].y, true);
-      qp[0] = fmaf(wh, x0[0], qp[0]);
-      qp[1] = fmaf(wh, x0[1], qp[1]);
-      qp[2] = fmaf(wh, x1[0], qp[2]);
-      qp[3] = fmaf(wh, x1[1], qp[3]);
-      qp[4] = fmaf(wh, x2[0], qp[4]);
-      qp[5] = fmaf(wh, x2[1], qp[5]);
-      qp[6] = fmaf(wh, x3[0], qp[6]);
-      qp[7] = fmaf(wh, x3[1], qp[7]);
-    };
-    for_each_index(add_head, std::make_integer_sequence<int, kHeads>{});
+      for (int g = 0; g < 4; ++g) {
+        const v4f* src = reinterpret_cast<const v4f*>(q_fold + (qc * 4 + g) * kDim + 8 * c);
+        const v4f a = src[0], b = src[1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pg[g][i] = live ? a[i] : 0.0f;
+          pg[g][4 + i] = live ? b[i] : 0.0f;
+        }
+      }
+    } else {
+      const uint8_t* qrow = q + qc * kHeads * kDim + 8 * c;
+      // All 64 heads' codes in flight at once; the weights of heads 4c ..
+      // 4c + 3 per lane, each head's weight broadcast along the 16-lane row
+      // by DPP (row_newbcast).
+      uint2 codes[kHeads];
+#pragma unroll
+      for (int h = 0; h < kHeads; ++h) codes[h] = *reinterpret_cast<const uint2*>(qrow + h * kDim);
+      const v4f w4 = *reinterpret_cast<const v4f*>(w + qc * kHeads + 4 * c);
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pg[g][i] = 0.0f;
+      auto add_head = [&](auto head) {
+        constexpr int h = decltype(head)::value;
+        const float wb = __int_as_float(
+            __builtin_amdgcn_update_dpp(0, __float_as_int(w4[h & 3]), 0x150 + (h >> 2), 0xF, 0xF, false));
+        const float wh = live ? wb : 0.0f;
+        const v2f x0 = __builtin_amdgcn_cvt_pk_f32_fp8(codes[h].x, false);
+        const v2f x1 = __builtin_amdgcn_cvt_pk_f32_fp8(codes[h].x, true);
+        const v2f x2 = __builtin_amdgcn_cvt_pk_f32_fp8(codes[h].y, false);
+        const v2f x3 = __builtin_amdgcn_cvt_pk_f32_fp8(codes[h].y, true);
+        float* p = pg[h >> 4];
+        p[0] = fmaf(wh, x0[0], p[0]);
+        p[1] = fmaf(wh, x0[1], p[1]);
+        p[2] = fmaf(wh, x1[0], p[2]);
+        p[3] = fmaf(wh, x1[1], p[3]);
+        p[4] = fmaf(wh, x2[0], p[4]);
+        p[5] = fmaf(wh, x2[1], p[5]);
+        p[6] = fmaf(wh, x3[0], p[6]);
+        p[7] = fmaf(wh, x3[1], p[7]);
+      };
+      for_each_index(add_head, std::make_integer_sequence<int, kHeads>{});
+    }
+    float qp[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qp[i] = 0.5f * (((pg[0][i] + pg[1][i]) + pg[2][i]) + pg[3][i]);
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(qp[i]));
@@ -418,12 +443,13 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
 }  // namespace
 }  // namespace dsa
 
-extern "C" int dsa_indexer_logits_fp8(const void* q, const void* k, const float* weights,
-                                      const float* kscale, const int32_t* starts,
-                                      const int32_t* ends, int64_t query_start, int64_t rows,
-                                      int64_t columns, int64_t ldo, float* out,
-                                      hipStream_t stream) {
-  using namespace dsa;
+namespace dsa {
+namespace {
+
+int logits_launch(const void* q, const void* k, const float* weights, const float* kscale,
+                  const int32_t* starts, const int32_t* ends, int64_t query_start, int64_t rows,
+                  int64_t columns, int64_t ldo, const float* q_fold, float* out,
+                  hipStream_t stream) {
   DSA_CHECK_ARG(rows >= 0 && columns >= 1, "logits requires nonempty K");
   DSA_CHECK_ARG(ldo >= columns, "output row stride must cover every column");
   DSA_CHECK_ARG(query_start >= 0 && query_start + rows <= columns,
@@ -434,8 +460,9 @@ extern "C" int dsa_indexer_logits_fp8(const void* q, const void* k, const float*
   DSA_CHECK_ARG(reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(weights) % 16 == 0 &&
-                    reinterpret_cast<uintptr_t>(kscale) % 4 == 0,
-                "q, k and weights must be 16-byte aligned");
+                    reinterpret_cast<uintptr_t>(kscale) % 4 == 0 &&
+                    reinterpret_cast<uintptr_t>(q_fold) % 16 == 0,
+                "q, k, weights and q_fold must be 16-byte aligned");
   DSA_CHECK_ARG(columns * kDim < 0xFFFFFFFFll, "K must be addressable with 32-bit offsets");
   const int64_t qgroups = (rows + kQueriesPerBlock - 1) / kQueriesPerBlock;
   const int64_t cus = device_cu_count();
@@ -448,7 +475,31 @@ extern "C" int dsa_indexer_logits_fp8(const void* q, const void* k, const float*
   DSA_CHECK_ARG(ldo < 0x7FFFFFFF - 64, "the logits row stride must fit int32");
   hipLaunchKernelGGL(logits_fp8_mfma, dim3((unsigned)splits, (unsigned)qgroups), dim3(kThreads),
                      0, stream, static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(k),
-                     weights, kscale, starts, ends, query_start, rows, columns, ldo, per, out);
+                     weights, kscale, starts, ends, query_start, rows, columns, ldo, per, q_fold,
+                     out);
   DSA_CHECK_LAUNCH("indexer logits");
   return kOk;
+}
+
+}  // namespace
+}  // namespace dsa
+
+extern "C" int dsa_indexer_logits_fp8(const void* q, const void* k, const float* weights,
+                                      const float* kscale, const int32_t* starts,
+                                      const int32_t* ends, int64_t query_start, int64_t rows,
+                                      int64_t columns, int64_t ldo, float* out,
+                                      hipStream_t stream) {
+  return dsa::logits_launch(q, k, weights, kscale, starts, ends, query_start, rows, columns, ldo,
+                            nullptr, out, stream);
+}
+
+extern "C" int dsa_indexer_logits_fp8_folded(const void* q, const void* k, const float* weights,
+                                             const float* kscale, const int32_t* starts,
+                                             const int32_t* ends, int64_t query_start,
+                                             int64_t rows, int64_t columns, int64_t ldo,
+                                             const float* q_fold, float* out,
+                                             hipStream_t stream) {
+  DSA_CHECK_ARG(rows == 0 || q_fold != nullptr, "null pointer");
+  return dsa::logits_launch(q, k, weights, kscale, starts, ends, query_start, rows, columns, ldo,
+                            q_fold, out, stream);
 }

@@ -47,9 +47,16 @@ __device__ __forceinline__ uint32_t quantize_one(float v, float scale, float inv
   return f32_to_e4m3fn(y);
 }
 
+// One lane's share of a quantised row: its 8 codes and the row's folded
+// weight (zeros for a row past the end).
+struct QuantLane {
+  uint32_t lo, hi;
+  float fold;
+};
+
 // 16 lanes per 128-wide bf16 row; each lane owns 8 consecutive values. Block
 // `block` of 256 threads covers rows 16 block .. 16 block + 15.
-__device__ __forceinline__ void quantize_rows_d128(int64_t block, const uint16_t* __restrict__ x,
+__device__ __forceinline__ QuantLane quantize_rows_d128(int64_t block, const uint16_t* __restrict__ x,
                                                    int64_t rows, int64_t row_stride,
                                                    uint8_t* __restrict__ y,
                                                    float* __restrict__ scales, int ue8m0,
@@ -74,7 +81,7 @@ __device__ __forceinline__ void quantize_rows_d128(int64_t block, const uint16_t
     m = m > a ? m : a;
   }
   m = max_abs_bits_reduce<16>(m);
-  if (!live) return;
+  if (!live) return QuantLane{0, 0, 0.0f};
   const float scale = scale_from_amax_bits(m, ue8m0 != 0);
   const float inverse = 1.0f / scale;
   uint32_t lo = 0, hi = 0;
@@ -83,9 +90,38 @@ __device__ __forceinline__ void quantize_rows_d128(int64_t block, const uint16_t
 #pragma unroll
   for (int i = 0; i < 4; ++i) hi |= quantize_one(v[4 + i], scale, inverse, ue8m0 != 0) << (8 * i);
   *reinterpret_cast<uint2*>(y + row * 128 + part * 8) = make_uint2(lo, hi);
+  const float fold = fold_out ? fold_in[row] * scale : 0.0f;
   if (part == 0) {
     scales[row] = scale;
-    if (fold_out) fold_out[row] = fold_in[row] * scale;
+    if (fold_out) fold_out[row] = fold;
+  }
+  return QuantLane{lo, hi, fold};
+}
+
+// Partial folded query of one block of 16 index-Q rows (heads 16 g .. 16 g + 15
+// of one query, g = block % 4): part[d] = sum_h w_folded[h] * q[h, d] over the
+// block's heads in increasing order, one fmaf chain per dim from 0, written to
+// q_fold[block, d] ([queries][4][128]). The logits kernel forms the same
+// chains itself when it is not given them, so both give the same bits.
+__device__ __forceinline__ void fold_partial(int64_t block, const QuantLane& mine,
+                                             float* __restrict__ q_fold) {
+  __shared__ uint32_t codes[16][32];
+  __shared__ float fold[16];
+  const int row = threadIdx.x >> 4;
+  const int part = threadIdx.x & 15;
+  codes[row][2 * part] = mine.lo;
+  codes[row][2 * part + 1] = mine.hi;
+  if (part == 0) fold[row] = mine.fold;
+  __syncthreads();
+  if (threadIdx.x < 128) {
+    const int d = threadIdx.x;
+    float acc = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 16; ++h) {
+      const float x = __builtin_amdgcn_cvt_f32_fp8((int)(codes[h][d >> 2] >> (8 * (d & 3))), 0);
+      acc = fmaf(fold[h], x, acc);
+    }
+    q_fold[block * 128 + d] = acc;
   }
 }
 
@@ -268,13 +304,15 @@ __global__ __launch_bounds__(256) void kv_pack_fp8(const uint16_t* __restrict__ 
 __global__ __launch_bounds__(256) void layer_prologue(
     const uint16_t* __restrict__ q, int64_t q_rows, const float* __restrict__ weights,
     uint8_t* __restrict__ q_codes, float* __restrict__ q_scales, float* __restrict__ w_folded,
-    const uint16_t* __restrict__ k, int64_t k_rows, uint8_t* __restrict__ k_codes,
+    float* __restrict__ q_fold, const uint16_t* __restrict__ k, int64_t k_rows,
+    uint8_t* __restrict__ k_codes,
     float* __restrict__ k_scales, const uint16_t* __restrict__ kv, int64_t tokens,
     int64_t token_offset, const int32_t* __restrict__ page_table, int64_t pages,
     uint8_t* __restrict__ cache, int32_t* __restrict__ status, int64_t nq, int64_t nk) {
   const int64_t b = blockIdx.x;
   if (b < nq) {
-    quantize_rows_d128(b, q, q_rows, 128, q_codes, q_scales, 1, weights, w_folded);
+    const QuantLane mine = quantize_rows_d128(b, q, q_rows, 128, q_codes, q_scales, 1, weights, w_folded);
+    if (q_fold) fold_partial(b, mine, q_fold);
   } else if (b < nq + nk) {
     quantize_rows_d128(b - nq, k, k_rows, 128, k_codes, k_scales, 1, nullptr, nullptr);
   } else {
@@ -305,7 +343,7 @@ extern "C" int dsa_kv_pack_fp8(const void* kv, int64_t tokens, int64_t token_off
 
 extern "C" int dsa_layer_prologue_fp8(const void* q, int64_t q_rows, const float* weights,
                                       void* q_codes, float* q_scales, float* w_folded,
-                                      const void* k, int64_t k_rows, void* k_codes,
+                                      float* q_fold, const void* k, int64_t k_rows, void* k_codes,
                                       float* k_scales, const void* kv, int64_t tokens,
                                       int64_t token_offset, const int32_t* page_table,
                                       int64_t pages, void* cache, int32_t* status,
@@ -324,6 +362,8 @@ extern "C" int dsa_layer_prologue_fp8(const void* q, int64_t q_rows, const float
                     reinterpret_cast<uintptr_t>(q_codes) % 8 == 0 &&
                     reinterpret_cast<uintptr_t>(k_codes) % 8 == 0,
                 "prologue inputs must be 16-byte and code outputs 8-byte aligned");
+  DSA_CHECK_ARG(q_fold == nullptr || q_rows % 64 == 0,
+                "the folded query needs whole queries of 64 index-Q rows");
   const int64_t nq = (q_rows * 16 + 255) / 256;
   const int64_t nk = (k_rows * 16 + 255) / 256;
   const int64_t nt = (tokens + 3) / 4;
@@ -331,7 +371,7 @@ extern "C" int dsa_layer_prologue_fp8(const void* q, int64_t q_rows, const float
   DSA_CHECK_ARG(nq + nk + nt < 0x7FFFFFFF, "prologue too large for one launch");
   hipLaunchKernelGGL(layer_prologue, dim3((unsigned)(nq + nk + nt)), dim3(256), 0, stream,
                      static_cast<const uint16_t*>(q), q_rows, weights,
-                     static_cast<uint8_t*>(q_codes), q_scales, w_folded,
+                     static_cast<uint8_t*>(q_codes), q_scales, w_folded, q_rows ? q_fold : nullptr,
                      static_cast<const uint16_t*>(k), k_rows, static_cast<uint8_t*>(k_codes),
                      k_scales, static_cast<const uint16_t*>(kv), tokens, token_offset, page_table,
                      pages, static_cast<uint8_t*>(cache), status, nq, nk);

@@ -169,7 +169,7 @@ def padded_columns(columns):
 
 
 def logits(q, k, weights, kscale, query_start, prefetch=None, *, _bounds=None,
-           _pad_to_stride=False):
+           _pad_to_stride=False, _q_fold=None):
     """Return causal FP32 ``[Q,N]`` logits with a padded physical row stride.
 
     ``out[i, j] = kscale[j] * sum_h weights[i, h] * relu(q[i, h] . k[j])`` for
@@ -180,6 +180,8 @@ def logits(q, k, weights, kscale, query_start, prefetch=None, *, _bounds=None,
 
     ``prefetch`` must be ``None``: the reference's fused ECHO prefetch is
     replaced in this build by the top-k-driven gather (``token_pool``).
+    ``_q_fold`` (f32 ``[Q, 4, 128]``, from the layer prologue) carries the
+    partial folded queries the kernel would otherwise form; same result bits.
     """
     if q.ndim != 3 or q.shape[1:] != (64, 128) or not q.is_cuda or len(q) < 1:
         raise ValueError("ECHO requires nonempty CUDA Q[query,64,128]")
@@ -207,26 +209,23 @@ def logits(q, k, weights, kscale, query_start, prefetch=None, *, _bounds=None,
         starts, ends = _bounds
         _check_tensor(starts, (rows,), torch.int32, device, "starts")
         _check_tensor(ends, (rows,), torch.int32, device, "ends")
+    if _q_fold is not None:
+        _check_tensor(_q_fold, (rows, 4, 128), torch.float32, device, "_q_fold")
+        if _q_fold.data_ptr() % 16:
+            _q_fold = _q_fold.clone()
     # The kernel reads q, k and weights in 16-byte units.
     q, k, weights = (t if t.data_ptr() % 16 == 0 else t.clone() for t in (q, k, weights))
     width = padded_columns(columns)
     output = torch.empty((rows, width), dtype=torch.float32, device=device)
+    args = [_native.ptr(q), _native.ptr(k), _native.ptr(weights), _native.ptr(kscale),
+            _native.ptr(starts), _native.ptr(ends), query_start, rows, columns, width]
     with torch.cuda.device(device):
-        _native.call(
-            "dsa_indexer_logits_fp8",
-            _native.ptr(q),
-            _native.ptr(k),
-            _native.ptr(weights),
-            _native.ptr(kscale),
-            _native.ptr(starts),
-            _native.ptr(ends),
-            query_start,
-            rows,
-            columns,
-            width,
-            _native.ptr(output),
-            _native.stream_of(device),
-        )
+        if _q_fold is None:
+            _native.call("dsa_indexer_logits_fp8", *args, _native.ptr(output),
+                         _native.stream_of(device))
+        else:
+            _native.call("dsa_indexer_logits_fp8_folded", *args, _native.ptr(_q_fold),
+                         _native.ptr(output), _native.stream_of(device))
     return output if _pad_to_stride else output[:, :columns]
 
 

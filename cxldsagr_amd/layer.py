@@ -132,7 +132,8 @@ class DSALayer:
         """Q quantisation + weight fold, new index K into the cache and the new
         KV records into the fp8 paged cache, in one launch
         (``dsa_layer_prologue_fp8``; the same bits as the three separate
-        operators)."""
+        operators). Also returns the partial folded queries ``[rows, 4, 128]``
+        that let the logits kernel skip forming them (same logits bits)."""
         rows = len(index_q)
         end = position + rows
         index_q, index_k, weights, kv = (t.contiguous() for t in (index_q, index_k, weights, kv))
@@ -140,18 +141,19 @@ class DSALayer:
         q8 = torch.empty(index_q.shape, dtype=torch.float8_e4m3fn, device=self.device)
         q_scales = torch.empty((*index_q.shape[:-1], 1), dtype=torch.float32, device=self.device)
         folded = torch.empty_like(weights)
+        q_fold = torch.empty((rows, 4, 128), dtype=torch.float32, device=self.device)
         with torch.cuda.device(self.device):
             _native.call(
                 "dsa_layer_prologue_fp8",
                 _native.ptr(index_q), rows * 64, _native.ptr(weights), _native.ptr(q8),
-                _native.ptr(q_scales), _native.ptr(folded),
+                _native.ptr(q_scales), _native.ptr(folded), _native.ptr(q_fold),
                 _native.ptr(index_k), rows, _native.ptr(self.index_keys[position:end]),
                 _native.ptr(self.index_scales[position:end]),
                 _native.ptr(kv), rows, position, _native.ptr(self.page_table),
                 self.kv_cache.shape[0], _native.ptr(self.kv_cache), None,
                 _native.stream_of(self.device),
             )
-        return q8, folded
+        return q8, folded, q_fold
 
     def _attend(self, q, ids, end):
         if self.kv_format == "fp8_paged":
@@ -170,15 +172,16 @@ class DSALayer:
         end = position + rows
         if end > self.capacity or len(q) != rows or len(kv) != rows or len(index_k) != rows:
             raise ValueError("query batch exceeds the layer capacity or inputs disagree in length")
+        q_fold = None
         if self._fused_prologue_applies(index_q, index_k, weights, kv):
-            q8, folded = self._prologue(index_q, index_k, weights, kv, position)
+            q8, folded, q_fold = self._prologue(index_q, index_k, weights, kv, position)
         else:
             indexer.quantize_into(index_k, self.index_keys[position:end],
                                   self.index_scales[position:end])
             q8, _, folded = indexer.quantize_index_folded(index_q, weights)
             self._append_kv(kv, position)
         scores = indexer.logits(q8, self.index_keys[:end], folded, self.index_scales[:end],
-                                position, _pad_to_stride=end >= self.topk)
+                                position, _pad_to_stride=end >= self.topk, _q_fold=q_fold)
         _, ids = indexer.exact_topk(scores, self.topk)
         selection = TokenSelection(ids)
         out = self._attend(q, ids, end)

@@ -84,6 +84,19 @@ int dsa_indexer_logits_fp8(const void* q, const void* k, const float* weights,
                            float* out, hipStream_t stream);
 
 /*
+ * A4, the same contract and the same bits as dsa_indexer_logits_fp8, given
+ * q_fold: f32 [rows, 4, 128], the partial folded queries that
+ * dsa_layer_prologue_fp8 writes (16-byte aligned). The kernel then skips
+ * forming them itself. Same reference interface as dsa_indexer_logits_fp8
+ * (echo.py:299-410); the layer step calls this one.
+ */
+int dsa_indexer_logits_fp8_folded(const void* q, const void* k, const float* weights,
+                                  const float* kscale, const int32_t* starts, const int32_t* ends,
+                                  int64_t query_start, int64_t rows, int64_t columns,
+                                  int64_t ldo, const float* q_fold, float* out,
+                                  hipStream_t stream);
+
+/*
  * A6 - exact top-k, k <= 2048, sorted descending, SMALL ties, -1 ids for
  * non-finite values. Replaces exact_topk,
  * operators/deepseek_v32/indexer/selection.py:62-113 (FlashInfer radix_topk
@@ -133,13 +146,17 @@ int dsa_kv_pack_fp8(const void* kv, int64_t tokens, int64_t token_offset,
  * records. No reference counterpart as one entry: it replaces the three
  * launches of models/deepseek_v32/projections.py:241-244 +
  * quantization.py:63-88, attention.py:323-326 and attention.py:400-401 in a
- * layer step. Results equal those three entry points bit for bit.
+ * layer step. Results equal those three entry points bit for bit. q_fold
+ * (optional, f32 [q_rows / 64, 4, 128]; q_rows a multiple of 64) receives
+ * the partial folded queries for dsa_indexer_logits_fp8_folded: entry
+ * [i, g, d] = sum over heads h = 16g .. 16g + 15 of w_folded[i, h] *
+ * q_codes[i, h, d], one fmaf chain per entry in increasing h.
  */
 int dsa_layer_prologue_fp8(const void* q, int64_t q_rows, const float* weights, void* q_codes,
-                           float* q_scales, float* w_folded, const void* k, int64_t k_rows,
-                           void* k_codes, float* k_scales, const void* kv, int64_t tokens,
-                           int64_t token_offset, const int32_t* page_table, int64_t pages,
-                           void* cache, int32_t* status, hipStream_t stream);
+                           float* q_scales, float* w_folded, float* q_fold, const void* k,
+                           int64_t k_rows, void* k_codes, float* k_scales, const void* kv,
+                           int64_t tokens, int64_t token_offset, const int32_t* page_table,
+                           int64_t pages, void* cache, int32_t* status, hipStream_t stream);
 
 /*
  * A7 - sparse MLA over flat bf16 records. Replaces sparse_mla /

@@ -18,6 +18,7 @@ import numpy as np
 import pytest
 import torch
 
+from oracle import fp8 as ofp8
 from oracle import layer as olayer
 from oracle import sparse_mla as omla
 
@@ -133,7 +134,7 @@ def test_fused_prologue_equals_the_separate_stages(gpu):
     index_k, kv = inputs.index_k[history:].to(gpu), inputs.kv[history:].to(gpu)
     index_q[5, 7, 3] = float("nan")
     assert fused._fused_prologue_applies(index_q, index_k, weights, kv)
-    q8, folded = fused._prologue(index_q, index_k, weights, kv, history)
+    q8, folded, q_fold = fused._prologue(index_q, index_k, weights, kv, history)
     ref_q8, _, ref_folded = indexer.quantize_index_folded(index_q, weights)
     indexer.quantize_into(index_k, plain.index_keys[history:tokens], plain.index_scales[history:tokens])
     attention.pack_kv_fp8(kv, plain.kv_cache, plain.page_table, token_offset=history)
@@ -143,3 +144,19 @@ def test_fused_prologue_equals_the_separate_stages(gpu):
     assert torch.equal(fused.index_keys.view(torch.uint8), plain.index_keys.view(torch.uint8))
     assert torch.equal(fused.index_scales.view(torch.int32), plain.index_scales.view(torch.int32))
     assert torch.equal(fused.kv_cache, plain.kv_cache)
+
+    # Partial folded queries: per query and 16-head group, sum_h w_folded[h] *
+    # q[h, :] (float64 here, so compared to float32 rounding).
+    codes = ofp8.decode(q8.view(torch.uint8).cpu().numpy()).astype(np.float64)
+    w64 = folded.cpu().numpy().astype(np.float64)
+    expect = np.einsum("qgh,qghd->qgd", w64.reshape(queries, 4, 16), codes.reshape(queries, 4, 16, 128))
+    got = q_fold.cpu().numpy()
+    ok = np.isfinite(expect)
+    np.testing.assert_allclose(got[ok], expect[ok], rtol=1e-5, atol=1e-5 * np.abs(expect[ok]).max())
+    assert np.isnan(got[~ok]).all()
+    # The logits kernel given those partials writes the same bits as when it
+    # forms them itself (both finite and NaN rows).
+    keys, scales = fused.index_keys[:tokens], fused.index_scales[:tokens]
+    a = indexer.logits(q8, keys, folded, scales, history, _pad_to_stride=True)
+    b = indexer.logits(q8, keys, folded, scales, history, _pad_to_stride=True, _q_fold=q_fold)
+    assert torch.equal(a.view(torch.int32), b.view(torch.int32))
