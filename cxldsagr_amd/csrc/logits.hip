@@ -18,16 +18,17 @@
 //   as four e4m3 digits (q' to ~2^-17 of its largest element). The four lane
 //   rows are then combined with a reduce-scatter on the gfx950 row-swap
 //   permutes (v_permlane32_swap, v_permlane16_swap) so lane l ends with key
-//   l of a 64-key stage: one coalesced 256-byte row store.
+//   l of a 64-key pass: one coalesced 256-byte row store.
 // * The epilogue of one (query, 16-key) unit runs while the four MFMAs of the
 //   next unit execute (explicitly interleaved).
 // * Work-group: 4 waves (one per SIMD, so Q of 4 queries stays in registers
 //   and each B operand read from LDS feeds 16 MFMAs) x 4 queries = 16
 //   queries; the key range is split so the grid is about one work-group per CU.
-// * K stages (64 keys x 128 B, plus the 64 key scales) arrive by LDS DMA
+// * K stages (128 keys x 128 B, plus the 128 key scales) arrive by LDS DMA
 //   (global_load_lds_dwordx4 / _dword) into a ring kRing - 1 stages ahead,
 //   with the 16-byte chunks of each key XOR-swizzled by (key & 7) against
-//   bank conflicts of the B-operand reads.
+//   bank conflicts of the B-operand reads; one barrier per stage, and the
+//   stage is computed in two passes of 64 keys.
 // * Loads and stores never share a wave: vmcnt counts both, and with stores
 //   pending it no longer says which loads are done. Wave 0 issues every DMA
 //   (and waits on vmcnt for them) but stores nothing; its rows go through LDS
@@ -50,12 +51,14 @@ constexpr int kDim = 128;
 constexpr int kWaves = 4;
 constexpr int kQueriesPerWave = 4;
 constexpr int kQueriesPerBlock = kWaves * kQueriesPerWave;
-constexpr int kStageKeys = 64;
+constexpr int kStageKeys = 128;                    // keys per DMA stage and barrier
+constexpr int kHalfKeys = 64;                      // keys per compute pass (lane = key)
 constexpr int kThreads = kWaves * 64;
 constexpr int kRing = 4;
-constexpr int kKBytes = kStageKeys * kDim;         // 8 KB of keys per stage
+constexpr int kKBytes = kStageKeys * kDim;         // 16 KB of keys per stage
 constexpr int kKLoads = kKBytes / (64 * 16);       // DMA instructions for the keys (wave 0)
-constexpr int kStageBytes = kKBytes + 64 * 4;      // + the stage's 64 key scales
+constexpr int kSLoads = kStageKeys / 64;           // DMA instructions for the key scales
+constexpr int kStageBytes = kKBytes + kStageKeys * 4;  // + the stage's key scales
 constexpr int kDigits = 4;                         // e4m3 digits of the folded query
 
 
@@ -63,6 +66,10 @@ constexpr int kDigits = 4;                         // e4m3 digits of the folded 
 template <typename F, int... I>
 __device__ __forceinline__ void for_each_index(F&& f, std::integer_sequence<int, I...>) {
   (f(std::integral_constant<int, I>{}), ...);
+}
+
+__device__ __forceinline__ v4u lds_v4u(uint32_t addr) {
+  return *(const v4u __attribute__((address_space(3)))*)(uintptr_t)addr;
 }
 
 __device__ __forceinline__ void lds_barrier() {
@@ -284,8 +291,9 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
 
   // DMA plan (wave 0 only): K chunk p = 64 i + lane of a stage (load i) is
   // key 8i + lane / 8, stored chunk lane % 8 = logical chunk ^ (key & 7); then
-  // one 4-byte load per lane of the 64 key scales. Keys past the end re-read
-  // the last key (their columns are -inf), and stages past the end key 0.
+  // 4-byte loads of the stage's key scales (key 64 i + lane). Keys past the
+  // end re-read the last key (their columns are -inf), and stages past the
+  // end key 0.
   const uint32_t ring_base = (uint32_t)(uintptr_t)&ring[0][0];
   const int lane_key = lane >> 3;
   const uint32_t lane_chunk = 16u * (uint32_t)((lane & 7) ^ (lane_key & 7));
@@ -300,16 +308,21 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
       const int32_t key = min(8 * i + lane_key, last);
       dma16_s(kbase, (uint32_t)key * kDim + lane_chunk, slot_base + i * 1024);
     }
-    dma4_s(kscale + key0, 4u * (uint32_t)min(lane, last), slot_base + kKBytes);
+#pragma unroll
+    for (int i = 0; i < kSLoads; ++i)
+      dma4_s(kscale + key0, 4u * (uint32_t)min(64 * i + lane, last), slot_base + kKBytes + 256 * i);
   };
   // Wave 0's finished rows, [stage parity][query][key].
   __shared__ __align__(16) float staged[2][kQueriesPerWave][kStageKeys];
   auto store_staged = [&](int st) {
-    const int64_t key = kb + (int64_t)st * kStageKeys + lane;
 #pragma unroll
-    for (int j = 0; j < kQueriesPerWave; ++j) {
-      const int64_t qi = q0 + j;  // wave 0's queries
-      if (qi < rows && key < ke) out[qi * ldo + key] = staged[st & 1][j][lane];
+    for (int hf = 0; hf < kStageKeys / kHalfKeys; ++hf) {
+      const int64_t key = kb + (int64_t)st * kStageKeys + kHalfKeys * hf + lane;
+#pragma unroll
+      for (int j = 0; j < kQueriesPerWave; ++j) {
+        const int64_t qi = q0 + j;  // wave 0's queries
+        if (qi < rows && key < ke) out[qi * ldo + key] = staged[st & 1][j][kHalfKeys * hf + lane];
+      }
     }
   };
 
@@ -323,7 +336,7 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
 
   for (int s = 0; s < stages; ++s) {
     // Wave 0's loads of stage s have landed; stage s - 1 is free.
-    if (wave == 0) wait_dma<(kKLoads + 1) * (kRing - 2)>();
+    if (wave == 0) wait_dma<(kKLoads + kSLoads) * (kRing - 2)>();
     lds_barrier();
     if (wave == 0) {
       issue(s + kRing - 1);
@@ -332,93 +345,99 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
     }
 
     const uint32_t stage = ring_base + (uint32_t)(s % kRing) * kStageBytes;
-    const int64_t key0 = kb + (int64_t)s * kStageKeys;
+    // The stage's keys in two passes of 64 (lane l of a pass ends with key l).
+#pragma unroll
+    for (int hf = 0; hf < kStageKeys / kHalfKeys; ++hf) {
+      const int64_t key0 = kb + (int64_t)s * kStageKeys + kHalfKeys * hf;
+      const uint32_t half = stage + (uint32_t)(kHalfKeys * hf * kDim);
 
-    // B operand of key group u: key 16u + col, logical chunks 2g, 2g + 1.
-    auto load_b = [&](int u) -> v8i {
-      const int key = 16 * u + col;
-      const uint32_t base = stage + key * kDim;
-      const v4u lo = *(const v4u __attribute__((address_space(3)))*)(uintptr_t)(base + (((2 * group) ^ (key & 7)) << 4));
-      const v4u hi = *(const v4u __attribute__((address_space(3)))*)(uintptr_t)(base + (((2 * group + 1) ^ (key & 7)) << 4));
-      return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-    };
-
-    // Units i = 4u + j (key group u, query j): the MFMAs of unit i are issued
-    // before the epilogue of unit i - 1.
-    constexpr int kUnits = 4 * kQueriesPerWave;
-    float part[kQueriesPerWave][4];
-    v8i b[2];
-    b[0] = load_b(0);
-    b[1] = load_b(1);
-    v4f acc[2][4];
-    v4f acc_lin[2];  // linear half of key group u (parity u & 1), all four queries
-    auto mfmas = [&](int i) {
-      const int u = i / kQueriesPerWave, j = i % kQueriesPerWave;
+      // B operand of key group u: key 16u + col of the pass, logical chunks 2g,
+      // 2g + 1 (the swizzle by key & 7 is the same within the stage).
+      auto load_b = [&](int u) -> v8i {
+        const int key = 16 * u + col;
+        const uint32_t base = half + key * kDim;
+        const v4u lo = lds_v4u(base + (((2 * group) ^ (key & 7)) << 4));
+        const v4u hi = lds_v4u(base + (((2 * group + 1) ^ (key & 7)) << 4));
+        return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+      };
+      // Units i = 4u + j (key group u, query j): the MFMAs of unit i are issued
+      // before the epilogue of unit i - 1.
+      constexpr int kUnits = 4 * kQueriesPerWave;
+      float part[kQueriesPerWave][4];
+      v8i b[2];
+      b[0] = load_b(0);
+      b[1] = load_b(1);
+      v4f acc[2][4];
+      v4f acc_lin[2];  // linear half of key group u (parity u & 1), all four queries
+      auto mfmas = [&](int i) {
+        const int u = i / kQueriesPerWave, j = i % kQueriesPerWave;
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
-        acc[i & 1][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-            qa[j][t], b[u & 1], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0, 0, 0, 0);
-      if (j == 0)
-        acc_lin[u & 1] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-            qd, b[u & 1], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0, 0, 0, 0);
-    };
-    auto epilogue = [&](int i) {
-      const int u = i / kQueriesPerWave, j = i % kQueriesPerWave;
-      // relu(s) w = (|s| + s) w / 2: the |s| half here, one FMA per head
-      // (wt holds w / 2), four independent chains (one per head tile); the
-      // s half is the linear MFMA's share of this lane.
-      float pt[4];
+        for (int t = 0; t < 4; ++t)
+          acc[i & 1][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              qa[j][t], b[u & 1], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0, 0, 0, 0);
+        if (j == 0)
+          acc_lin[u & 1] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              qd, b[u & 1], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0, 0, 0, 0);
+      };
+      auto epilogue = [&](int i) {
+        const int u = i / kQueriesPerWave, j = i % kQueriesPerWave;
+        // relu(s) w = (|s| + s) w / 2: the |s| half here, one FMA per head
+        // (wt holds w / 2), four independent chains (one per head tile); the
+        // s half is the linear MFMA's share of this lane.
+        float pt[4];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) pt[t] = fabsf(acc[i & 1][t][0]) * wt[j][4 * t];
+        for (int t = 0; t < 4; ++t) pt[t] = fabsf(acc[i & 1][t][0]) * wt[j][4 * t];
 #pragma unroll
-      for (int r = 1; r < 4; ++r)
+        for (int r = 1; r < 4; ++r)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) pt[t] = fmaf(fabsf(acc[i & 1][t][r]), wt[j][4 * t + r], pt[t]);
-      float p = (pt[0] + pt[1]) + (pt[2] + pt[3]);
-      p = fmaf(acc_lin[u & 1][j], fl[j], p);
-      // Pins the epilogue here: otherwise instruction selection sinks it below
-      // every MFMA of the stage and all 64 results stay live.
-      asm volatile("" : "+v"(p));
-      part[j][u] = p;
-    };
-    mfmas(0);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 1; i < kUnits; ++i) {
-      mfmas(i);
-      // b[u & 1] is free once the last query of group u has its MFMAs issued.
-      const bool refill = i % kQueriesPerWave == kQueriesPerWave - 1 && i / kQueriesPerWave + 2 < 4;
-      if (refill) b[(i / kQueriesPerWave) & 1] = load_b(i / kQueriesPerWave + 2);
-      epilogue(i - 1);
-      // One MFMA, then the FMAs of one accumulator of the previous unit,
-      // four times (five MFMAs with a key group's linear one): the results
-      // read were issued a full unit earlier, and the VALU work runs under
-      // the MFMAs.
-      if (refill) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      if (i % kQueriesPerWave == 0) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
-      }
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
-      }
+          for (int t = 0; t < 4; ++t) pt[t] = fmaf(fabsf(acc[i & 1][t][r]), wt[j][4 * t + r], pt[t]);
+        float p = (pt[0] + pt[1]) + (pt[2] + pt[3]);
+        p = fmaf(acc_lin[u & 1][j], fl[j], p);
+        // Pins the epilogue here: otherwise instruction selection sinks it below
+        // every MFMA of the stage and all 64 results stay live.
+        asm volatile("" : "+v"(p));
+        part[j][u] = p;
+      };
+      mfmas(0);
       __builtin_amdgcn_sched_barrier(0);
-    }
-    epilogue(kUnits - 1);
-
-    const int32_t key = (int32_t)(key0 + lane);
-    const float ks = *(const float __attribute__((address_space(3)))*)(uintptr_t)(stage + kKBytes + 4 * lane);
 #pragma unroll
-    for (int j = 0; j < kQueriesPerWave; ++j) {
-      const float total = reduce_scatter4(part[j]);
-      const bool visible = key >= qs[j] && key < qe[j];
-      const float v = visible ? total * ks : neg_inf;
-      if (wave == 0) {
-        staged[s & 1][j][lane] = v;
-      } else if (qw + j < rows && key < ke) {
-        out[(qw + j) * ldo + key] = v;
+      for (int i = 1; i < kUnits; ++i) {
+        mfmas(i);
+        // b[u & 1] is free once the last query of group u has its MFMAs issued.
+        const bool refill = i % kQueriesPerWave == kQueriesPerWave - 1 && i / kQueriesPerWave + 2 < 4;
+        if (refill) b[(i / kQueriesPerWave) & 1] = load_b(i / kQueriesPerWave + 2);
+        epilogue(i - 1);
+        // One MFMA, then the FMAs of one accumulator of the previous unit,
+        // four times (five MFMAs with a key group's linear one): the results
+        // read were issued a full unit earlier, and the VALU work runs under
+        // the MFMAs.
+        if (refill) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        if (i % kQueriesPerWave == 0) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      epilogue(kUnits - 1);
+
+      const int32_t key = (int32_t)(key0 + lane);
+      const float ks = *(const float __attribute__((address_space(3)))*)(uintptr_t)(
+          stage + kKBytes + 4 * (kHalfKeys * hf + lane));
+#pragma unroll
+      for (int j = 0; j < kQueriesPerWave; ++j) {
+        const float total = reduce_scatter4(part[j]);
+        const bool visible = key >= qs[j] && key < qe[j];
+        const float v = visible ? total * ks : neg_inf;
+        if (wave == 0) {
+          staged[s & 1][j][kHalfKeys * hf + lane] = v;
+        } else if (qw + j < rows && key < ke) {
+          out[(qw + j) * ldo + key] = v;
+        }
       }
     }
   }
