@@ -81,11 +81,7 @@ __device__ __forceinline__ void wait_dma() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kOutstanding) : "memory");
 }
 
-__device__ __forceinline__ void dma16(const void* src, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-               ::"s"(lds_base), "v"(src) : "memory", "m0");
-}
-// Scalar-base forms: 16 or 4 bytes per lane from base + off (32-bit lane
+// LDS DMA, scalar base: 16 or 4 bytes per lane from base + off (32-bit lane
 // offset) to lds_base + 16 l or + 4 l.
 __device__ __forceinline__ void dma16_s(const void* base, uint32_t off, uint32_t lds_base) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
