@@ -10,29 +10,33 @@
 //
 // Mapping (gfx950, wave64). A work-group owns one query row and 64 heads
 // and walks the selection in blocks of 32 keys with 4 waves, one per SIMD,
-// in two roles, so that the matrix work of one role runs beside the
-// conversion and LDS stores of the other (MFMA and VALU work of one wave
-// serialise on its SIMD):
+// in two roles:
 // * Score waves 0 and 1 compute S^T = K Q^T for all 32 keys and heads
 //   32 sw .. 32 sw + 31 with v_mfma_f32_32x32x16_bf16 (Q^T of their 32 heads
-//   stays in AGPRs, 144 registers), then the online softmax of their heads,
-//   writing P^T (bf16) and the per-head rescale factors to LDS.
+//   stays in registers, 144 of them, as the B operand), and the online
+//   softmax of their heads, writing P^T (bf16) and per-head rescale factors
+//   to LDS.
 // * Load waves 2 and 3 stage the records: lane (kk, j) (kk = 16 (w - 2) +
 //   lane / 4, j = lane % 4) loads a quarter of key kk's record with 16-byte
-//   loads, kLookahead blocks ahead, and converts it into bf16 rows of one of
-//   three LDS buffers the step before the block is scored (fp8 records by
-//   v_cvt_scalef32_pk_bf16_fp8 with their tile scales; e4m3 x 2^k is exact in
-//   bf16). Conversion happens once per key, not once per wave that reads it.
-// * After the block's barrier all four waves accumulate O^T += V^T P^T
-//   (v_mfma_f32_16x16x32_bf16) over all 64 heads: score waves for 48 dims
-//   each, load waves for 208 each, which evens out the two roles' time per
-//   block. V^T comes from ds_read_b64_tr_b16: lane 4 jj + qq of row group g
-//   addresses key 2 jj + 8 (g & 1) + (g >> 1) (and + 16) at dims d0 + 4 qq.
-// * Row sums come out of the same MFMA pipe: wave w adds P^T of head tile w
-//   against a row of ones, so l sums exactly the bf16 P the product used.
-// A buffer written in step b - 1 is read by the scores of block b and,
-// after that block's barrier, by its PV product, hence three buffers; P and
-// the rescale factors are double buffered by block parity.
+//   loads, kLookahead blocks ahead, and converts it into bf16 rows of a
+//   block buffer in LDS (fp8 records by v_cvt_scalef32_pk_bf16_fp8 with
+//   their tile scales; e4m3 x 2^k is exact in bf16), once per key.
+// * All four accumulate O^T += V^T P^T (v_mfma_f32_16x16x32_bf16, V^T from
+//   ds_read_b64_tr_b16) over all 64 heads: score waves for 96 dims each,
+//   load waves for 160 each. Row sums come from the same MFMA pipe: each
+//   wave adds P^T of one head tile against a row of ones, so l sums exactly
+//   the bf16 P the product used.
+// The work is software-pipelined so that every wave has matrix work and
+// independent VALU / LDS work in the same step, which its SIMD runs side by
+// side (the code issues them interleaved): in step `it` the score waves
+// compute S(it) and the softmax of block it - 1 (its scores kept in
+// registers) and the PV product of block it - 2; the load waves convert the
+// rows of block it + 1 and run the PV product of block it - 2. One barrier
+// per step; four block buffers (S reads it, PV reads it - 2, it + 1 is
+// written); P and the rescale factors are double buffered by block parity.
+// The physical rows of the selection live in a ring of 8 blocks in LDS that
+// the load waves keep 6 blocks ahead (the id and page-table loads issued
+// two and one steps before use, ahead of the record loads).
 //
 // Online softmax in log2 units with lazy rescaling (only when a block raises
 // a head's running max by more than 8, so p <= 2^8).
@@ -75,9 +79,13 @@ struct Format {
 // even (or odd) keys of a V^T transpose read on disjoint 8-bank windows.
 constexpr int kRowBytes = kQkDim * 2 + 16;
 constexpr int kBufBytes = kBlock * kRowBytes;
-constexpr int kBuffers = 3;
+constexpr int kBuffers = 4;
+// Physical rows of the selected keys, by block, in a ring of kRing blocks
+// filled kRingAhead blocks ahead of the block being scored.
+constexpr int kRing = 8;
+constexpr int kRingAhead = 6;
 // 16-dim tiles of O^T per score wave and per load wave (two of each).
-constexpr int kScoreDimTiles = 3;
+constexpr int kScoreDimTiles = 6;
 constexpr int kLoadDimTiles = (kVDim / 16 - 2 * kScoreDimTiles) / 2;
 
 struct __align__(16) Lds {
@@ -88,7 +96,7 @@ struct __align__(16) Lds {
   uint8_t p[2][4][64][16];
   float alpha[2][kHeadsPerGroup];  // per-head rescale factor of the block, by parity
   float row_sum[kHeadsPerGroup];
-  int32_t rows[kMaxSelected];  // physical record row per selected position, -1 = padding
+  int32_t ring[kRing][kBlock];  // block b at slot b % kRing: record row per key, -1 = padding
 };
 
 // Key order inside a block. Row m = 8a + 4h + i of the 32x32 score tile holds
@@ -117,24 +125,6 @@ __device__ __forceinline__ uint32_t dequant_pair(uint32_t word, float scale) {
 }
 
 typedef float v16f __attribute__((ext_vector_type(16)));
-
-// acc += a b with the 32x32x16 bf16 MFMA, b (Q^T) pinned to AGPRs: Q^T of 32
-// heads (144 registers) does not fit the VGPRs beside the O accumulators, and
-// as a compiler-chosen spill it is copied back into an aligned tuple before
-// every use. As inline assembly the MFMA is invisible to the hazard
-// recognizer, so it covers its own wait states: the leading s_nop 1 gives the
-// 2 required after a VALU write of `a` or `acc`; back-to-back MFMAs into the
-// same accumulator need none; the reader of the final accumulator waits with
-// mfma_drain32().
-__device__ __forceinline__ void mfma32_qb(v16f& acc, v8bf a, v8bf b) {
-  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "a"(b));
-}
-// Wait states between the last inline-assembly MFMA and any read of its
-// results (more than the 18 a 16-pass XDL op needs). The accumulator is an
-// operand, so no read of it can be scheduled above the wait.
-__device__ __forceinline__ void mfma_drain32(v16f& a) {
-  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(a));
-}
 
 typedef v4s __attribute__((address_space(3))) * lds_v4s;
 
@@ -173,28 +163,27 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
   // takes two per trip; a padding block has no valid key and adds nothing).
   const int n_blocks = (int)((topk + 2 * kBlock - 1) / (2 * kBlock)) * 2;
 
-  // Physical record row of selected position i; -1 for padding, an id
-  // outside [0, n_tokens) or a page outside the cache.
-  auto phys_of = [&](int i) -> int32_t {
-    int32_t phys = -1;
-    if (i < topk) {
-      const int64_t id = ids[i];
-      if (id >= 0 && id < n_tokens) {
-        if (kFp8) {
-          const int64_t page = page_table[id / kPageTokens];
-          if (page >= 0 && page < pages) phys = (int32_t)(page * kPageTokens + id % kPageTokens);
-        } else {
-          phys = (int32_t)id;
-        }
-      }
-    }
-    return phys;
+  // Selected id of key `key` of block b (-1 past the selection), its page
+  // and its physical record row (-1 for padding, an id outside [0, n_tokens)
+  // or a page outside the cache).
+  auto id_at = [&](int bl, int key) -> int32_t {
+    const int i = bl * kBlock + key;
+    return bl < n_blocks && i < topk ? ids[i] : -1;
+  };
+  auto page_of = [&](int32_t id) -> int32_t {
+    if (!kFp8) return 0;
+    return id >= 0 && id < n_tokens ? page_table[id / kPageTokens] : -1;
+  };
+  auto phys_from = [&](int32_t id, int32_t page) -> int32_t {
+    if (id < 0 || id >= n_tokens) return -1;
+    if (!kFp8) return id;
+    return page >= 0 && page < pages ? (int32_t)((int64_t)page * kPageTokens + id % kPageTokens) : -1;
   };
 
   // Roles: waves 0 and 1 score (32 heads each, all 32 keys of a block, with
-  // 32x32x16 MFMAs) and run the softmax; waves 2 and 3 stage the records of
-  // the next block (HBM -> registers -> bf16 rows in LDS). All four then
-  // accumulate O^T for their share of the 512 dims over all 64 heads.
+  // 32x32x16 MFMAs) and run the softmax; waves 2 and 3 stage the records
+  // (HBM -> registers -> bf16 rows in LDS). All four accumulate O^T for their
+  // share of the 512 dims over all 64 heads.
   const bool scorer = wave < 2;
   const int sw = wave & 1;           // score wave: heads 32 sw .. + 31
   const int n = lane & 31;           // score lane: head 32 sw + n
@@ -218,25 +207,26 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
   // Load role: key kk of each block, quarter j of its record.
   const int kk = 16 * (wave & 1) + (lane >> 2);
   const int j = lane & 3;
-  const uint32_t rows_base = (uint32_t)(uintptr_t)&lds.rows[0];
+  const uint32_t ring_base = (uint32_t)(uintptr_t)&lds.ring[0][0];
   const uint32_t kv_base = (uint32_t)(uintptr_t)&lds.kv[0][0];
   const uint32_t p_base = (uint32_t)(uintptr_t)&lds.p[0][0][0][0];
+  auto buf_of = [&](int bl) -> uint32_t { return kv_base + (uint32_t)(bl & (kBuffers - 1)) * kBufBytes; };
 
-  // Per-block base addresses are formed once and hidden from the optimizer:
-  // otherwise it hoists (lane offset + constant) out of the loop and pays an
-  // add per LDS access instead of using the instruction's offset field.
+  // Per-block base addresses are formed once and hidden from the optimizer
+  // (an identity DPP move it cannot see through): otherwise it hoists (lane
+  // offset + constant) out of the loop and pays an add per LDS access instead
+  // of using the instruction's offset field. Unlike an empty asm statement it
+  // does not cut the scheduling region.
   auto lane_base = [](uint32_t buf, uint32_t lane_off) -> uint32_t {
-    uint32_t a = buf + lane_off;
-    asm volatile("" : "+v"(a));
-    return a;
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(buf + lane_off), 0xE4, 0xF, 0xF, false);
+  };
+  auto row_of = [&](int bl) -> int32_t {
+    return bl < n_blocks ? lds_load<int32_t>(ring_base + 4 * (uint32_t)((bl % kRing) * kBlock + kk)) : -1;
   };
   // Block b's record bytes of this lane -> registers. Blocks past the end
   // (and invalid ids) read the zero record, so the load count per block is
   // fixed. fp8 latent loads i cover record bytes 64i + 16j (64 contiguous
   // bytes per key and instruction); bf16 loads 2i + u cover 128i + 32j + 16u.
-  auto row_of = [&](int b) -> int32_t {
-    return b < n_blocks ? lds_load<int32_t>(rows_base + 4 * (uint32_t)(b * kBlock + kk)) : -1;
-  };
   auto fetch = [&](auto set, int32_t phys) __attribute__((always_inline)) {
     v4u* st = pool + decltype(set)::value;
     const uint8_t* rec = phys >= 0 ? kv + (int64_t)phys * F::kRecordBytes : zero_record;
@@ -301,166 +291,293 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
   constexpr int kLookahead = kFp8 ? 3 : 2;
   using Set0 = std::integral_constant<int, 0>;
   using Set1 = std::integral_constant<int, kFp8 ? F::kLoads : 0>;
-  // Prologue: the rows table of all positions, blocks 0 .. kLookahead - 1
-  // requested and block 0 converted. In the loop the row of the next block
-  // to fetch is read from the table one step ahead.
-  for (int i = threadIdx.x; i < n_blocks * kBlock; i += kThreads) lds.rows[i] = phys_of(i);
-  __syncthreads();  // rows table
+
+  // Prologue: the rows of blocks 0 .. kRingAhead - 1 into the ring; the load
+  // waves then keep it kRingAhead blocks ahead (lane: key kk). The id and
+  // page loads are branch-free (clamped addresses, out-of-range results
+  // replaced).
+  for (int t = threadIdx.x; t < kRingAhead * kBlock; t += kThreads) {
+    const int32_t id = id_at(t / kBlock, t % kBlock);
+    lds.ring[t / kBlock][t % kBlock] = phys_from(id, page_of(id));
+  }
+  auto id_load = [&](int bl) -> int32_t {
+    const int i = bl * kBlock + kk;
+    const bool in = bl < n_blocks && i < topk;
+    const int32_t id = ids[in ? i : 0];
+    return in ? id : -1;
+  };
+  auto page_load = [&](int32_t id) -> int32_t {
+    if (!kFp8) return 0;
+    const bool in = id >= 0 && id < n_tokens;
+    const int32_t page = page_table[in ? id / kPageTokens : 0];
+    return in ? page : -1;
+  };
+  int32_t ring_id[2] = {-1, -1}, ring_page[2] = {-1, -1};
+  if (!scorer) {
+    ring_id[0] = id_load(kRingAhead);
+    ring_id[1] = id_load(kRingAhead + 1);
+    ring_page[1] = page_load(ring_id[0]);
+  }
+  __syncthreads();  // ring
   int32_t phys_next = -1;
   if (!scorer) {
     fetch(Set0{}, row_of(0));
     if (kFp8) fetch(Set1{}, row_of(1));
-    unpack(Set0{}, kv_base);
+    unpack(Set0{}, buf_of(0));
     fetch(Set0{}, row_of(kLookahead - 1));
     phys_next = row_of(kLookahead);
   }
   lds_barrier();
 
-  int buf_cur = 0;  // buffer of block it
-  // kScore is the wave's role, a compile-time constant of each of the two
-  // loops below: with one loop per role the wait-count pass sees only that
-  // role's loads and waits for exactly the set being unpacked.
-  // ka: the first kAheadK K operands of block it, read before the step (in
-  // the previous step's PV phase: block it + 1's rows are complete once
-  // block it's barrier has passed).
-  constexpr int kAheadK = 6;
-  auto k_prefetch = [&](v4u (&ka)[kAheadK], uint32_t buf) __attribute__((always_inline)) {
-    const uint32_t kbase = lane_base(buf, k_lane);
-#pragma unroll
-    for (int d = 0; d < kAheadK; ++d) ka[d] = lds_load<v4u>(kbase + 32 * d);
-  };
-  auto step = [&](int it, auto set, auto role, auto& o, v4u (&ka)[kAheadK]) __attribute__((always_inline)) {
+  // Software pipeline, one barrier per step. Step `it`:
+  //   score waves: S(it) = K Q^T of block it, the softmax of block it - 1
+  //     (its scores kept in registers from the previous step), the PV
+  //     product of block it - 2 for their dims;
+  //   load waves: rows of block it + 1 into LDS, records of block
+  //     it + kLookahead into registers, the PV product of block it - 2.
+  // Each wave thus has matrix work (S, PV) and independent VALU / LDS work
+  // (softmax, conversion and row stores) in the same step, which the SIMD
+  // runs side by side. Buffers: S reads it, PV reads it - 2, the load waves
+  // write it + 1 (last read by PV(it - 3), before the previous barrier): four
+  // buffers. P and the rescale factors of block b sit at parity b & 1.
+  auto step = [&](int it, auto set, auto parity, auto role, auto parts, auto& o, v16f& s_prev)
+                  __attribute__((always_inline)) {
     constexpr bool kScore = decltype(role)::value;
+    constexpr int kParts = decltype(parts)::value;
+    constexpr bool kS = (kParts & 1) != 0;     // score waves: S(it); load waves: rows of it + 1
+    constexpr bool kSoft = (kParts & 2) != 0;  // score waves: softmax(it - 1)
+    constexpr bool kPV = (kParts & 4) != 0;    // PV(it - 2)
     constexpr int kM = kScore ? kScoreDimTiles : kLoadDimTiles;
-    const uint32_t buf = kv_base + (uint32_t)buf_cur * kBufBytes;
-    const int buf_next_i = buf_cur + 1 == kBuffers ? 0 : buf_cur + 1;
-    const uint32_t parity = (uint32_t)(it & 1);
 
-    if constexpr (kScore) {
-      // ---- S^T = K Q^T: 32 keys x heads 32 sw .. + 31, 36 k-steps of 16
-      // dims accumulated back to back.
-      // Valid keys of the block (bit = key), read ahead of the MFMAs.
-      const int32_t prow = lds_load<int32_t>(rows_base + 4 * (uint32_t)(it * kBlock + n));
-      v16f sa = {};
-      const uint32_t kbase = lane_base(buf, k_lane);
-#pragma unroll
-      for (int ks = 0; ks < kQkDim / 16; ++ks) {
-        const v8bf a = as_v8bf(ka[ks % kAheadK]);
-        if (ks + kAheadK < kQkDim / 16) ka[ks % kAheadK] = lds_load<v4u>(kbase + 32 * (ks + kAheadK));
-        mfma32_qb(sa, a, as_v8bf(pool[ks]));
-      }
-      const uint32_t vmask = (uint32_t)__builtin_amdgcn_ballot_w64(h == 0 && prow >= 0);
-      mfma_drain32(sa);
-
-      // ---- online softmax of head 32 sw + n over the block: this lane holds
-      // keys score_key(8(r / 4) + 4h + r % 4), the other half (lane ^ 32)
-      // the rest. Maxima are taken on raw scores (scale_log2 > 0) and invalid
-      // keys become -inf, so p = exp2(s * scale_log2 - m) is one FMA and one
-      // exp2. Row sums are not formed here: the PV product adds P^T against a
-      // row of ones (the same bf16 P, so O / l is a weighted mean of V).
-      float sc[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sc[r] = sa[r];
-      if (vmask != 0xFFFFFFFFu) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = score_key(8 * (r >> 2) + 4 * h + (r & 3));
-          sc[r] = (vmask >> key) & 1u ? sc[r] : neg_inf;
-        }
-      }
-      float mx = fmaxf(fmaxf(sc[0], sc[1]), sc[2]);
-#pragma unroll
-      for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, sc[r]), sc[r + 1]);
-      mx = fmaxf(mx, sc[15]);
-      {
-        const uint32_t u = __float_as_uint(mx);
-        const auto sw32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-        mx = fmaxf(__uint_as_float(sw32[0]), __uint_as_float(sw32[1])) * scale_log2;
-      }
-      const bool need = mx > m_run + kRescaleThreshold || (m_run == neg_inf && mx != neg_inf);
-      const float m_new = need ? fmaxf(m_run, mx) : m_run;
-      // exp2(-inf) = 0 covers the first valid block.
-      const float alpha = need ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
-      m_run = m_new;
-      // With no valid key so far every score is -inf and p = exp2(-inf) = 0.
-      const float neg_m = m_run == neg_inf ? 0.0f : -m_run;
-      uint32_t pk[8];
-#pragma unroll
-      for (int r = 0; r < 16; r += 2)
-        pk[r / 2] = pack_bf16(__builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], scale_log2, neg_m)),
-                              __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r + 1], scale_log2, neg_m)));
-      if (h == 0) lds.alpha[parity][32 * sw + n] = alpha;
-      // P^T -> LDS: registers 4a' .. 4a' + 3 are k-indices 4(a' >> 1) .. +3 of
-      // operand slot (c = n % 16, g = 2h + (a' & 1)) of head tile 2 sw + n / 16.
-      const uint32_t p_tile = p_base + parity * 4096 + (uint32_t)((2 * sw + (n >> 4)) * 64 + (n & 15)) * 16;
-#pragma unroll
-      for (int ap = 0; ap < 4; ++ap) {
-        const int gg = 2 * h + (ap & 1);
-        lds_store<v2u>(p_tile + (uint32_t)gg * 256 + 8 * (ap >> 1), v2u{pk[2 * ap], pk[2 * ap + 1]});
-      }
-    } else {
-      // ---- block it + 1 -> bf16 rows (its buffer last held block it - 2,
-      // whose readers all passed the previous barrier); block
-      // it + kLookahead -> the freed registers.
-      unpack(set, kv_base + (uint32_t)buf_next_i * kBufBytes);
-      fetch(set, phys_next);
-      phys_next = row_of(it + kLookahead + 1);
-    }
-    // The first V^T operands of this block (its rows are complete since the
-    // previous barrier) are read before the barrier.
-    const uint32_t vbase = lane_base(buf, v_lane);
-    auto v_addr = [&](int m) -> uint32_t { return vbase + 32 * m; };
-    constexpr int kAhead = 2;
-    v4s vlo[kAhead], vhi[kAhead];
-#pragma unroll
-    for (int d = 0; d < kAhead; ++d) {
-      vlo[d] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)v_addr(d));
-      vhi[d] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)(v_addr(d) + kHalf));
-    }
-    lds_barrier();  // P, alpha and block it + 1's rows visible
-
-    // ---- O^T += V^T P^T for dims dim0 .. dim0 + 16 kM - 1, all 64 heads.
-    // Reads first (rescale factors, P^T, then the score waves' first K
-    // operands of block it + 1), then the rescale of O^T if any head's
-    // running max rose.
+    // ---- the step's first LDS reads, before any wait or branch: block
+    // it - 2's rescale factors, block it - 1's padding mask, P^T of the four
+    // head tiles (and of this wave's tile for its row sums), the first V^T
+    // operands (two ds_read_b64_tr_b16 per 16-dim tile, kAheadV tiles ahead)
+    // and the first K operands of S(it).
+    const uint32_t par_pv = (uint32_t)(it & 1);
+    // Load waves read all their V^T operands up front: their row stores
+    // later in the step would otherwise sit ahead of V^T reads in the LDS.
+    constexpr int kAheadV = kScore ? 2 : kLoadDimTiles;
+    constexpr int kAheadK = 6;
     float al[4];
+    int32_t prow = 0;
+    v8bf pb[4], p_own;
+    v4s vlo[kAheadV], vhi[kAheadV];
+    v4u ka[kAheadK];
+    uint32_t vbase = 0, kbase = 0;
+    if constexpr (kPV) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) al[t] = lds.alpha[parity][16 * t + c];
-    v8bf pb[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-      pb[t] = as_v8bf(lds_load<v4u>(p_base + parity * 4096 + (uint32_t)(t * 64 + lane) * 16));
-    const v8bf p_own = as_v8bf(lds_load<v4u>(p_base + parity * 4096 + (uint32_t)(wave * 64 + lane) * 16));
-    if constexpr (kScore) k_prefetch(ka, kv_base + (uint32_t)buf_next_i * kBufBytes);
-    bool rescale = false;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) rescale |= al[t] != 1.0f;
-    if (__builtin_amdgcn_ballot_w64(rescale)) {
+      for (int t = 0; t < 4; ++t) al[t] = lds.alpha[par_pv][16 * t + c];
+    }
+    if constexpr (kScore && kSoft)
+      prow = lds_load<int32_t>(ring_base + 4 * (uint32_t)(((it - 1) % kRing) * kBlock + n));
+    if constexpr (kPV) {
 #pragma unroll
       for (int t = 0; t < 4; ++t)
+        pb[t] = as_v8bf(lds_load<v4u>(p_base + par_pv * 4096 + (uint32_t)(t * 64 + lane) * 16));
+      p_own = as_v8bf(lds_load<v4u>(p_base + par_pv * 4096 + (uint32_t)(wave * 64 + lane) * 16));
+      vbase = lane_base(buf_of(it - 2), v_lane);
 #pragma unroll
-        for (int m = 0; m < kM; ++m) o[t][m] *= al[t];
-      l_acc *= lds.alpha[parity][16 * wave + c];
+      for (int d = 0; d < kAheadV; ++d) {
+        vlo[d] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)(vbase + 32 * d));
+        vhi[d] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)(vbase + 32 * d + kHalf));
+      }
     }
-    {
-      const v4u ones = v4u{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
-      l_acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(ones), p_own, l_acc, 0, 0, 0);
-    }
+    if constexpr (kScore && kS) {
+      kbase = lane_base(buf_of(it), k_lane);
 #pragma unroll
-    for (int m = 0; m < kM; ++m) {
-      const v8bf a = __builtin_bit_cast(
-          v8bf, __builtin_shufflevector(vlo[m % kAhead], vhi[m % kAhead], 0, 1, 2, 3, 4, 5, 6, 7));
-      if (m + kAhead < kM) {
-        vlo[m % kAhead] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)v_addr(m + kAhead));
-        vhi[m % kAhead] =
-            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)(v_addr(m + kAhead) + kHalf));
+      for (int d = 0; d < kAheadK; ++d) ka[d] = lds_load<v4u>(kbase + 32 * d);
+    }
+
+    // The step's two data-dependent checks, placed after some independent
+    // work so that their LDS reads have landed: rescale O^T (and the row
+    // sums) by block it - 2's factors if any head's running max rose, and
+    // turn the padding keys of block it - 1 into -inf before its softmax.
+    auto checks = [&]() __attribute__((always_inline)) {
+      if constexpr (kPV) {
+        bool rescale = false;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) rescale |= al[t] != 1.0f;
+        if (__builtin_amdgcn_ballot_w64(rescale)) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int m = 0; m < kM; ++m) o[t][m] *= al[t];
+          l_acc *= lds.alpha[par_pv][16 * wave + c];
+        }
+      }
+      if constexpr (kScore && kSoft) {
+        const uint32_t vmask = (uint32_t)__builtin_amdgcn_ballot_w64(h == 0 && prow >= 0);
+        if (vmask != 0xFFFFFFFFu) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = score_key(8 * (r >> 2) + 4 * h + (r & 3));
+            s_prev[r] = (vmask >> key) & 1u ? s_prev[r] : neg_inf;
+          }
+        }
+      }
+    };
+    // PV MFMA number k of this step (k < 4 kM: dim tile k / 4, head tile
+    // k % 4; k = 4 kM: the row sums of this wave's head tile).
+    auto pv_mfma = [&](int k) __attribute__((always_inline)) {
+      if (k == 4 * kM) {
+        const v4u ones = v4u{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+        l_acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_v8bf(ones), p_own, l_acc, 0, 0, 0);
+        return;
+      }
+      const int m = k >> 2, t = k & 3;
+      const v8bf va = __builtin_bit_cast(
+          v8bf, __builtin_shufflevector(vlo[m % kAheadV], vhi[m % kAheadV], 0, 1, 2, 3, 4, 5, 6, 7));
+      o[t][m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[t], o[t][m], 0, 0, 0);
+      if (t == 3 && m + kAheadV < kM) {
+        vlo[m % kAheadV] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)(vbase + 32 * (m + kAheadV)));
+        vhi[m % kAheadV] =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(uintptr_t)(vbase + 32 * (m + kAheadV) + kHalf));
+      }
+    };
+    constexpr int kPvMfmas = kPV ? 4 * kM + 1 : 0;
+
+    if constexpr (kScore) {
+      // ---- S(it) = K Q^T (32 keys x heads 32 sw .. + 31, 36 k-steps of 16
+      // dims, back to back), the PV MFMAs and the softmax of block it - 1 in
+      // one instruction stream: each k-step issues its MFMA(s), then a slice
+      // of the softmax's VALU work, which runs while the MFMAs execute.
+      //
+      // Softmax of head 32 sw + n: this lane holds keys score_key(8(r / 4) +
+      // 4h + r % 4), the other half (lane ^ 32) the rest. Maxima on raw
+      // scores (scale_log2 > 0), so that p = exp2(s * scale_log2 - m) is one
+      // FMA and one exp2. Row sums come from the PV product (P^T against a
+      // row of ones).
+      v16f sa = {};
+      float mx = neg_inf, alpha = 1.0f, neg_m = 0.0f;
+      uint32_t pk[8];
+      const uint32_t par_soft = (uint32_t)((it - 1) & 1);
+      auto soft_slice = [&](int ks) __attribute__((always_inline)) {
+        if (ks < 8) {
+          mx = fmaxf(fmaxf(mx, s_prev[2 * ks]), s_prev[2 * ks + 1]);
+        } else if (ks == 8) {
+          const uint32_t u = __float_as_uint(mx);
+          const auto sw32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+          mx = fmaxf(__uint_as_float(sw32[0]), __uint_as_float(sw32[1])) * scale_log2;
+          const bool need = mx > m_run + kRescaleThreshold || (m_run == neg_inf && mx != neg_inf);
+          const float m_new = need ? fmaxf(m_run, mx) : m_run;
+          // exp2(-inf) = 0 covers the first valid block.
+          alpha = need ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+          m_run = m_new;
+          // With no valid key so far every score is -inf and p = 0.
+          neg_m = m_run == neg_inf ? 0.0f : -m_run;
+        } else if (ks < 17) {
+          const int r = 2 * (ks - 9);
+          pk[ks - 9] = pack_bf16(__builtin_amdgcn_exp2f(__builtin_fmaf(s_prev[r], scale_log2, neg_m)),
+                                 __builtin_amdgcn_exp2f(__builtin_fmaf(s_prev[r + 1], scale_log2, neg_m)));
+        } else if (ks == 17) {
+          // Both row halves hold the same factor; both write it.
+          lds.alpha[par_soft][32 * sw + n] = alpha;
+          // P^T -> LDS: registers 4a' .. 4a' + 3 are k-indices 4(a' >> 1) ..
+          // +3 of operand slot (c = n % 16, g = 2h + (a' & 1)) of head tile
+          // 2 sw + n / 16.
+          const uint32_t p_tile = p_base + par_soft * 4096 + (uint32_t)((2 * sw + (n >> 4)) * 64 + (n & 15)) * 16;
+#pragma unroll
+          for (int ap = 0; ap < 4; ++ap) {
+            const int gg = 2 * h + (ap & 1);
+            lds_store<v2u>(p_tile + (uint32_t)gg * 256 + 8 * (ap >> 1), v2u{pk[2 * ap], pk[2 * ap + 1]});
+          }
+        }
+      };
+      // The first kHead k-steps run S alone (the checks' reads land
+      // meanwhile); then PV MFMAs and softmax slices join.
+      constexpr int kHead = kS ? 6 : 0;
+      constexpr int kBody = kPvMfmas > 18 ? kPvMfmas : 18;
+      constexpr int kSteps = kS ? kQkDim / 16 : kBody;
+      if constexpr (kHead == 0) checks();
+#pragma unroll
+      for (int ks = 0; ks < kSteps; ++ks) {
+        if constexpr (kS) {
+          const v8bf a = as_v8bf(ka[ks % kAheadK]);
+          if (ks + kAheadK < kQkDim / 16) ka[ks % kAheadK] = lds_load<v4u>(kbase + 32 * (ks + kAheadK));
+          sa = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, as_v8bf(pool[ks]), sa, 0, 0, 0);
+        }
+        if (kHead > 0 && ks == kHead - 1) checks();
+        const int kb = ks - kHead;
+        if (kb >= 0 && kb < kPvMfmas) pv_mfma(kb);
+        if constexpr (kSoft) {
+          if (kb >= 0) soft_slice(kb);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
-      for (int t = 0; t < 4; ++t) o[t][m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[t], o[t][m], 0, 0, 0);
+      for (int k = kSteps - kHead; k < kPvMfmas; ++k) pv_mfma(k);
+      static_assert(!kS || kQkDim / 16 - kHead >= 18, "softmax slices must fit the S k-steps");
+      if constexpr (kS) s_prev = sa;
+    } else {
+      // ---- rows of block it + 1 (its buffer last held block it - 3) in
+      // eight rounds beside the PV MFMAs; the records of block it +
+      // kLookahead into the freed registers.
+      const uint32_t rec = kS ? lane_base(buf_of(it + 1), (uint32_t)kk * kRowBytes + 32 * j) : 0;
+      const v4u* st = pool + decltype(set)::value;
+      auto unpack_round = [&](int i) __attribute__((always_inline)) {
+        if (kFp8) {
+          const float s_i = __builtin_bit_cast(v4f, st[8])[i >> 1];
+          const v4u w = st[i];
+          const v4u lo{dequant_pair<false>(w.x, s_i), dequant_pair<true>(w.x, s_i),
+                       dequant_pair<false>(w.y, s_i), dequant_pair<true>(w.y, s_i)};
+          const v4u hi{dequant_pair<false>(w.z, s_i), dequant_pair<true>(w.z, s_i),
+                       dequant_pair<false>(w.w, s_i), dequant_pair<true>(w.w, s_i)};
+          lds_store<v4u>(rec + 128 * i, lo);
+          lds_store<v4u>(rec + 128 * i + 16, hi);
+          if (i == 7) {
+            lds_store<v4u>(rec + 2 * kVDim, st[9]);
+            lds_store<v4u>(rec + 2 * kVDim + 16, st[10]);
+          }
+        } else {
+          lds_store<v4u>(rec + 128 * i, st[2 * i]);
+          lds_store<v4u>(rec + 128 * i + 16, st[2 * i + 1]);
+          if (i == 7) {
+            lds_store<v4u>(rec + 2 * kVDim, st[16]);
+            lds_store<v4u>(rec + 2 * kVDim + 16, st[17]);
+          }
+        }
+      };
+      // Two rounds first (the checks' reads land meanwhile), then the PV
+      // MFMAs with the other rounds spread over them.
+      constexpr int kRounds = kS ? 8 : 0;
+      constexpr int kFirst = kRounds > 2 ? 2 : kRounds;
+#pragma unroll
+      for (int r = 0; r < kFirst; ++r) unpack_round(r);
+      checks();
+      constexpr int kLeft = kRounds - kFirst;
+      constexpr int kSpread = kLeft > 0 && kPvMfmas / kLeft > 1 ? kPvMfmas / kLeft : 1;
+      constexpr int kSteps = kPvMfmas > kSpread * kLeft ? kPvMfmas : kSpread * kLeft;
+#pragma unroll
+      for (int k = 0; k < kSteps; ++k) {
+        if (k < kPvMfmas) pv_mfma(k);
+        if (k % kSpread == 0 && k / kSpread < kLeft) unpack_round(kFirst + k / kSpread);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if constexpr (kS) {
+        // Ring: row of block it + kRingAhead (its slot held block it - 2)
+        // from the id loaded two steps and the page loaded one step earlier;
+        // then the page of block it + 7 and the id of block it + 8. These
+        // loads go out before the record loads, so that waiting for them next
+        // step waits for nothing the step does not wait for anyway. Loaded
+        // values live in one register per step parity and are never copied
+        // (a copy would wait for the load); the four lanes of a key store the
+        // same value.
+        constexpr int kP = decltype(parity)::value, kQ = 1 - kP;
+        lds.ring[(it + kRingAhead) % kRing][kk] = phys_from(ring_id[kP], ring_page[kQ]);
+        ring_page[kP] = page_load(ring_id[kQ]);
+        ring_id[kP] = id_load(it + kRingAhead + 2);
+        fetch(set, phys_next);
+        phys_next = row_of(it + kLookahead + 1);
+      }
     }
-    buf_cur = buf_next_i;
+    lds_barrier();
   };
-  // Two blocks per trip so that each register set stays a fixed register set.
+  using Pre0 = std::integral_constant<int, 1>;   // S / rows only
+  using Pre1 = std::integral_constant<int, 3>;   // + softmax
+  using Full = std::integral_constant<int, 7>;   // + PV
+  using Tail0 = std::integral_constant<int, 6>;  // softmax + PV
+  using Tail1 = std::integral_constant<int, 4>;  // PV only
   auto run = [&](auto role) __attribute__((always_inline)) {
     constexpr int kM = decltype(role)::value ? kScoreDimTiles : kLoadDimTiles;
     // O^T: head tile t (heads 16t + c), dims dim0 + 16m + 4g + r.
@@ -469,12 +586,18 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int m = 0; m < kM; ++m) o[t][m] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    v4u ka[kAheadK];
-    if constexpr (decltype(role)::value) k_prefetch(ka, kv_base);
-    for (int it = 0; it < n_blocks; it += 2) {
-      step(it, Set1{}, role, o, ka);
-      step(it + 1, Set0{}, role, o, ka);
+    v16f s_prev = {};
+    using Even = std::integral_constant<int, 0>;
+    using Odd = std::integral_constant<int, 1>;
+    step(0, Set1{}, Even{}, role, Pre0{}, o, s_prev);
+    step(1, Set0{}, Odd{}, role, Pre1{}, o, s_prev);
+    // Two blocks per trip so that each register set stays a fixed register set.
+    for (int it = 2; it < n_blocks; it += 2) {
+      step(it, Set1{}, Even{}, role, Full{}, o, s_prev);
+      step(it + 1, Set0{}, Odd{}, role, Full{}, o, s_prev);
     }
+    step(n_blocks, Set1{}, Even{}, role, Tail0{}, o, s_prev);
+    step(n_blocks + 1, Set0{}, Odd{}, role, Tail1{}, o, s_prev);
     // The fetches past the last block are never read; let them land before
     // the registers are released.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
