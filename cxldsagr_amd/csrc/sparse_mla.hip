@@ -61,7 +61,7 @@ constexpr int kVDim = 512;
 constexpr int kHeadsPerGroup = 64;
 constexpr int kBlock = 32;            // keys per block
 constexpr int kThreads = 256;
-constexpr int kMaxSelected = 4096;    // rows table capacity per query row
+constexpr int kMaxSelected = 4096;    // widest selection per query row
 constexpr int kPageTokens = 64;
 constexpr float kRescaleThreshold = 8.0f;
 
@@ -195,11 +195,6 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
   constexpr int kPool = kQkDim / 16;
   static_assert((kFp8 ? 2 : 1) * F::kLoads <= kPool, "staging does not fit the pool");
   v4u pool[kPool];
-  if (scorer) {
-    const uint16_t* qrow = q + ((row * heads + head0 + 32 * sw + n) * kQkDim) + 8 * h;
-#pragma unroll
-    for (int ks = 0; ks < kPool; ++ks) pool[ks] = *reinterpret_cast<const v4u*>(qrow + 16 * ks);
-  }
   float m_run = neg_inf;  // score lane: running max of its head (scaled)
   // Row sums of heads 16 wave + c (P^T against ones; every row alike).
   v4f l_acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
@@ -317,12 +312,23 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
     ring_id[0] = id_load(kRingAhead);
     ring_id[1] = id_load(kRingAhead + 1);
     ring_page[1] = page_load(ring_id[0]);
+    // The records of blocks 0 and 1 from this lane's own id and page loads,
+    // without waiting for the ring.
+    const int32_t id0 = id_load(0), id1 = id_load(1);
+    fetch(Set0{}, phys_from(id0, page_load(id0)));
+    if (kFp8) fetch(Set1{}, phys_from(id1, page_load(id1)));
   }
   __syncthreads();  // ring
+  // Q^T of the score wave's heads (72 KiB per work-group), loaded only now:
+  // issued at the start, the Q loads of all work-groups would queue ahead of
+  // the id and page loads that start the pipeline.
+  if (scorer) {
+    const uint16_t* qrow = q + ((row * heads + head0 + 32 * sw + n) * kQkDim) + 8 * h;
+#pragma unroll
+    for (int ks = 0; ks < kPool; ++ks) pool[ks] = *reinterpret_cast<const v4u*>(qrow + 16 * ks);
+  }
   int32_t phys_next = -1;
   if (!scorer) {
-    fetch(Set0{}, row_of(0));
-    if (kFp8) fetch(Set1{}, row_of(1));
     unpack(Set0{}, buf_of(0));
     fetch(Set0{}, row_of(kLookahead - 1));
     phys_next = row_of(kLookahead);
@@ -486,7 +492,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
       };
       // The first kHead k-steps run S alone (the checks' reads land
       // meanwhile); then PV MFMAs and softmax slices join.
-      constexpr int kHead = kS ? 6 : 0;
+      constexpr int kHead = kS ? 3 : 0;
       constexpr int kBody = kPvMfmas > 18 ? kPvMfmas : 18;
       constexpr int kSteps = kS ? kQkDim / 16 : kBody;
       if constexpr (kHead == 0) checks();
