@@ -149,17 +149,57 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
   float wt[kQueriesPerWave][16];
   int32_t qs[kQueriesPerWave], qe[kQueriesPerWave];
   const int64_t qw = q0 + wave * kQueriesPerWave;
+
+  // Linear half of the head sum: sum_h (w_h / 2) s_h = k . q' with
+  // q' = sum_h (w_h / 2) q_h, formed here in fp32 (lane 16j + c: query j,
+  // dims 8c .. 8c + 7) and written as kDigits e4m3 digits, digit d at scale
+  // 2^(E_j - 4d) (|q'| < 2^(E_j + 8)): each digit holds the residual of the
+  // ones before it to within half an e4m3 ulp, so the four carry q' to about
+  // 2^-17 of its largest element. In the MFMA operand, row 4d + j is digit d
+  // of query j; its C row then sits in lane group d, register j, so the
+  // reduction over lane groups that sums head partials also sums the digits.
+  //
+  // Load order: the inputs of q' and the head weights first, then the query
+  // operands (the bulk of the bytes), so that forming q' waits only for its
+  // own inputs and overlaps the latency of the query operands.
+  __shared__ __align__(16) uint8_t digits[kWaves][kQueriesPerWave][kDigits][kDim];
+  v8i qd;
+  float fl[kQueriesPerWave];
+  const int fj = lane >> 4;
+  const int fc = lane & 15;
+  const bool flive = qw + fj < rows;
+  const int64_t fqc = flive ? qw + fj : 0;
+  // q' in four partial sums over heads 16g .. 16g + 15 (each one fmaf chain
+  // from 0 in increasing head order), then 0.5 (((p0 + p1) + p2) + p3): the
+  // same bits whether the partials come from the layer prologue (q_fold,
+  // [rows][4][128]) or are formed here.
+  float pg[4][8];
+  uint2 codes[kHeads];
+  v4f w4;
+  if (q_fold) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const v4f* src = reinterpret_cast<const v4f*>(q_fold + (fqc * 4 + g) * kDim + 8 * fc);
+      const v4f a = src[0], b = src[1];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pg[g][i] = flive ? a[i] : 0.0f;
+        pg[g][4 + i] = flive ? b[i] : 0.0f;
+      }
+    }
+  } else {
+    // All 64 heads' codes in flight at once; the weights of heads 4c ..
+    // 4c + 3 per lane.
+    const uint8_t* qrow = q + fqc * kHeads * kDim + 8 * fc;
+#pragma unroll
+    for (int h = 0; h < kHeads; ++h) codes[h] = *reinterpret_cast<const uint2*>(qrow + h * kDim);
+    w4 = *reinterpret_cast<const v4f*>(w + fqc * kHeads + 4 * fc);
+  }
 #pragma unroll
   for (int j = 0; j < kQueriesPerWave; ++j) {
     const int64_t qi = qw + j;
     const bool live = qi < rows;
     const int64_t qc = live ? qi : 0;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const v4u* src = reinterpret_cast<const v4u*>(q + ((qc * kHeads + 16 * t + col) * kDim + 32 * group));
-      const v4u lo = src[0], hi = src[1];
-      qa[j][t] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-    }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const v4f wv = *reinterpret_cast<const v4f*>(w + qc * kHeads + 16 * t + 4 * group);
@@ -172,58 +212,31 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
     qs[j] = live ? (starts ? starts[qc] : 0) : 0;
     qe[j] = live ? (int32_t)e : 0;
   }
-
-  // Linear half of the head sum: sum_h (w_h / 2) s_h = k . q' with
-  // q' = sum_h (w_h / 2) q_h, formed here in fp32 (lane 16j + c: query j,
-  // dims 8c .. 8c + 7) and written as kDigits e4m3 digits, digit d at scale
-  // 2^(E_j - 4d) (|q'| < 2^(E_j + 8)): each digit holds the residual of the
-  // ones before it to within half an e4m3 ulp, so the four carry q' to about
-  // 2^-17 of its largest element. In the MFMA operand, row 4d + j is digit d
-  // of query j; its C row then sits in lane group d, register j, so the
-  // reduction over lane groups that sums head partials also sums the digits.
-  __shared__ __align__(16) uint8_t digits[kWaves][kQueriesPerWave][kDigits][kDim];
-  v8i qd;
-  float fl[kQueriesPerWave];
+#pragma unroll
+  for (int j = 0; j < kQueriesPerWave; ++j) {
+    const int64_t qc = qw + j < rows ? qw + j : 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const v4u* src = reinterpret_cast<const v4u*>(q + ((qc * kHeads + 16 * t + col) * kDim + 32 * group));
+      const v4u lo = src[0], hi = src[1];
+      qa[j][t] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    }
+  }
   {
-    const int j = lane >> 4;
-    const int c = lane & 15;
-    const int64_t qi = qw + j;
-    const bool live = qi < rows;
-    const int64_t qc = live ? qi : 0;
-    // q' in four partial sums over heads 16g .. 16g + 15 (each one fmaf chain
-    // from 0 in increasing head order), then 0.5 (((p0 + p1) + p2) + p3): the
-    // same bits whether the partials come from the layer prologue (q_fold,
-    // [rows][4][128]) or are formed here.
-    float pg[4][8];
-    if (q_fold) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const v4f* src = reinterpret_cast<const v4f*>(q_fold + (qc * 4 + g) * kDim + 8 * c);
-        const v4f a = src[0], b = src[1];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          pg[g][i] = live ? a[i] : 0.0f;
-          pg[g][4 + i] = live ? b[i] : 0.0f;
-        }
-      }
-    } else {
-      const uint8_t* qrow = q + qc * kHeads * kDim + 8 * c;
-      // All 64 heads' codes in flight at once; the weights of heads 4c ..
-      // 4c + 3 per lane, each head's weight broadcast along the 16-lane row
-      // by DPP (row_newbcast).
-      uint2 codes[kHeads];
-#pragma unroll
-      for (int h = 0; h < kHeads; ++h) codes[h] = *reinterpret_cast<const uint2*>(qrow + h * kDim);
-      const v4f w4 = *reinterpret_cast<const v4f*>(w + qc * kHeads + 4 * c);
+    const int j = fj;
+    const int c = fc;
+    if (!q_fold) {
 #pragma unroll
       for (int g = 0; g < 4; ++g)
 #pragma unroll
         for (int i = 0; i < 8; ++i) pg[g][i] = 0.0f;
+      // Each head's weight broadcast along the 16-lane row by DPP
+      // (row_newbcast).
       auto add_head = [&](auto head) {
         constexpr int h = decltype(head)::value;
         const float wb = __int_as_float(
             __builtin_amdgcn_update_dpp(0, __float_as_int(w4[h & 3]), 0x150 + (h >> 2), 0xF, 0xF, false));
-        const float wh = live ? wb : 0.0f;
+        const float wh = flive ? wb : 0.0f;
         const v2f x0 = __builtin_amdgcn_cvt_pk_f32_fp8(codes[h].x, false);
         const v2f x1 = __builtin_amdgcn_cvt_pk_f32_fp8(codes[h].x, true);
         const v2f x2 = __builtin_amdgcn_cvt_pk_f32_fp8(codes[h].y, false);
