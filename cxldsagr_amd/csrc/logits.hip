@@ -126,6 +126,7 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
   const int col = lane & 15;
   const int64_t q0 = (int64_t)blockIdx.y * kQueriesPerBlock;
   const int64_t kb = (int64_t)blockIdx.x * keys_per_split;
+  if (kb >= ldo) return;  // a padding split (whole work-group, before any barrier)
   const int64_t ke = kb + keys_per_split < ldo ? kb + keys_per_split : ldo;
   const float neg_inf = -__builtin_inff();
 
@@ -499,6 +500,11 @@ int logits_launch(const void* q, const void* k, const float* weights, const floa
   int64_t per = (ldo + splits - 1) / splits;
   per = (per + kStageKeys - 1) / kStageKeys * kStageKeys;
   splits = (ldo + per - 1) / per;
+  // Work-groups are dealt to the eight XCDs round-robin by linear id
+  // (x + splits * y): with a multiple of 8 splits every query group of one
+  // key range runs on the same XCD and the eight share its keys through that
+  // XCD's L2. The added splits start past the last column and exit at once.
+  if (splits >= 8) splits = (splits + 7) / 8 * 8;
   DSA_CHECK_ARG(qgroups < 65536, "too many query rows for one launch");
   DSA_CHECK_ARG(ldo < 0x7FFFFFFF - 64, "the logits row stride must fit int32");
   hipLaunchKernelGGL(logits_fp8_mfma, dim3((unsigned)splits, (unsigned)qgroups), dim3(kThreads),
