@@ -4,4 +4,4 @@ Host operators mirror the reference's operator API; every operator launches
 hand-written gfx950 kernels from libdsa_gfx950.so (see include/dsa_gfx950.h).
 """
 
-__all__ = ["indexer"]
+__all__ = ["attention", "contracts", "indexer", "kv_transfer", "layer", "ops", "token_pool"]
