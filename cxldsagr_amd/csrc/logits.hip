@@ -392,16 +392,15 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
       auto epilogue = [&](int i) {
         const int u = i / kQueriesPerWave, j = i % kQueriesPerWave;
         // relu(s) w = (|s| + s) w / 2: the |s| half here, one FMA per head
-        // (wt holds w / 2), four independent chains (one per head tile); the
-        // s half is the linear MFMA's share of this lane.
-        float pt[4];
+        // (wt holds w / 2) in one chain over the head tiles in order; the s
+        // half is the linear MFMA's share of this lane. (One chain: a wave's
+        // dependent FMAs issue back to back, and partial chains would cost
+        // three adds per unit.)
+        float p = fabsf(acc[i & 1][0][0]) * wt[j][0];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) pt[t] = fabsf(acc[i & 1][t][0]) * wt[j][4 * t];
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int r = 1; r < 4; ++r)
-#pragma unroll
-          for (int t = 0; t < 4; ++t) pt[t] = fmaf(fabsf(acc[i & 1][t][r]), wt[j][4 * t + r], pt[t]);
-        float p = (pt[0] + pt[1]) + (pt[2] + pt[3]);
+          for (int r = (t == 0 ? 1 : 0); r < 4; ++r) p = fmaf(fabsf(acc[i & 1][t][r]), wt[j][4 * t + r], p);
         p = fmaf(acc_lin[u & 1][j], fl[j], p);
         // Pins the epilogue here: otherwise instruction selection sinks it below
         // every MFMA of the stage and all 64 results stay live.
@@ -429,7 +428,7 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
