@@ -307,20 +307,31 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
   const uint32_t ring_base = (uint32_t)(uintptr_t)&ring[0][0];
   const int lane_key = lane >> 3;
   const uint32_t lane_chunk = 16u * (uint32_t)((lane & 7) ^ (lane_key & 7));
+  const uint32_t lane_off = (uint32_t)lane_key * kDim + lane_chunk;
   auto issue = [&](int s) {
     const uint32_t slot_base = ring_base + (uint32_t)(s % kRing) * kStageBytes;
     const bool live = s < stages;
     const int64_t key0 = live ? kb + (int64_t)s * kStageKeys : 0;
     const int32_t last = live ? (int32_t)(columns - 1 - key0) : 0;  // >= 0: key0 < columns
     const uint8_t* kbase = k + key0 * kDim;
+    if (last >= kStageKeys - 1) {
+      // A whole stage: every lane offset is a constant and the per-load
+      // steps go into the scalar base (no vector arithmetic per load).
 #pragma unroll
-    for (int i = 0; i < kKLoads; ++i) {
-      const int32_t key = min(8 * i + lane_key, last);
-      dma16_s(kbase, (uint32_t)key * kDim + lane_chunk, slot_base + i * 1024);
+      for (int i = 0; i < kKLoads; ++i) dma16_s(kbase + 1024 * i, lane_off, slot_base + i * 1024);
+#pragma unroll
+      for (int i = 0; i < kSLoads; ++i)
+        dma4_s(kscale + key0 + 64 * i, 4u * (uint32_t)lane, slot_base + kKBytes + 256 * i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kKLoads; ++i) {
+        const int32_t key = min(8 * i + lane_key, last);
+        dma16_s(kbase, (uint32_t)key * kDim + lane_chunk, slot_base + i * 1024);
+      }
+#pragma unroll
+      for (int i = 0; i < kSLoads; ++i)
+        dma4_s(kscale + key0, 4u * (uint32_t)min(64 * i + lane, last), slot_base + kKBytes + 256 * i);
     }
-#pragma unroll
-    for (int i = 0; i < kSLoads; ++i)
-      dma4_s(kscale + key0, 4u * (uint32_t)min(64 * i + lane, last), slot_base + kKBytes + 256 * i);
   };
   // Wave 0's finished rows, [stage parity][query][key].
   __shared__ __align__(16) float staged[2][kQueriesPerWave][kStageKeys];
