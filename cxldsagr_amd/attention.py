@@ -3,9 +3,9 @@
 Drop-in for the reference's attention operators (same names, argument order,
 padding semantics and validation messages):
 
-* ``sparse_mla``           - ``operators/deepseek_v32/attention/device_only/mla.py:156-181``
+* ``sparse_mla``           - ``operators/deepseek_v32/attention/device_only/mla.py:90-115``
   with ``_validate`` (``attention/_validation.py:8-24``) and the input
-  preparation of ``mla.py:124-153`` (contiguity, 16-byte alignment, int64 ids
+  preparation of ``mla.py:70-87`` (contiguity, 16-byte alignment, int64 ids
   masked before narrowing). The selection is not padded to 128: the kernel
   accepts any count.
 * ``sparse_mla_from_pool`` - ``operators/deepseek_v32/attention/offload/mla.py:12-20``.

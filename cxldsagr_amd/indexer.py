@@ -113,28 +113,6 @@ def _quantize(x, scale_fmt, weights):
             _native.call("dsa_quantize_fp8_rows_fold", *common, _native.ptr(weights),
                          _native.ptr(folded), _native.stream_of(x.device))
     return data, scales, folded
-    # Rows must sit at a uniform stride with unit element stride; other
-    # layouts are copied on the device first.
-    if x.is_contiguous():
-        source, row_stride = x, dim
-    elif x.ndim == 2 and x.stride(1) == 1:
-        source, row_stride = x, x.stride(0)
-    else:
-        source, row_stride = x.contiguous(), dim
-    with torch.cuda.device(x.device):
-        _native.call(
-            "dsa_quantize_fp8_rows",
-            _native.ptr(source),
-            _native.DTYPE_CODES[x.dtype],
-            rows,
-            dim,
-            row_stride,
-            _native.ptr(data),
-            _native.ptr(scales),
-            1 if scale_fmt == "ue8m0" else 0,
-            _native.stream_of(x.device),
-        )
-    return data, scales
 
 
 def quantize_into(x, codes, scales, scale_fmt="ue8m0"):

@@ -161,7 +161,7 @@ int dsa_layer_prologue_fp8(const void* q, int64_t q_rows, const float* weights, 
 /*
  * A7 - sparse MLA over flat bf16 records. Replaces sparse_mla /
  * sparse_mla_from_pool (FlashMLA flash_mla_sparse_fwd),
- * operators/deepseek_v32/attention/device_only/mla.py:156-181 and
+ * operators/deepseek_v32/attention/device_only/mla.py:90-115 and
  * operators/deepseek_v32/attention/offload/mla.py:12-20.
  * q: bf16 [rows, heads, 576] (heads a multiple of 64); kv: bf16
  * [kv_rows, 576]; indices: int32 [rows, topk], ids outside [0, kv_rows) are

@@ -17,7 +17,7 @@ reference checkout):
                    oracle in ``indexer/tests/test_echo_indexer.py:86-109``.
 * ``topk``       - ``operators/deepseek_v32/indexer/selection.py:62-113``.
 * ``sparse_mla`` - ``operators/deepseek_v32/attention/reference/torch.py:13-28``,
-                   ``attention/_validation.py:8-24``, ``device_only/mla.py:136-153``.
+                   ``attention/_validation.py:8-24``, ``device_only/mla.py:58-115``.
 * ``kv_fp8``     - the 656-byte paged fp8 KV record (no reference counterpart;
                    built from the A1 quantiser rule).
 * ``recall``     - ``cache/sparse_token_cache.py:483-569`` and

@@ -6,7 +6,7 @@ rounds to nearest even; magnitudes >= 480 (the first value that would round
 past 448) and NaN become 0x7F with the input sign, the behaviour of
 ``tensor.to(torch.float8_e4m3fn)``.
 
-Pinned by: ``tests/test_oracle_fp8.py`` compares ``encode`` bit-for-bit with
+Pinned by: ``tests/test_oracle_fp8_quantize.py`` compares ``encode`` bit-for-bit with
 torch's own float8 cast over every bf16 bit pattern, random fp32 values and all
 e4m3 rounding midpoints, and ``decode`` with torch's float8->float32 cast over
 all 256 codes.

@@ -16,10 +16,13 @@ t % 64`` of the ``[pages * 64, 656]`` byte array. Dequantisation is
 bf16 value, so attention over the dequantised cache is attention over a bf16
 cache.
 
-Pinned by ``tests/test_oracle_kv_fp8.py``: encode/decode round trip within the
-e4m3 half-ulp bound, exact bf16 representability of every dequantised value,
-exact RoPE pass-through, page-table addressing against a hand-built case, and
-the A1 pins it reuses.
+Pinned by ``tests/test_oracle_kv_fp8.py``: every byte field against torch's
+own float8 cast with the reference's log2/ceil UE8M0 scale per tile (codes,
+little-endian fp32 scales at bytes 512-527, RoPE bits at 528-655), the
+encode/decode round trip within the e4m3 half-ulp bound, exact bf16
+representability of every dequantised value, and page-table addressing on a
+hand-built two-page permuted table and a random permutation. The same file
+plants mistakes in copies of the encoder and requires the pins to catch each.
 """
 
 import numpy as np

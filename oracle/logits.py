@@ -11,7 +11,7 @@ for ``starts[i] <= j < ends[i]`` and ``-inf`` elsewhere, with
 (``echo.py:357-361``). The output row stride is ``ceil(N / 256) * 256``; the
 padded columns are ``-inf`` (``echo.py:381,397-409``).
 
-Pinned by ``tests/test_oracle_logits.py``: a float64 brute-force loop on tiny
+Pinned by ``tests/test_oracle_logits_topk.py``: a float64 brute-force loop on tiny
 shapes, closed forms (zero weights give exactly 0, a one-hot head weight gives
 ``relu(q_h . k) * kscale``, all-negative dot products give 0) and the exact
 ``-inf`` placement for every causal boundary of a small case.

@@ -23,7 +23,7 @@ default both agree on every bf16 amax (pinned in the tests), for
 ``scale_fmt=None`` they can differ by one ulp of the scale and this oracle
 follows the GPU path.
 
-Pinned by ``tests/test_oracle_quantize.py``: all 65,536 bf16 encodings as the
+Pinned by ``tests/test_oracle_fp8_quantize.py``: all 65,536 bf16 encodings as the
 row maximum against torch's ``exp2(ceil(log2(.)))`` formulation and float8
 cast, the reference test's non-finite rows and e4m3 midpoints at six row
 scales, and closed-form scale values.

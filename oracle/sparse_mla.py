@@ -8,13 +8,17 @@ once per slot, negative or out-of-range ids are padding), and in fp32
     P = softmax_j(q[r] @ kv[S_r].T * scale)     out[r] = P @ kv[S_r, :value_dim]
 
 rounded to bf16. A row without a valid id is all zeros. int64 ids are masked
-before narrowing (``attention/device_only/mla.py:144-148``), which this oracle
+before narrowing (``attention/device_only/mla.py:78-82``), which this oracle
 gets for free by comparing in int64.
 
 Pinned by ``tests/test_oracle_sparse_mla.py``: the reference's known answers
 (duplicates/padding -> 4, 0, 2; RoPE dimensions only steer scores -> 0.75;
-+-10000 logits -> exactly 2; empty inputs -> zeros) and a float64 brute-force
-loop on small random shapes.
++-100 x 100 logits around empty tiles -> exactly 2; int64 ids that would wrap
+when narrowed -> padding; empty inputs -> zeros), ``sparse_mla_brute_force``
+(float64 scalar loops) on small random shapes with duplicates, padding and
+out-of-range ids, and closed forms (one valid key -> its value row, equal
+scores -> the mean value row). The same file plants mistakes in copies of
+this function and requires the pins to catch each.
 """
 
 import numpy as np

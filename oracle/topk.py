@@ -12,7 +12,7 @@ followed by the non-finite index mask (``selection.py:43-51``).
   path (``indexer/csrc/q1_topk_sort.cu:24-42``).
 * Values keep their bits; the index is ``-1`` where ``|value|`` is inf or NaN.
 
-Pinned by ``tests/test_oracle_topk.py``: values equal ``torch.topk`` bit-for-bit,
+Pinned by ``tests/test_oracle_logits_topk.py``: values equal ``torch.topk`` bit-for-bit,
 ids equal torch's stable descending argsort on rows without signed zeros, the
 reference's known answers (all-equal rows -> ``arange``, masked rows -> -1, the
 signed-zero/extreme-value row), and a brute-force Python sort on small rows.

@@ -3,10 +3,12 @@ stage and the CPU oracle's outputs for them (quantise, logits, top-k, fp8 KV
 pack, sparse MLA over the paged cache).
 
 The reference ships no data fixtures for this path (its tests draw inputs
-from seeds), so these vectors come from the oracle, whose functions are
-pinned by the reference's own test cases (tests/test_oracle_*.py). Committed
-vectors keep the GPU tests independent of later oracle edits, and
-tests/test_golden.py re-derives them to catch any drift.
+from seeds), so these vectors come from the oracle. They pin nothing by
+themselves: each oracle function is pinned independently in
+tests/test_oracle_*.py (the reference's own test cases restated, torch's
+casts, closed forms and brute force). Committed vectors keep the GPU tests
+independent of later oracle edits, and tests/test_golden.py re-derives them
+to catch any drift.
 
 Run from the repository root: python tests/golden/make_golden.py
 """
