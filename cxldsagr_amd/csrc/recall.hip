@@ -190,18 +190,24 @@ __global__ __launch_bounds__(256) void recall_gather(const uint8_t* __restrict__
   }
 }
 
+// Selected id -> physical pool row. History ids map through h2d; candidate
+// ids (transient_start <= id < written) to rows slots + 1 + id -
+// transient_start, which must lie inside the record rows. Every other id
+// (padding, unwritten, past the candidate rows) maps to -1, so that a bad
+// selection reads no stale record (recall_mark has flagged it in status).
 __global__ void recall_map(const int32_t* __restrict__ indices, int64_t n, int64_t history_end,
-                           int64_t transient_start, int64_t slots,
-                           const int32_t* __restrict__ page_table, const int32_t* __restrict__ h2d,
-                           int32_t* __restrict__ physical) {
+                           int64_t written, int64_t transient_start, int64_t slots,
+                           int64_t record_rows, const int32_t* __restrict__ page_table,
+                           const int32_t* __restrict__ h2d, int32_t* __restrict__ physical) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const int64_t id = indices[i];
   int32_t out = -1;
   if (id >= 0 && id < history_end) {
     out = h2d[to_global(page_table, id)];
-  } else if (transient_start >= 0 && id >= transient_start) {
-    out = (int32_t)(slots + 1 + id - transient_start);
+  } else if (transient_start >= 0 && id >= transient_start && id < written) {
+    const int64_t row = slots + 1 + id - transient_start;
+    if (row < record_rows) out = (int32_t)row;
   }
   physical[i] = out;
 }
@@ -281,6 +287,8 @@ extern "C" int dsa_pool_recall(const int32_t* indices, int64_t n, const int32_t*
                 "records must hold slots + 1 rows of a 16-byte multiple width");
   DSA_CHECK_ARG(transient_start < 0 || transient_start >= history_end,
                 "the transient suffix starts after the host-backed history");
+  DSA_CHECK_ARG(transient_start < 0 || written - transient_start <= record_rows - (slots + 1),
+                "transient suffix exceeds candidate slot capacity");
   DSA_CHECK_ARG(protect_stamp >= 0 && chosen_stamp > protect_stamp && chosen_stamp < 0x7FFFFFFF,
                 "invalid FIFO timestamps");
   DSA_CHECK_ARG(indices && page_table && h2d && d2h && priority && stats && physical && records &&
@@ -333,7 +341,8 @@ extern "C" int dsa_pool_recall(const int32_t* indices, int64_t n, const int32_t*
   }
   if (n > 0)
     hipLaunchKernelGGL(recall_map, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
-                       indices, n, history_end, transient_start, slots, page_table, h2d, physical);
+                       indices, n, history_end, written, transient_start, slots, record_rows,
+                       page_table, h2d, physical);
   DSA_CHECK_LAUNCH("exact recall");
   return kOk;
 }

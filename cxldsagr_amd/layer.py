@@ -189,6 +189,97 @@ class DSALayer:
         return out, selection
 
 
+class OffloadDSALayer:
+    """One layer of one session whose KV records live in a bounded HBM token pool.
+
+    The offload half of the reference runner (``attention.py:201-235``): the
+    indexer keys stay resident (as in the reference); the main KV records sit
+    in the pool's pinned host arena and only the selected ones are recalled
+    into the pool's slots before sparse MLA reads them by physical id. New
+    tokens are either persistent (written to the session's host pages, then
+    recalled like history when selected) or transient GR candidates (written
+    to the pool's candidate rows and never committed,
+    ``cache/sparse_token_cache.py:244-318``).
+
+    ``consume`` mirrors ``_consume``: exact recall of the selection; when its
+    union does not fit the pool (``WorkingSetTooLarge``), the query batch is
+    halved recursively and the halves concatenated, and a single query whose
+    selection does not fit raises ``ValueError``. ``capacity_splits`` counts
+    the splits as the reference's ``stats.capacity_splits`` does.
+    """
+
+    def __init__(self, pool, session, capacity, *, topk=2048, scale=576**-0.5, layer_idx=0):
+        if type(capacity) is not int or capacity < 1 or capacity > session.capacity:
+            raise ValueError("capacity must be a positive integer within the session's pages")
+        self.pool, self.session = pool, session
+        self.device = pool.device
+        self.capacity, self.topk, self.scale, self.layer_idx = capacity, topk, scale, layer_idx
+        self.index_keys = torch.zeros((capacity, 128), dtype=torch.float8_e4m3fn, device=self.device)
+        self.index_scales = torch.zeros(capacity, dtype=torch.float32, device=self.device)
+        self.capacity_splits = 0
+
+    @property
+    def written(self):
+        return self.session.written
+
+    def write_history(self, index_k, kv):
+        """Bulk-append projected history: index K into the resident cache, KV records
+        (fp8-packed) into the session's host pages."""
+        start, end = self.session.written, self.session.written + len(index_k)
+        if len(kv) != len(index_k) or end > self.capacity:
+            raise ValueError("history exceeds the layer capacity or K/KV lengths differ")
+        indexer.quantize_into(index_k, self.index_keys[start:end], self.index_scales[start:end])
+        self.pool.write_history(self.session, kv)
+        return start
+
+    def forward(self, index_q, index_k, weights, q, kv, *, transient=False):
+        """One query batch at ``position = session.written``; returns (out, selection).
+
+        ``transient=True`` runs the GR candidate step: the batch's KV goes to
+        the pool's candidate rows and the session's history is not extended.
+        """
+        position = self.session.written
+        rows = len(index_q)
+        end = position + rows
+        if end > self.capacity or len(q) != rows or len(kv) != rows or len(index_k) != rows:
+            raise ValueError("query batch exceeds the layer capacity or inputs disagree in length")
+        if transient and rows > self.pool.candidate_slots:
+            raise ValueError("transient suffix exceeds candidate slot capacity")
+        q8, _, folded = indexer.quantize_index_folded(index_q, weights)
+        indexer.quantize_into(index_k, self.index_keys[position:end], self.index_scales[position:end])
+        scores = indexer.logits(q8, self.index_keys[:end], folded, self.index_scales[:end],
+                                position, _pad_to_stride=end >= self.topk)
+        _, ids = indexer.exact_topk(scores, self.topk)
+        del scores
+        if transient:
+            self.pool.write_candidates(kv)
+            out = self.consume(q, ids, written=end, transient_start=position)
+        else:
+            self.pool.write_history(self.session, kv)
+            out = self.consume(q, ids, written=end)
+        return out, TokenSelection(ids)
+
+    def consume(self, q, ids, *, written, transient_start=None):
+        """Recall then sparse MLA over the pool, splitting the query batch on
+        ``WorkingSetTooLarge`` (``attention.py:213-228``)."""
+        from cxldsagr_amd.token_pool import WorkingSetTooLarge
+
+        try:
+            physical = self.pool.ensure(ids, self.session, written=written,
+                                        transient_start=transient_start)
+        except WorkingSetTooLarge:
+            if len(q) == 1:
+                raise ValueError("offload slots must fit at least one query's exact selection") from None
+            self.capacity_splits += 1
+            middle = len(q) // 2
+            left = self.consume(q[:middle], ids[:middle], written=written,
+                                transient_start=transient_start)
+            right = self.consume(q[middle:], ids[middle:], written=written,
+                                 transient_start=transient_start)
+            return torch.cat((left, right))
+        return self.pool.attend(q, physical, self.scale)
+
+
 class LayerIndexer:
     """``Indexer`` protocol adapter: ``context.auxiliary_state`` carries the new
     tokens' bf16 index K (``"index_k"``) and head weights (``"weights"``)."""

@@ -131,6 +131,9 @@ class TokenPool:
         history = written if transient_start is None else transient_start
         if history > session.written:
             raise ValueError("host-backed history exceeds the session's written records")
+        if transient_start is not None and not 0 <= written - transient_start <= self.candidate_slots:
+            # cache/sparse_token_cache.py:254-256
+            raise ValueError("transient suffix exceeds candidate slot capacity")
         union_checked = 0
         if history > self.slots:
             ids = indices[(indices >= 0) & (indices < history)]

@@ -220,9 +220,11 @@ int dsa_pool_workspace_bytes(int64_t slots, int64_t history_capacity, int64_t* b
  * (native stages sparse_selection_classify / allocate / gather_records /
  * publish / map, operators/deepseek_v32/indexer/cache_ops.py:303-1016).
  * indices: int32 [n] logical ids (-1 padding); page_table: int32 logical page
- * -> global host page; ids in [0, history_end) are host-backed, ids at or
- * past transient_start (>= 0) are candidate rows slots + 1 + id -
- * transient_start. Pool state: h2d int32 [host_rows] (MISSING = INT32_MAX),
+ * -> global host page; ids in [0, history_end) are host-backed, ids in
+ * [transient_start, written) (transient_start >= 0) are candidate rows
+ * slots + 1 + id - transient_start, which must lie inside record_rows (else
+ * the call fails); every other id, including one at or past `written`, maps
+ * to -1 (padding). Pool state: h2d int32 [host_rows] (MISSING = INT32_MAX),
  * d2h / priority int64 [slots + 1] (slot 0 is the sentinel), records
  * [record_rows, record_bytes] on the device, host records pinned
  * [host_rows, record_bytes]. Hits are stamped protect_stamp, recalled slots

@@ -21,6 +21,7 @@ import torch
 from oracle import fp8 as ofp8
 from oracle import layer as olayer
 from oracle import sparse_mla as omla
+from oracle import topk as otopk
 
 pytestmark = pytest.mark.gpu
 
@@ -49,14 +50,14 @@ def _run_layer(gpu, history, queries, seed):
     return inputs, out, selection.token_ids, scores
 
 
-def _oracle(inputs, rows):
-    history = inputs.history
+def _oracle(inputs, rows, fp8_records=True):
+    """Oracle indexer scores and top-k for ``rows`` (no attention)."""
     kv_bits = inputs.kv.view(torch.int16).numpy().view(np.uint16)
-    cache = olayer.HistoryCache(inputs.index_k.float().numpy(), kv_bits, fp8_records=True)
-    scores, values, ids, out = olayer.dsa_layer(
-        inputs.index_q.float().numpy(), inputs.weights.numpy(), inputs.mla_q.float().numpy(),
-        cache, history, rows, k=TOPK, scale=SCALE)
-    return cache, scores, values, ids, out
+    cache = olayer.HistoryCache(inputs.index_k.float().numpy(), kv_bits, fp8_records=fp8_records)
+    scores = olayer.index_scores(inputs.index_q.float().numpy(), inputs.weights.numpy(), cache,
+                                 inputs.history, rows)
+    values, ids = otopk.exact_topk(scores, TOPK)
+    return cache, scores, values, ids
 
 
 def _check_selection(gpu_ids, ref_ids, ref_scores_row, kth):
@@ -77,15 +78,16 @@ def _check_attention(actual, expected):
 
 
 @pytest.mark.parametrize(
-    ("history", "queries", "rows"),
+    ("history", "queries", "rows", "mla_rows"),
     [
-        (4096, 128, [0, 1, 63, 127]),        # BASELINE config 0 shape
-        (65536, 128, [0, 127]),              # configs 1/2: the benchmark layer
+        (4096, 128, list(range(128)), [0, 1, 63, 127]),         # BASELINE config 0 shape
+        (65536, 128, list(range(128)), [0, 31, 64, 127]),       # configs 1/2: the benchmark
     ],
 )
-def test_layer_matches_oracle(gpu, history, queries, rows):
+def test_layer_matches_oracle(gpu, history, queries, rows, mla_rows):
+    """Logits and selections on every query row; sparse MLA on a sample."""
     inputs, out, ids, scores = _run_layer(gpu, history, queries, seed=947)
-    cache, ref_scores, ref_values, ref_ids, _ = _oracle(inputs, np.asarray(rows))
+    cache, ref_scores, ref_values, ref_ids = _oracle(inputs, np.asarray(rows))
     tokens = history + queries
     gpu_scores = scores.cpu().numpy()[rows]
     ref = ref_scores[:, :tokens]
@@ -98,8 +100,79 @@ def test_layer_matches_oracle(gpu, history, queries, rows):
         _check_selection(gpu_ids[i], ref_ids[i], ref[i], float(ref_values[i, -1]))
 
     # Sparse MLA over the GPU's own selection.
+    sample = np.asarray(mla_rows)
+    _, expected = omla.sparse_mla(inputs.mla_q.float().numpy()[sample], cache.records,
+                                  ids.cpu().numpy()[sample], SCALE)
+    _check_attention(out.float().cpu().numpy()[sample], expected)
+
+
+@pytest.mark.parametrize("kv_format", ["fp8_paged", "bf16"])
+def test_config4_long_context_layer(gpu, kv_format):
+    """131072 history + 512 queries, 10 % heavy hitters in 8
+    contiguous spans. Oracle parity on three rows (logits, selection, MLA),
+    selection properties on all 512 rows."""
+    from cxldsagr_amd.layer import DSALayer
+    from cxldsagr_amd.workloads import CONFIGS, make_layer_inputs
+
+    history, queries, kwargs = CONFIGS["config4"]
+    inputs = make_layer_inputs(history, queries, seed=947, **kwargs)
+    tokens = history + queries
+    layer = DSALayer(tokens, device=gpu, kv_format=kv_format,
+                     page_table=inputs.page_table if kv_format == "fp8_paged" else None)
+    layer.write_history(inputs.index_k[:history].to(gpu), inputs.kv[:history].to(gpu))
+    out, selection = layer.forward(inputs.index_q.to(gpu), inputs.index_k[history:].to(gpu),
+                                   inputs.weights.to(gpu), inputs.mla_q.to(gpu),
+                                   inputs.kv[history:].to(gpu))
+    ids = selection.token_ids
+    torch.cuda.synchronize()
+    assert ids.shape == (queries, TOPK)
+    # Every row: TOPK distinct causal ids.
+    sorted_ids, _ = torch.sort(ids, dim=1)
+    assert bool((sorted_ids[:, 1:] > sorted_ids[:, :-1]).all())
+    ends = history + torch.arange(queries, device=gpu)
+    assert bool((ids >= 0).all()) and bool((ids.max(dim=1).values <= ends).all())
+
+    rows = np.array([0, 255, 511])
+    cache, ref_scores, ref_values, ref_ids = _oracle(inputs, rows,
+                                                     fp8_records=kv_format == "fp8_paged")
+    gpu_ids = ids.cpu().numpy()[rows]
+    for i in range(len(rows)):
+        _check_selection(gpu_ids[i], ref_ids[i], ref_scores[i, :tokens], float(ref_values[i, -1]))
     _, expected = omla.sparse_mla(inputs.mla_q.float().numpy()[rows], cache.records, gpu_ids, SCALE)
     _check_attention(out.float().cpu().numpy()[rows], expected)
+
+
+def test_config4_fp8_versus_bf16_delta(gpu):
+    """BASELINE config 4 asks for the accuracy delta of the fp8 paged cache
+    against the bf16 (unquantised) records: both layers select with the same
+    indexer (identical selections), so the output difference is the fp8
+    record quantisation alone. Asserted: cosine >= 0.999 between the two
+    outputs, and each within the north-star bar of its own oracle (previous
+    test). The measured figures are printed."""
+    from cxldsagr_amd.layer import DSALayer
+    from cxldsagr_amd.workloads import CONFIGS, make_layer_inputs
+
+    history, queries, kwargs = CONFIGS["config4"]
+    inputs = make_layer_inputs(history, queries, seed=947, **kwargs)
+    tokens = history + queries
+    outs, sels = {}, {}
+    for kv_format in ("fp8_paged", "bf16"):
+        layer = DSALayer(tokens, device=gpu, kv_format=kv_format,
+                         page_table=inputs.page_table if kv_format == "fp8_paged" else None)
+        layer.write_history(inputs.index_k[:history].to(gpu), inputs.kv[:history].to(gpu))
+        outs[kv_format], sel = layer.forward(
+            inputs.index_q.to(gpu), inputs.index_k[history:].to(gpu), inputs.weights.to(gpu),
+            inputs.mla_q.to(gpu), inputs.kv[history:].to(gpu))
+        sels[kv_format] = sel.token_ids
+        del layer
+    assert torch.equal(sels["fp8_paged"], sels["bf16"])
+    a = outs["fp8_paged"].double().flatten()
+    b = outs["bf16"].double().flatten()
+    cosine = float(a @ b / (a.norm() * b.norm()))
+    max_abs = float((a - b).abs().max())
+    rel_rms = float((a - b).norm() / b.norm())
+    print(f"config4 fp8-vs-bf16: cosine {cosine:.6f} max-abs {max_abs:.4f} rel-rms {rel_rms:.4e}")
+    assert cosine >= 0.999
 
 
 def test_layer_selection_is_sorted_and_causal(gpu):
@@ -160,3 +233,44 @@ def test_fused_prologue_equals_the_separate_stages(gpu):
     a = indexer.logits(q8, keys, folded, scales, history, _pad_to_stride=True)
     b = indexer.logits(q8, keys, folded, scales, history, _pad_to_stride=True, _q_fold=q_fold)
     assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+
+
+@pytest.mark.parametrize("kv_format", ["fp8_paged", "bf16"])
+def test_contract_adapters_equal_layer_forward(gpu, kv_format):
+    """A layer step driven only through the reference's contracts, the way
+    EchoAttentionRunner calls Indexer then MainAttention
+    (models/attention_contracts.py:47-60): LayerIndexer(q, cache_access,
+    AttentionContext) -> TokenSelection, LayerAttention(q, selection,
+    cache_access, context) -> output. Selection and output bits equal
+    DSALayer.forward's on the same inputs."""
+    from cxldsagr_amd.contracts import AttentionContext, TokenSelection
+    from cxldsagr_amd.layer import DSALayer, LayerAttention, LayerIndexer
+    from cxldsagr_amd.workloads import make_layer_inputs
+
+    history, queries = 4096, 64
+    inputs = make_layer_inputs(history, queries, seed=31)
+    tokens = history + queries
+    table = inputs.page_table if kv_format == "fp8_paged" else None
+    x = {name: getattr(inputs, name).to(gpu) for name in
+         ("index_q", "index_k", "weights", "mla_q", "kv")}
+    layers = []
+    for _ in range(2):
+        layer = DSALayer(tokens, device=gpu, kv_format=kv_format, page_table=table)
+        layer.write_history(x["index_k"][:history], x["kv"][:history])
+        layers.append(layer)
+    out_ref, sel_ref = layers[0].forward(x["index_q"], x["index_k"][history:], x["weights"],
+                                         x["mla_q"], x["kv"][history:])
+    layer = layers[1]
+    context = AttentionContext(layer_idx=0, query_start=history, query_length=queries,
+                               auxiliary_state={"index_k": x["index_k"][history:],
+                                                "weights": x["weights"],
+                                                "kv": x["kv"][history:]})
+    selection = LayerIndexer(layer)(x["index_q"], layer, context)
+    assert isinstance(selection, TokenSelection)
+    out = LayerAttention(layer)(x["mla_q"], selection, layer, context)
+    torch.cuda.synchronize()
+    assert layer.length == tokens and layer.max_seq_len == tokens
+    assert torch.equal(selection.token_ids, sel_ref.token_ids)
+    assert torch.equal(out.view(torch.int16), out_ref.view(torch.int16))
+    with pytest.raises(ValueError, match="TokenSelection"):
+        LayerAttention(layer)(x["mla_q"], None, layer, context)

@@ -99,3 +99,105 @@ def test_oversize_union_raises_before_launch(gpu):
         pool.ensure(torch.arange(100, dtype=torch.int32, device=gpu)[None], session)
     physical = pool.ensure(torch.arange(64, dtype=torch.int32, device=gpu)[None], session)
     assert sorted(physical[0].tolist()) == list(range(1, 65))
+
+
+def test_unwritten_and_excess_candidate_ids_map_to_padding(gpu):
+    """Ids at or past ``written`` come back as -1 (and flag the status word),
+    so attention never reads a stale candidate row; a transient suffix larger
+    than the candidate rows is rejected before launch
+    (cache/sparse_token_cache.py:254-256)."""
+    from cxldsagr_amd.token_pool import TokenPool
+
+    gen = torch.Generator().manual_seed(12)
+    pool = TokenPool(1024, 256, device=gpu, candidate_slots=8)
+    session = pool.allocate_session(1024)
+    pool.write_history(session, torch.randn(500, 576, generator=gen).bfloat16().to(gpu))
+    pool.write_candidates(torch.randn(8, 576, generator=gen).bfloat16().to(gpu))
+    sel = torch.tensor([[0, 10, 500, 505, 506, 507, 600, -1]], dtype=torch.int32, device=gpu)
+    physical = pool.ensure(sel, session, written=506, transient_start=500)
+    torch.cuda.synchronize()
+    got = physical[0].tolist()
+    assert got[2:4] == [pool.slots + 1, pool.slots + 6]
+    assert got[4:] == [-1, -1, -1, -1], got
+    with pytest.raises(ValueError, match="unwritten"):
+        pool.check_status()
+    assert pool.check_status() == 0
+    with pytest.raises(ValueError, match="candidate slot capacity"):
+        pool.ensure(sel, session, written=509, transient_start=500)
+
+
+def _offload_inputs(gpu, history, queries, seed):
+    from cxldsagr_amd.workloads import make_layer_inputs
+
+    inputs = make_layer_inputs(history, queries, seed=seed)
+    return inputs, {name: getattr(inputs, name).to(gpu) for name in
+                    ("index_q", "index_k", "weights", "mla_q", "kv")}
+
+
+def test_offload_layer_splits_queries_and_matches_resident_layer(gpu):
+    """A9 offload: recall -> sparse_mla_from_pool, the query batch halved while
+    the selection's union exceeds the pool (attention.py:213-228). Output bits
+    equal the resident fp8 paged layer on the same selection."""
+    from cxldsagr_amd.layer import DSALayer, OffloadDSALayer
+    from cxldsagr_amd.token_pool import TokenPool
+
+    history, queries = 8192, 16
+    inputs, x = _offload_inputs(gpu, history, queries, seed=21)
+    tokens = history + queries
+    resident = DSALayer(tokens, device=gpu, kv_format="fp8_paged", page_table=inputs.page_table)
+    resident.write_history(x["index_k"][:history], x["kv"][:history])
+    out_r, sel_r = resident.forward(x["index_q"], x["index_k"][history:], x["weights"],
+                                    x["mla_q"], x["kv"][history:])
+
+    pool = TokenPool(tokens + 64 - tokens % 64, 3072, device=gpu, history_capacity=tokens)
+    session = pool.allocate_session(tokens)
+    layer = OffloadDSALayer(pool, session, tokens)
+    layer.write_history(x["index_k"][:history], x["kv"][:history])
+    out_o, sel_o = layer.forward(x["index_q"], x["index_k"][history:], x["weights"],
+                                 x["mla_q"], x["kv"][history:])
+    torch.cuda.synchronize()
+    assert torch.equal(sel_o.token_ids, sel_r.token_ids)
+    assert layer.capacity_splits >= 1
+    assert pool.check_status() == 0
+    assert torch.equal(out_o.view(torch.int16), out_r.view(torch.int16))
+
+
+def test_offload_layer_transient_candidates(gpu):
+    """GR candidate step: the batch's KV sits in the candidate rows, history is
+    not extended, and the output equals the resident layer's."""
+    from cxldsagr_amd.layer import DSALayer, OffloadDSALayer
+    from cxldsagr_amd.token_pool import TokenPool
+
+    history, queries = 4096, 64
+    inputs, x = _offload_inputs(gpu, history, queries, seed=22)
+    tokens = history + queries
+    resident = DSALayer(tokens, device=gpu, kv_format="fp8_paged", page_table=inputs.page_table)
+    resident.write_history(x["index_k"][:history], x["kv"][:history])
+    out_r, sel_r = resident.forward(x["index_q"], x["index_k"][history:], x["weights"],
+                                    x["mla_q"], x["kv"][history:])
+    pool = TokenPool(8192, 8192, device=gpu, candidate_slots=queries)
+    session = pool.allocate_session(tokens)
+    layer = OffloadDSALayer(pool, session, tokens)
+    layer.write_history(x["index_k"][:history], x["kv"][:history])
+    out_o, sel_o = layer.forward(x["index_q"], x["index_k"][history:], x["weights"],
+                                 x["mla_q"], x["kv"][history:], transient=True)
+    torch.cuda.synchronize()
+    assert session.written == history
+    assert layer.capacity_splits == 0 and pool.check_status() == 0
+    assert torch.equal(sel_o.token_ids, sel_r.token_ids)
+    assert torch.equal(out_o.view(torch.int16), out_r.view(torch.int16))
+
+
+def test_offload_single_query_that_cannot_fit_raises(gpu):
+    from cxldsagr_amd.layer import OffloadDSALayer
+    from cxldsagr_amd.token_pool import TokenPool
+
+    history, queries = 4096, 1
+    _, x = _offload_inputs(gpu, history, queries, seed=23)
+    pool = TokenPool(4160, 1024, device=gpu)
+    session = pool.allocate_session(4160)
+    layer = OffloadDSALayer(pool, session, history + queries)
+    layer.write_history(x["index_k"][:history], x["kv"][:history])
+    with pytest.raises(ValueError, match="at least one query"):
+        layer.forward(x["index_q"], x["index_k"][history:], x["weights"], x["mla_q"],
+                      x["kv"][history:])
