@@ -209,8 +209,10 @@ class OffloadDSALayer:
     """
 
     def __init__(self, pool, session, capacity, *, topk=2048, scale=576**-0.5, layer_idx=0):
-        if type(capacity) is not int or capacity < 1 or capacity > session.capacity:
-            raise ValueError("capacity must be a positive integer within the session's pages")
+        # The index-K capacity may exceed the session's host pages: transient
+        # candidate tokens have index keys but no host records.
+        if type(capacity) is not int or capacity < 1:
+            raise ValueError("capacity must be a positive integer")
         self.pool, self.session = pool, session
         self.device = pool.device
         self.capacity, self.topk, self.scale, self.layer_idx = capacity, topk, scale, layer_idx

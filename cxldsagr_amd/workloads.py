@@ -56,6 +56,9 @@ class LayerInputs:
 def make_layer_inputs(history, queries, *, seed=947, heads=128, heavy_fraction=0.05,
                       spans=None):
     """Inputs of one DSA layer with ``history`` cached tokens and ``queries`` new ones."""
+    if queries < 1:
+        # The heavy-hitter direction is the mean query; without queries it is undefined.
+        raise ValueError("make_layer_inputs needs at least one query token")
     gen = torch.Generator().manual_seed(seed)
     tokens = history + queries
     index_q = torch.randn(queries, 64, 128, generator=gen).bfloat16()

@@ -67,11 +67,11 @@ def test_config3_multi_user_two_rounds(gpu):
     identity = torch.arange(pages, dtype=torch.int32, device=gpu)
     users = []
     for u in range(USERS):
-        inputs = make_layer_inputs(HISTORY, 0, seed=947 + u)
+        inputs = make_layer_inputs(HISTORY, QUERIES, seed=947 + u)
         session = pool.allocate_session(HISTORY)
         layer = OffloadDSALayer(pool, session, tokens)
-        kv = inputs.kv.to(gpu)
-        layer.write_history(inputs.index_k.to(gpu), kv)
+        kv = inputs.kv[:HISTORY].to(gpu)
+        layer.write_history(inputs.index_k[:HISTORY].to(gpu), kv)
         resident = torch.zeros(pages, 64, 656, dtype=torch.uint8, device=gpu)
         pack_kv_fp8(kv, resident, identity)
         users.append((layer, resident))
@@ -95,6 +95,8 @@ def test_config3_multi_user_two_rounds(gpu):
             torch.cuda.synchronize()
             assert pool.check_status() == 0
             assert layer.session.written == HISTORY
+            # Every row selects TOPK real tokens (no padding, no non-finite score).
+            assert bool((selection.token_ids >= 0).all())
             assert torch.equal(out.view(torch.int16), expected.view(torch.int16)), (rnd, u)
             if rnd == 0 and u == 0:
                 ids = selection.token_ids.cpu().numpy()
@@ -112,6 +114,7 @@ def test_config3_multi_user_two_rounds(gpu):
         metrics = pool.metrics()
         print(f"config3 round {rnd + 1}: live slots {live}, recalled so far "
               f"{metrics['recalled_records']}, evicted {metrics['evicted_records']}", flush=True)
-        assert live <= SLOTS
+        assert 0 < live <= SLOTS
     # 16 users x ~64K selected history each cannot stay resident in 262,144 slots.
     assert pool.metrics()["evicted_records"] > 0
+    assert pool.metrics()["recalled_records"] > SLOTS

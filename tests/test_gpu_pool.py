@@ -157,6 +157,7 @@ def test_offload_layer_splits_queries_and_matches_resident_layer(gpu):
                                  x["mla_q"], x["kv"][history:])
     torch.cuda.synchronize()
     assert torch.equal(sel_o.token_ids, sel_r.token_ids)
+    assert bool((sel_o.token_ids >= 0).all())
     assert layer.capacity_splits >= 1
     assert pool.check_status() == 0
     assert torch.equal(out_o.view(torch.int16), out_r.view(torch.int16))
@@ -185,6 +186,8 @@ def test_offload_layer_transient_candidates(gpu):
     assert session.written == history
     assert layer.capacity_splits == 0 and pool.check_status() == 0
     assert torch.equal(sel_o.token_ids, sel_r.token_ids)
+    ids = sel_o.token_ids
+    assert bool((ids >= 0).all()) and bool((ids >= history).any()) and bool((ids < history).any())
     assert torch.equal(out_o.view(torch.int16), out_r.view(torch.int16))
 
 
