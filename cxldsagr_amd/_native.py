@@ -33,6 +33,7 @@ SIGNATURES = {
     "dsa_topk_radix": [_ptr, _i64, _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr],
     "dsa_topk_workspace_bytes": [_i64, ctypes.POINTER(ctypes.c_int64)],
     "dsa_topk_radix_split": [_ptr, _i64, _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr, _i64, _ptr],
+    "dsa_topk_radix_split_static": [_ptr, _i64, _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr],
     "dsa_kv_pack_fp8": [_ptr, _i64, _i64, _ptr, _i64, _ptr, _ptr, _ptr],
     "dsa_layer_prologue_fp8": [_ptr, _i64, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _ptr, _ptr,
                                _ptr, _i64, _i64, _ptr, _i64, _ptr, _ptr, _ptr],

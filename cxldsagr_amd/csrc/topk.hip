@@ -32,6 +32,8 @@
 // sorts its own top min(count, half) keys into a workspace and a second
 // launch merges the two sorted lists of every row (merge path), so Q rows
 // occupy 2Q compute units.
+#include <mutex>
+
 #include "dsa_common.h"
 #include "../../include/dsa_gfx950.h"
 
@@ -882,4 +884,62 @@ extern "C" int dsa_topk_radix_split(const float* scores, int64_t rows, int64_t c
                      (int)count, values, indices, out_ld);
   DSA_CHECK_LAUNCH("exact top-k");
   return kOk;
+}
+
+// ---- the same two-part top-k with its half-row lists in a library-owned
+// device array instead of a caller workspace, for callers that cannot
+// allocate. `scratch` is a host-side stand-in in host code: its device
+// address on each GPU comes from hipGetSymbolAddress, resolved once per
+// device with that device current, and only that address is passed to the
+// kernels. Every call on one GPU shares that GPU's array.
+namespace dsa {
+namespace {
+constexpr int64_t kStaticTopkRows = 512;
+__device__ __align__(256) uint64_t scratch[kStaticTopkRows * 2 * kMaxK];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mutex;
+uint64_t* scratch_ptr[kMaxDevices] = {};
+
+int scratch_for_current_device(uint64_t** out) {
+  int device = -1;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) {
+    set_error("hipGetDevice failed: %s", hipGetErrorString(err));
+    return kLaunchFailed;
+  }
+  DSA_CHECK_ARG(device >= 0 && device < kMaxDevices, "device ordinal %d out of range", device);
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (scratch_ptr[device] == nullptr) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || ptr == nullptr) {
+      set_error("hipGetSymbolAddress(scratch) failed on device %d: %s", device,
+                hipGetErrorString(err));
+      return kLaunchFailed;
+    }
+    scratch_ptr[device] = static_cast<uint64_t*>(ptr);
+  }
+  *out = scratch_ptr[device];
+  return kOk;
+}
+}  // namespace
+}  // namespace dsa
+
+extern "C" int dsa_topk_radix_split_static(const float* scores, int64_t rows, int64_t columns,
+                                           int64_t ld, int64_t k, float* values,
+                                           int32_t* indices, int64_t out_ld,
+                                           hipStream_t stream) {
+  using namespace dsa;
+  DSA_CHECK_ARG(rows >= 0 && rows <= kStaticTopkRows,
+                "dsa_topk_radix_split_static handles at most %lld rows per call (got %lld)",
+                (long long)kStaticTopkRows, (long long)rows);
+  if (rows == 0 || columns < 4 * kMaxK)
+    return dsa_topk_radix_split(scores, rows, columns, ld, k, values, indices, out_ld, nullptr, 0,
+                                stream);
+  uint64_t* keys = nullptr;
+  const int status = scratch_for_current_device(&keys);
+  if (status != kOk) return status;
+  return dsa_topk_radix_split(scores, rows, columns, ld, k, values, indices, out_ld, keys,
+                              (int64_t)sizeof(scratch), stream);
 }

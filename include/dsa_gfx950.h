@@ -123,6 +123,22 @@ int dsa_topk_radix_split(const float* scores, int64_t rows, int64_t columns, int
                          float* values, int32_t* indices, int64_t out_ld, void* workspace,
                          int64_t workspace_bytes, hipStream_t stream);
 
+/*
+ * A6, dsa_topk_radix_split without a workspace argument and without any
+ * allocation: the half-row lists go to a library-owned device array of
+ * 512 rows x 2 x 2048 x 8 bytes (16 MiB per GPU, held until the process
+ * ends), addressed through hipGetSymbolAddress once per device. At most 512
+ * rows per call; more is rejected. Same results as dsa_topk_radix_split.
+ * Calls that overlap on one GPU (several streams) race on the array; the
+ * contents of one call are never read by the next. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).
+ */
+int dsa_topk_radix_split_static(const float* scores, int64_t rows, int64_t columns, int64_t ld,
+                                int64_t k, float* values, int32_t* indices, int64_t out_ld,
+                                hipStream_t stream);
+
 
 /*
  * A8 producer - pack bf16 [tokens, 576] (512 latent + 64 RoPE) into the
