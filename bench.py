@@ -12,8 +12,9 @@ seed, seeded synthetic inputs of the DeepSeek-V3.2 shapes).
 Prints one JSON line. ``value`` is microseconds per layer (lower is better).
 ``roofline`` is for the kernel with the largest share of the step, timed with
 HIP events on the stream it is launched on; ``kernels`` lists every stage.
-``cpu_baseline`` times the numpy oracle of the same layer on a bounded sample
-of query rows on this machine's cores, scaled to 128 rows.
+``cpu_baseline`` times the torch CPU restatement of the same layer
+(``oracle/torch_layer.py``, pinned to the numpy oracle) on all 128 query rows
+with torch's intra-op threads on this process's cores.
 """
 
 import argparse
@@ -41,7 +42,7 @@ def parse_args():
     p.add_argument("--history", type=int, default=65536)
     p.add_argument("--queries", type=int, default=128)
     p.add_argument("--seed", type=int, default=947)
-    p.add_argument("--cpu-rows", type=int, default=8,
+    p.add_argument("--cpu-rows", type=int, default=128,
                    help="query rows of the CPU baseline sample (scaled to all rows)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--only", choices=["layer", "logits", "topk", "mla"], default=None,
@@ -116,29 +117,33 @@ def in_layer_stage_us(torch, layer, history, tokens, topk, iters, args):
 
 
 def cpu_baseline(inputs, rows_sample, topk):
+    """The same layer on the host: ``oracle.torch_layer`` (torch CPU kernels,
+    intra-op threads on every core of this process's affinity, capped by
+    OMP_NUM_THREADS where the environment sets a CPU share)."""
     import numpy as np
+    import torch
 
-    from oracle import layer as olayer
+    from oracle import kv_fp8
+    from oracle import torch_layer as tlayer
 
-    try:
-        from threadpoolctl import threadpool_info
-
-        threads = max([info.get("num_threads", 1) for info in threadpool_info()] or [1])
-    except Exception:  # pragma: no cover - reporting only
-        threads = os.cpu_count() or 1
+    threads = len(os.sched_getaffinity(0))
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
+    torch.set_num_threads(max(1, threads))
     history, queries = inputs.history, inputs.queries
-    index_q = inputs.index_q.float().cpu().numpy()
-    index_k = inputs.index_k.float().cpu().numpy()
-    weights = inputs.weights.cpu().numpy()
-    mla_q = inputs.mla_q.float().cpu().numpy()
-    kv_bits = inputs.kv.cpu().view(__import__("torch").int16).numpy().view(np.uint16)
-    cache = olayer.HistoryCache(index_k, kv_bits, fp8_records=True)
-    rows = np.linspace(0, queries - 1, rows_sample).round().astype(np.int64)
-    olayer.dsa_layer(index_q, weights, mla_q, cache, history, rows[:1], k=topk)  # warm-up
+    index_q = inputs.index_q.float().cpu()
+    weights = inputs.weights.float().cpu()
+    mla_q = inputs.mla_q.float().cpu()
+    kv_bits = inputs.kv.cpu().view(torch.int16).numpy().view(np.uint16)
+    records = torch.from_numpy(kv_fp8.decode_records(kv_fp8.encode_records(kv_bits)))
+    cache = tlayer.HistoryCache(inputs.index_k.float().cpu(), records)  # resident, as on the GPU
+    rows_sample = min(max(1, rows_sample), queries)
+    rows = torch.from_numpy(np.linspace(0, queries - 1, rows_sample).round().astype(np.int64))
+    tlayer.dsa_layer(index_q, weights, mla_q, cache, history, rows[:1], k=topk)  # warm-up
     times = []
     for _ in range(3):
         t0 = time.perf_counter_ns()
-        olayer.dsa_layer(index_q, weights, mla_q, cache, history, rows, k=topk)
+        tlayer.dsa_layer(index_q, weights, mla_q, cache, history, rows, k=topk)
         times.append((time.perf_counter_ns() - t0) / 1e3)
     per_layer = sorted(times)[1] * queries / len(rows)
     cpu_model = ""
@@ -149,14 +154,15 @@ def cpu_baseline(inputs, rows_sample, topk):
                 break
     except OSError:
         pass
+    scaled = "" if len(rows) == queries else f", scaled x{queries / len(rows):g}"
     return {
         "value": round(per_layer, 1),
         "unit": "us/layer",
-        "cores": int(threads),
+        "cores": int(torch.get_num_threads()),
         "kind": "port",
-        "sample": f"numpy oracle layer (A1 Q quantise, A4 logits, A6 top-k, A7 MLA over "
-                  f"dequantised fp8 records) on {len(rows)} of {queries} query rows, median of 3, "
-                  f"scaled x{queries / len(rows):g}; resident K/KV caches prebuilt as on the GPU",
+        "sample": f"torch CPU restatement of the oracle layer (A1 Q quantise, A4 logits, A6 "
+                  f"top-k, A7 MLA over dequantised fp8 records), {len(rows)} of {queries} query "
+                  f"rows, median of 3{scaled}; resident K/KV caches prebuilt as on the GPU",
         "cpu": cpu_model,
         "affinity": len(os.sched_getaffinity(0)),
     }

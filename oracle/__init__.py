@@ -1,7 +1,7 @@
 """CPU oracle for the DeepSeek-V3.2 DSA prefill hot path.
 
-TEST INFRASTRUCTURE ONLY. This package is a numpy restatement of the
-reference algorithms and exists to check the HIP kernels. Only ``tests/``,
+TEST INFRASTRUCTURE ONLY. This package is a numpy (and, for the timed CPU
+baseline, torch CPU) restatement of the reference algorithms and exists to check the HIP kernels. Only ``tests/``,
 ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
 it, and only as the checker (or as the timed CPU baseline). The product path in
 ``cxldsagr_amd`` never imports it and fails loudly when the HIP library is
@@ -24,6 +24,8 @@ reference checkout):
                    ``operators/common/kv_transfer.py:21-68``.
 * ``layer``      - the CPU DSA layer in the order of
                    ``models/deepseek_v32/attention.py:276-425``.
+* ``torch_layer`` - the same layer on torch's CPU kernels, multi-threaded: the
+                   timed CPU baseline of ``bench.py`` (pinned to ``layer``).
 
 Every function is pinned by a check in ``tests/test_oracle_*.py`` that does not
 retype its formula (golden vectors, library routines, closed forms, brute
