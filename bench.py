@@ -381,15 +381,74 @@ def bench_config4(args):
     print(json.dumps(result))
 
 
+def pcie_reference(pool, records=262144, reps=5, seed=11):
+    """Host-to-device rates on this box for the config-3 recall to be judged by:
+    the pinned contiguous hipMemcpyAsync peak (the SDMA engines), the zero-copy
+    record gather of the recall (csrc/gather.hip) on random and on address-
+    sorted host rows, and a staged alternative (CPU gather of the rows into a
+    pinned staging buffer, one hipMemcpyAsync, a device scatter into the slots)
+    timed end to end. Same record count and row size (656 B) throughout."""
+    import torch
+
+    from cxldsagr_amd import kv_transfer
+
+    device = pool.device
+    host = pool.host
+    rows = min(records, host.shape[0], pool.slots)
+    nbytes = rows * host.shape[1]
+    gen = torch.Generator().manual_seed(seed)
+    host_ids_cpu = torch.randperm(host.shape[0], generator=gen)[:rows]
+    device_ids_cpu = torch.randperm(rows, generator=gen)
+    dst = torch.empty((rows, host.shape[1]), dtype=torch.uint8, device=device)
+    host_ids = host_ids_cpu.to(device)
+    device_ids = device_ids_cpu.to(device)
+    sorted_ids = torch.sort(host_ids).values
+    staging = torch.empty((rows, host.shape[1]), dtype=torch.uint8, pin_memory=True)
+    dstage = torch.empty_like(dst)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        return nbytes * reps / (time.perf_counter() - t0) / 1e9
+
+    def staged():
+        torch.index_select(host, 0, host_ids_cpu, out=staging)
+        kv_transfer.copy_host_records_async(staging, dstage, host_start=0, device_start=0, count=rows)
+        dst.index_copy_(0, device_ids, dstage)
+
+    result = {
+        "records": rows,
+        "bytes": nbytes,
+        "memcpy_h2d_GBps": timed(lambda: kv_transfer.copy_host_records_async(
+            host, dst, host_start=0, device_start=0, count=rows)),
+        "zero_copy_gather_random_GBps": timed(lambda: kv_transfer.gather_host_records(
+            host, dst, host_ids, device_ids)),
+        "zero_copy_gather_sorted_GBps": timed(lambda: kv_transfer.gather_host_records(
+            host, dst, sorted_ids, device_ids)),
+        "staged_cpu_gather_sdma_GBps": timed(staged),
+        "cpu_threads": torch.get_num_threads(),
+    }
+    if kv_transfer.transfer_status(device):
+        raise RuntimeError("reference gather flagged an invalid id")
+    return {k: round(v, 2) if isinstance(v, float) else v for k, v in result.items()}
+
+
 def bench_config3(args):
     """GR multi-user recall: `users` sessions of 65536 fp8 history records
     in a pinned host arena, a shared HBM pool of 25 % of all history (262,144 slots for 16
-    users), resident indexer keys for every user, two rounds of 128 fresh candidate tokens per
+    users), resident indexer keys for every user, rounds of 128 fresh candidate tokens per
     user. Per user and layer: logits -> top-k -> exact recall (gather of the misses from pinned
-    host) -> sparse MLA over the pool."""
+    host) -> sparse MLA over the pool. Rounds 1-2 run the users one after another, as the
+    reference's runner does; rounds 3-4 run them through ``MultiUserStep`` (each user's recall
+    on a second stream, overlapping its neighbours' indexer and sparse MLA)."""
     import torch
 
-    from cxldsagr_amd import indexer
+    from cxldsagr_amd.layer import OffloadDSALayer
+    from cxldsagr_amd.multi_user import MultiUserStep
     from cxldsagr_amd.token_pool import TokenPool
     from cxldsagr_amd.workloads import make_layer_inputs
 
@@ -397,72 +456,73 @@ def bench_config3(args):
     users, history, queries, topk = args.users, 65536, 128, 2048
     tokens = history + queries
     slots = users * history // 4
-    pool = TokenPool(users * history, slots, device=device, candidate_slots=queries,
+    pool = TokenPool(users * history, slots, device=device, candidate_slots=2 * queries,
                      history_capacity=history)
-    state = []
+    layers = []
     for u in range(users):
         inputs = make_layer_inputs(history, queries, seed=args.seed + u)
-        session = pool.allocate_session(history)
-        pool.write_history(session, inputs.kv[:history].to(device))
-        keys = torch.empty((tokens, 128), dtype=torch.float8_e4m3fn, device=device)
-        scales = torch.empty(tokens, dtype=torch.float32, device=device)
-        indexer.quantize_into(inputs.index_k[:history].to(device), keys[:history], scales[:history])
-        state.append({"session": session, "keys": keys, "scales": scales,
-                      "history_index_k": None})
+        layer = OffloadDSALayer(pool, pool.allocate_session(history), tokens, topk=topk)
+        layer.write_history(inputs.index_k[:history].to(device), inputs.kv[:history].to(device))
+        layers.append(layer)
         del inputs
     torch.cuda.synchronize()
+    step = MultiUserStep(layers)
 
     def round_inputs(round_seed):
         per_user = []
         for u in range(users):
             # Fresh candidates: new queries, index keys and KV for the 128 new tokens.
             fresh = make_layer_inputs(0, queries, seed=round_seed * 1000 + u)
-            per_user.append({k: getattr(fresh, k).to(device) for k in
-                             ("index_q", "index_k", "weights", "mla_q", "kv")})
+            per_user.append(tuple(getattr(fresh, k).to(device) for k in
+                                  ("index_q", "index_k", "weights", "mla_q", "kv")))
         return per_user
 
-    def run_user(u, x, timing):
-        st = state[u]
-        q8, _, w_eff = indexer.quantize_index_folded(x["index_q"], x["weights"])
-        indexer.quantize_into(x["index_k"], st["keys"][history:], st["scales"][history:])
-        scores = indexer.logits(q8, st["keys"], w_eff, st["scales"], history, _pad_to_stride=True)
-        _, ids = indexer.exact_topk(scores, topk)
-        pool.write_candidates(x["kv"])
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        physical = pool.ensure(ids, st["session"], written=tokens, transient_start=history)
-        e1.record()
-        timing.append((e0, e1))
-        return pool.attend(x["mla_q"], physical, 576**-0.5)
+    def sequential(batches, timing):
+        for layer, (index_q, index_k, weights, mla_q, kv) in zip(layers, batches):
+            ids = layer.select(index_q, index_k, weights)
+            pool.write_candidates(kv)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            physical = pool.ensure(ids, layer.session, written=tokens, transient_start=history)
+            e1.record()
+            timing.append((e0, e1))
+            pool.attend(mla_q, physical, layer.scale)
 
     rounds = []
-    for r in range(2):
-        x = round_inputs(r + 1)
+    for r, mode in enumerate(("sequential", "sequential", "overlapped", "overlapped")):
+        batches = round_inputs(r + 1)
         before = pool.metrics()["recalled_records"]
         timing = []
         torch.cuda.synchronize()
         start = torch.cuda.Event(enable_timing=True)
         stop = torch.cuda.Event(enable_timing=True)
         start.record()
-        for u in range(users):
-            run_user(u, x[u], timing)
+        if mode == "sequential":
+            sequential(batches, timing)
+        else:
+            step.transient_round(batches)
         stop.record()
         torch.cuda.synchronize()
         pool.check_status()
         recalled = pool.metrics()["recalled_records"] - before
-        fetch_us = sum(a.elapsed_time(b) for a, b in timing) * 1e3
         fetch_bytes = recalled * 656
-        rounds.append({
+        entry = {
             "round": r + 1,
+            "mode": mode,
             "layer_us": round(start.elapsed_time(stop) * 1e3, 1),
             "fetch_records": recalled,
             "fetch_bytes_per_layer": fetch_bytes,
             "fetch_bytes_per_user": fetch_bytes // users,
-            "recall_us": round(fetch_us, 1),
-            "pcie_GBps": round(fetch_bytes / fetch_us / 1e3, 2) if fetch_us > 0 else None,
-        })
+        }
+        if timing:
+            fetch_us = sum(a.elapsed_time(b) for a, b in timing) * 1e3
+            entry["recall_us"] = round(fetch_us, 1)
+            entry["pcie_GBps"] = round(fetch_bytes / fetch_us / 1e3, 2) if fetch_us > 0 else None
+        else:
+            entry["pcie_GBps_over_layer"] = round(fetch_bytes / (entry["layer_us"] * 1e3), 2)
+        rounds.append(entry)
     print(json.dumps({"config": 3, "users": users, "history": history, "queries": queries,
-                      "pool_slots": slots, "rounds": rounds}))
+                      "pool_slots": slots, "rounds": rounds, "pcie_reference": pcie_reference(pool)}))
 
 
 if __name__ == "__main__":

@@ -127,13 +127,17 @@ __global__ __launch_bounds__(kClassifyThreads) void recall_classify(
   }
 }
 
+// Sort keys of the victim order; kept slots (the sentinel, this selection's
+// hits and, with keep_floor >= 0, every slot stamped at or after keep_floor)
+// sort last and are never chosen.
 __global__ void recall_victim_keys(const int64_t* __restrict__ d2h,
                                    const int64_t* __restrict__ priority,
                                    const uint32_t* __restrict__ kept_bits, int64_t slots,
-                                   uint64_t* __restrict__ keys) {
+                                   int64_t keep_floor, uint64_t* __restrict__ keys) {
   const int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (s > slots) return;
-  const bool kept = s == 0 || ((kept_bits[s >> 5] >> (s & 31)) & 1u);
+  const bool kept = s == 0 || ((kept_bits[s >> 5] >> (s & 31)) & 1u) ||
+                    (keep_floor >= 0 && d2h[s] != kMissing && priority[s] >= keep_floor);
   if (kept) {
     keys[s] = ~0ull;
     return;
@@ -191,13 +195,14 @@ __global__ __launch_bounds__(256) void recall_gather(const uint8_t* __restrict__
 }
 
 // Selected id -> physical pool row. History ids map through h2d; candidate
-// ids (transient_start <= id < written) to rows slots + 1 + id -
-// transient_start, which must lie inside the record rows. Every other id
+// ids (transient_start <= id < written) to rows slots + 1 + candidate_offset
+// + id - transient_start, which must lie inside the record rows. Every other id
 // (padding, unwritten, past the candidate rows) maps to -1, so that a bad
 // selection reads no stale record (recall_mark has flagged it in status).
 __global__ void recall_map(const int32_t* __restrict__ indices, int64_t n, int64_t history_end,
                            int64_t written, int64_t transient_start, int64_t slots,
-                           int64_t record_rows, const int32_t* __restrict__ page_table,
+                           int64_t candidate_offset, int64_t record_rows,
+                           const int32_t* __restrict__ page_table,
                            const int32_t* __restrict__ h2d, int32_t* __restrict__ physical) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
@@ -206,7 +211,7 @@ __global__ void recall_map(const int32_t* __restrict__ indices, int64_t n, int64
   if (id >= 0 && id < history_end) {
     out = h2d[to_global(page_table, id)];
   } else if (transient_start >= 0 && id >= transient_start && id < written) {
-    const int64_t row = slots + 1 + id - transient_start;
+    const int64_t row = slots + 1 + candidate_offset + id - transient_start;
     if (row < record_rows) out = (int32_t)row;
   }
   physical[i] = out;
@@ -268,15 +273,22 @@ extern "C" int dsa_pool_workspace_bytes(int64_t slots, int64_t history_capacity,
   return kOk;
 }
 
-extern "C" int dsa_pool_recall(const int32_t* indices, int64_t n, const int32_t* page_table,
-                               int64_t history_end, int64_t written, int64_t transient_start,
-                               int64_t slots, const void* host, int64_t host_rows, void* records,
-                               int64_t record_rows, int64_t record_bytes, int32_t* h2d,
-                               int64_t* d2h, int64_t* priority, int64_t protect_stamp,
-                               int64_t chosen_stamp, void* workspace, int64_t workspace_bytes,
-                               int64_t history_capacity, int union_checked, int64_t* stats,
-                               int32_t* status, int32_t* physical, hipStream_t stream) {
-  using namespace dsa;
+namespace dsa {
+namespace {
+
+// One recall on `stream` (the steps in the header). keep_floor >= 0 also
+// keeps every slot stamped at or after it (a previous selection still being
+// read on another stream); candidate ids map to the candidate rows from
+// candidate_offset on.
+int recall_impl(const int32_t* indices, int64_t n, const int32_t* page_table,
+                int64_t history_end, int64_t written, int64_t transient_start,
+                int64_t slots, const void* host, int64_t host_rows, void* records,
+                int64_t record_rows, int64_t record_bytes, int32_t* h2d,
+                int64_t* d2h, int64_t* priority, int64_t protect_stamp,
+                int64_t chosen_stamp, void* workspace, int64_t workspace_bytes,
+                int64_t history_capacity, int union_checked, int64_t* stats,
+                int32_t* status, int32_t* physical, int64_t keep_floor,
+                int64_t candidate_offset, hipStream_t stream) {
   DSA_CHECK_ARG(n >= 0 && slots >= 1 && history_end >= 0 && written >= history_end,
                 "invalid recall shape");
   DSA_CHECK_ARG(history_end <= history_capacity, "history exceeds the planned workspace");
@@ -287,8 +299,12 @@ extern "C" int dsa_pool_recall(const int32_t* indices, int64_t n, const int32_t*
                 "records must hold slots + 1 rows of a 16-byte multiple width");
   DSA_CHECK_ARG(transient_start < 0 || transient_start >= history_end,
                 "the transient suffix starts after the host-backed history");
-  DSA_CHECK_ARG(transient_start < 0 || written - transient_start <= record_rows - (slots + 1),
+  DSA_CHECK_ARG(candidate_offset >= 0, "candidate offset must be nonnegative");
+  DSA_CHECK_ARG(transient_start < 0 ||
+                    written - transient_start + candidate_offset <= record_rows - (slots + 1),
                 "transient suffix exceeds candidate slot capacity");
+  DSA_CHECK_ARG(keep_floor < 0 || keep_floor < protect_stamp,
+                "the keep floor must precede this recall's stamps");
   DSA_CHECK_ARG(protect_stamp >= 0 && chosen_stamp > protect_stamp && chosen_stamp < 0x7FFFFFFF,
                 "invalid FIFO timestamps");
   DSA_CHECK_ARG(indices && page_table && h2d && d2h && priority && stats && physical && records &&
@@ -319,7 +335,7 @@ extern "C" int dsa_pool_recall(const int32_t* indices, int64_t n, const int32_t*
                      history_end, page_table, h2d, priority, ws.kept_bits, protect_stamp,
                      ws.misses, ws.counters, stats);
   hipLaunchKernelGGL(recall_victim_keys, dim3((unsigned)((slots + 1 + 255) / 256)), dim3(256), 0,
-                     stream, d2h, priority, ws.kept_bits, slots, ws.keys);
+                     stream, d2h, priority, ws.kept_bits, slots, keep_floor, ws.keys);
   size_t sort_bytes = ws.sort_bytes;
   hipError_t err = rocprim::radix_sort_keys(ws.sort_temp, sort_bytes, ws.keys, ws.sorted,
                                             (size_t)(slots + 1), 0, 64, stream, false);
@@ -341,8 +357,40 @@ extern "C" int dsa_pool_recall(const int32_t* indices, int64_t n, const int32_t*
   }
   if (n > 0)
     hipLaunchKernelGGL(recall_map, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
-                       indices, n, history_end, written, transient_start, slots, record_rows,
-                       page_table, h2d, physical);
+                       indices, n, history_end, written, transient_start, slots,
+                       candidate_offset, record_rows, page_table, h2d, physical);
   DSA_CHECK_LAUNCH("exact recall");
   return kOk;
+}
+
+}  // namespace
+}  // namespace dsa
+
+extern "C" int dsa_pool_recall(const int32_t* indices, int64_t n, const int32_t* page_table,
+                               int64_t history_end, int64_t written, int64_t transient_start,
+                               int64_t slots, const void* host, int64_t host_rows, void* records,
+                               int64_t record_rows, int64_t record_bytes, int32_t* h2d,
+                               int64_t* d2h, int64_t* priority, int64_t protect_stamp,
+                               int64_t chosen_stamp, void* workspace, int64_t workspace_bytes,
+                               int64_t history_capacity, int union_checked, int64_t* stats,
+                               int32_t* status, int32_t* physical, hipStream_t stream) {
+  return dsa::recall_impl(indices, n, page_table, history_end, written, transient_start, slots, host,
+                          host_rows, records, record_rows, record_bytes, h2d, d2h, priority,
+                          protect_stamp, chosen_stamp, workspace, workspace_bytes,
+                          history_capacity, union_checked, stats, status, physical, -1, 0, stream);
+}
+
+extern "C" int dsa_pool_recall_pipelined(
+    const int32_t* indices, int64_t n, const int32_t* page_table, int64_t history_end,
+    int64_t written, int64_t transient_start, int64_t slots, const void* host, int64_t host_rows,
+    void* records, int64_t record_rows, int64_t record_bytes, int32_t* h2d, int64_t* d2h,
+    int64_t* priority, int64_t protect_stamp, int64_t chosen_stamp, void* workspace,
+    int64_t workspace_bytes, int64_t history_capacity, int union_checked, int64_t* stats,
+    int32_t* status, int32_t* physical, int64_t keep_floor, int64_t candidate_offset,
+    hipStream_t stream) {
+  return dsa::recall_impl(indices, n, page_table, history_end, written, transient_start, slots, host,
+                          host_rows, records, record_rows, record_bytes, h2d, d2h, priority,
+                          protect_stamp, chosen_stamp, workspace, workspace_bytes,
+                          history_capacity, union_checked, stats, status, physical, keep_floor,
+                          candidate_offset, stream);
 }

@@ -247,12 +247,7 @@ class OffloadDSALayer:
             raise ValueError("query batch exceeds the layer capacity or inputs disagree in length")
         if transient and rows > self.pool.candidate_slots:
             raise ValueError("transient suffix exceeds candidate slot capacity")
-        q8, _, folded = indexer.quantize_index_folded(index_q, weights)
-        indexer.quantize_into(index_k, self.index_keys[position:end], self.index_scales[position:end])
-        scores = indexer.logits(q8, self.index_keys[:end], folded, self.index_scales[:end],
-                                position, _pad_to_stride=end >= self.topk)
-        _, ids = indexer.exact_topk(scores, self.topk)
-        del scores
+        ids = self.select(index_q, index_k, weights)
         if transient:
             self.pool.write_candidates(kv)
             out = self.consume(q, ids, written=end, transient_start=position)
@@ -260,6 +255,22 @@ class OffloadDSALayer:
             self.pool.write_history(self.session, kv)
             out = self.consume(q, ids, written=end)
         return out, TokenSelection(ids)
+
+    def select(self, index_q, index_k, weights):
+        """The indexer half of ``forward`` for a batch at ``session.written``:
+        quantise the batch's index Q (folding its scales into the head
+        weights) and index K (into the resident cache), fp8 logits over every
+        visible key, exact top-k; returns the int32 ``[rows, topk]`` ids."""
+        position = self.session.written
+        end = position + len(index_q)
+        if end > self.capacity or len(index_k) != len(index_q) or len(weights) != len(index_q):
+            raise ValueError("query batch exceeds the layer capacity or inputs disagree in length")
+        q8, _, folded = indexer.quantize_index_folded(index_q, weights)
+        indexer.quantize_into(index_k, self.index_keys[position:end], self.index_scales[position:end])
+        scores = indexer.logits(q8, self.index_keys[:end], folded, self.index_scales[:end],
+                                position, _pad_to_stride=end >= self.topk)
+        _, ids = indexer.exact_topk(scores, self.topk)
+        return ids
 
     def consume(self, q, ids, *, written, transient_start=None):
         """Recall then sparse MLA over the pool, splitting the query batch on

@@ -1,0 +1,96 @@
+"""Several sessions' layer steps over one shared token pool, the recall of one
+user overlapping the indexer and sparse MLA of its neighbours.
+
+The reference's multi-user GR runner steps its users one after another per
+layer (``serving/persistent.py:56``; per user ``_consume`` of
+``models/deepseek_v32/attention.py:201-235``: recall, then sparse MLA), so
+every user's PCIe recall is exposed. Here one layer of a round of users runs
+as a two-stream pipeline on the pool's device:
+
+* compute stream: user u's indexer (quantise, logits, top-k) and candidate
+  write, then user u - 1's sparse MLA over the pool;
+* recall stream: user u's exact recall, after user u's top-k and after user
+  u - 2's sparse MLA (the last reader of the slots user u may evict).
+
+User u's recall keeps user u - 1's slots out of its victims (``keep_since``)
+while that user's MLA may still be reading them, and users alternate between
+two halves of the candidate rows, so no row is overwritten before its reader
+is done. Every selected id still resolves to a row holding its record, so each
+user's output equals, bit for bit, the sequential step's; only the pool's
+victim choice (which slots hold what) differs from the sequential FIFO order.
+"""
+
+import torch
+
+from cxldsagr_amd.layer import OffloadDSALayer, TokenSelection
+
+
+class MultiUserStep:
+    """One layer for a list of ``OffloadDSALayer`` s that share one ``TokenPool``.
+
+    The pool needs candidate rows for two batches in flight
+    (``candidate_slots >= 2 * rows``) and room for two users' selections at
+    once (``2 * history <= slots`` for every session, so that a recall never
+    runs out of victims while the previous user's slots are kept).
+    """
+
+    def __init__(self, layers):
+        if not layers or not all(isinstance(layer, OffloadDSALayer) for layer in layers):
+            raise ValueError("MultiUserStep needs a nonempty list of OffloadDSALayer")
+        pool = layers[0].pool
+        if any(layer.pool is not pool for layer in layers):
+            raise ValueError("all sessions must share one token pool")
+        self.layers, self.pool, self.device = list(layers), pool, pool.device
+        self._recall_stream = torch.cuda.Stream(self.device)
+
+    def transient_round(self, batches):
+        """GR candidate step for every user: ``batches[u]`` is
+        ``(index_q, index_k, weights, q, kv)`` of user u's candidate tokens at
+        its ``session.written``. Returns ``[(out, TokenSelection), ...]`` in
+        user order, enqueued on the current stream (no host synchronisation)."""
+        if len(batches) != len(self.layers):
+            raise ValueError("one batch per user")
+        pool = self.pool
+        rows = {len(b[0]) for b in batches}
+        if len(rows) != 1:
+            raise ValueError("every user's batch must have the same number of rows")
+        rows = rows.pop()
+        if 2 * rows > pool.candidate_slots:
+            raise ValueError("overlapped users need candidate rows for two batches")
+        for layer, batch in zip(self.layers, batches):
+            if 2 * layer.session.written > pool.slots:
+                raise ValueError("overlapped recall needs room for two users' selections")
+            if any(len(x) != rows for x in batch):
+                raise ValueError("query batch inputs disagree in length")
+        compute = torch.cuda.current_stream(self.device)
+        recall = self._recall_stream
+        n = len(self.layers)
+        selected, recalled, done = ([torch.cuda.Event() for _ in range(n)] for _ in range(3))
+        ids, physical, outs = [None] * n, [None] * n, [None] * n
+        keep = None
+        for u in range(n + 1):
+            if u < n:
+                layer = self.layers[u]
+                index_q, index_k, weights, q, kv = batches[u]
+                position = layer.session.written
+                offset = (u % 2) * rows
+                ids[u] = layer.select(index_q, index_k, weights)
+                pool.write_candidates(kv, offset=offset)
+                selected[u].record(compute)
+                recall.wait_event(selected[u])
+                if u >= 2:
+                    recall.wait_event(done[u - 2])
+                with torch.cuda.stream(recall):
+                    physical[u] = pool.ensure(ids[u], layer.session, written=position + rows,
+                                              transient_start=position, keep_since=keep,
+                                              candidate_offset=offset)
+                keep = pool.last_stamp
+                ids[u].record_stream(recall)
+                recalled[u].record(recall)
+            if u >= 1:
+                v = u - 1
+                compute.wait_event(recalled[v])
+                physical[v].record_stream(compute)
+                outs[v] = pool.attend(batches[v][3], physical[v], self.layers[v].scale)
+                done[v].record(compute)
+        return [(outs[u], TokenSelection(ids[u])) for u in range(n)]

@@ -73,6 +73,7 @@ class TokenPool:
         self.priority = torch.full((slots + 1,), -1, dtype=torch.int64, device=self.device)
         self.priority[0] = MISSING
         self.clock = 0
+        self.last_stamp = None  # protect stamp of the latest recall
         nbytes = _native.ctypes.c_int64(0)
         _native.call("dsa_pool_workspace_bytes", slots, self.history_capacity,
                      _native.ctypes.byref(nbytes))
@@ -117,13 +118,22 @@ class TokenPool:
                               token_offset=self.slots + 1 + offset)
 
     # ---------------------------------------------------------------- recall
-    def ensure(self, indices, session, *, written=None, transient_start=None):
+    def ensure(self, indices, session, *, written=None, transient_start=None, keep_since=None,
+               candidate_offset=0):
         """Exact recall of a logical selection; returns int32 physical pool ids.
 
         ``indices`` int32 ``[Q, K]`` on the pool device, ``-1`` padding. Ids
         below ``transient_start`` (or ``written``) are host-backed history;
         ids at or past ``transient_start`` are candidate rows. No host
         synchronisation unless the history exceeds the pool.
+
+        Overlapped users (no reference counterpart): ``keep_since`` (the
+        ``last_stamp`` of an earlier recall whose selection another stream
+        still reads) keeps every slot that recall or a later one stamped out
+        of the victims, and ``candidate_offset`` moves this call's candidate
+        rows by that many rows (``write_candidates(..., offset=...)``). The
+        pool contents then differ from the sequential FIFO order; every id
+        still maps to a row holding its record.
         """
         if indices.dtype != torch.int32 or indices.device != self.device:
             raise ValueError("indices must be int32 tensors on the pool device")
@@ -131,7 +141,13 @@ class TokenPool:
         history = written if transient_start is None else transient_start
         if history > session.written:
             raise ValueError("host-backed history exceeds the session's written records")
-        if transient_start is not None and not 0 <= written - transient_start <= self.candidate_slots:
+        if type(candidate_offset) is not int or candidate_offset < 0:
+            raise ValueError("candidate_offset must be a nonnegative integer")
+        if keep_since is not None and (type(keep_since) is not int or not 0 <= keep_since < self.clock):
+            raise ValueError("keep_since must be the stamp of an earlier recall")
+        if transient_start is not None and not (
+            0 <= written - transient_start <= self.candidate_slots - candidate_offset
+        ):
             # cache/sparse_token_cache.py:254-256
             raise ValueError("transient suffix exceeds candidate slot capacity")
         union_checked = 0
@@ -147,9 +163,12 @@ class TokenPool:
         physical = torch.empty_like(ids)
         protect, chosen = self.clock, self.clock + 1
         self.clock += 2
+        self.last_stamp = protect
+        pipelined = keep_since is not None or candidate_offset != 0
+        extra = (keep_since if keep_since is not None else -1, candidate_offset) if pipelined else ()
         with torch.cuda.device(self.device):
             _native.call(
-                "dsa_pool_recall",
+                "dsa_pool_recall_pipelined" if pipelined else "dsa_pool_recall",
                 _native.ptr(ids), ids.numel(), _native.ptr(session.page_table),
                 history, written, -1 if transient_start is None else transient_start,
                 self.slots, _native.ptr(self.host), self.host_capacity,
@@ -157,7 +176,7 @@ class TokenPool:
                 _native.ptr(self.h2d), _native.ptr(self.d2h), _native.ptr(self.priority),
                 protect, chosen, _native.ptr(self.workspace), self.workspace.numel(),
                 self.history_capacity, union_checked, _native.ptr(self.stats),
-                _native.ptr(self.status), _native.ptr(physical),
+                _native.ptr(self.status), _native.ptr(physical), *extra,
                 _native.stream_of(self.device),
             )
         return physical

@@ -257,6 +257,28 @@ int dsa_pool_recall(const int32_t* indices, int64_t n, const int32_t* page_table
                     int64_t workspace_bytes, int64_t history_capacity, int union_checked,
                     int64_t* stats, int32_t* status, int32_t* physical, hipStream_t stream);
 
+/*
+ * A10 for overlapped multi-user recall (no counterpart in the reference, whose
+ * users recall one after another): dsa_pool_recall with two more arguments.
+ * keep_floor >= 0 (below protect_stamp) also keeps every occupied slot whose
+ * priority is >= keep_floor out of the victims - pass the protect_stamp of the
+ * previous recall while that selection is still read by sparse MLA on another
+ * stream. candidate_offset >= 0 moves this call's candidate rows to
+ * slots + 1 + candidate_offset + id - transient_start (alternate halves of the
+ * candidate rows between users in flight). The victims then differ from the
+ * sequential FIFO order; every selected id still maps to a row holding its
+ * record. With keep_floor = -1 and candidate_offset = 0 it is dsa_pool_recall.
+ */
+int dsa_pool_recall_pipelined(const int32_t* indices, int64_t n, const int32_t* page_table,
+                              int64_t history_end, int64_t written, int64_t transient_start,
+                              int64_t slots, const void* host, int64_t host_rows, void* records,
+                              int64_t record_rows, int64_t record_bytes, int32_t* h2d,
+                              int64_t* d2h, int64_t* priority, int64_t protect_stamp,
+                              int64_t chosen_stamp, void* workspace, int64_t workspace_bytes,
+                              int64_t history_capacity, int union_checked, int64_t* stats,
+                              int32_t* status, int32_t* physical, int64_t keep_floor,
+                              int64_t candidate_offset, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -181,6 +181,62 @@ def test_logits_bounds_zero_weights_and_repeat_bit_exact(gpu):
     assert zero[visible].eq(0).all() and torch.isneginf(zero[~visible]).all()
 
 
+def _relu_rewrite_bound(q, k, w, s):
+    """Bound on |kernel - exact| per (query, key) for the kernel's head sum.
+
+    The kernel forms relu(s_h) w_h as (|s_h| + s_h) w_h / 2: the |s_h| half by
+    fp32 FMAs, the linear half as k . q' with q' = sum_h (w_h / 2) q_h carried
+    in four e4m3 digits (each digit the residual of the ones before to half an
+    e4m3 ulp: |q'_d - digits_d| <= 2^-16 max|q'|). With M = sum_h |w_h| sum_d
+    |q_hd k_d| and B = ||k||_1 max_d sum_h |w_h q_hd|, the fp32 dot products
+    and FMA chains add at most 2^-17 M + 2^-18 M + 2^-19 M and the digits and
+    the linear MFMA at most 2^-17 B + 2^-17 B, so |error| <= 2^-15 (M + B)
+    times the key scale, with room to spare. Keys whose 64 head products are
+    all negative are exactly 0 in the reference; here they are within it.
+    """
+    qd = q.float().double().cpu()
+    kd = k.float().double().cpu()
+    wd = w.double().cpu()
+    sd = s.double().cpu()
+    m = torch.einsum("qh,qhd,jd->qj", wd.abs(), qd.abs(), kd.abs())
+    b = kd.abs().sum(1)[None, :] * (wd.abs()[:, :, None] * qd.abs()).sum(1).amax(1)[:, None]
+    exact = torch.einsum("qh,qhj->qj", wd, torch.einsum("qhd,jd->qhj", qd, kd).clamp_min(0))
+    return exact * sd[None, :], 2.0**-15 * (m + b) * sd[None, :]
+
+
+def test_logits_relu_rewrite_bound_and_all_negative_keys(gpu):
+    """Keys whose 64 head dot products are all negative give exactly 0 in the
+    reference; the kernel's (|s| + s) / 2 rewrite leaves a residue that must
+    stay inside the stated bound, as must every other key's error."""
+    from cxldsagr_amd.indexer import logits
+
+    torch.manual_seed(77)
+    rows, columns = 12, 1536
+    q = torch.randn(rows, 64, 128).abs().to(torch.float8_e4m3fn)
+    k = torch.randn(columns, 128).to(torch.float8_e4m3fn)
+    negative = torch.zeros(columns, dtype=torch.bool)
+    negative[::2] = True
+    k[negative] = (-(torch.randn(int(negative.sum()), 128).abs() + 0.05)).to(torch.float8_e4m3fn)
+    w = torch.randn(rows, 64) * torch.logspace(-2, 1, rows)[:, None]  # both signs, wide range
+    s = torch.rand(columns) + 0.5
+    start = columns - rows
+    out = logits(q.to(gpu), k.to(gpu), w.to(gpu), s.to(gpu), start).cpu().double()
+    exact, bound = _relu_rewrite_bound(q, k, w, s)
+    visible = torch.arange(columns)[None, :] < (start + 1 + torch.arange(rows))[:, None]
+    assert torch.isneginf(out[~visible]).all()
+    err = (out - exact).abs()[visible]
+    assert (err <= bound[visible]).all(), float((err / bound[visible]).max())
+    zero_keys = visible & negative[None, :]
+    assert exact[zero_keys].eq(0).all()
+    residue = out[zero_keys].abs()
+    assert (residue <= bound[zero_keys]).all()
+    # The bound is tight enough to matter: far below the size of the logits.
+    assert float(bound[visible].max()) < 1e-2 * float(exact[visible].abs().max())
+    print(f"all-negative keys: max |residue| {float(residue.max()):.3e}, "
+          f"max residue / bound {float((residue / bound[zero_keys]).max()):.3f}; "
+          f"all keys: max err / bound {float((err / bound[visible]).max()):.3f}")
+
+
 def test_logits_rejects_invalid_inputs(gpu):
     from cxldsagr_amd.indexer import logits
 
