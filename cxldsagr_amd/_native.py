@@ -49,7 +49,7 @@ SIGNATURES = {
                         _ptr],
     "dsa_pool_recall_pipelined": [_ptr, _i64, _ptr, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr,
                                   _i64, _i64, _ptr, _ptr, _ptr, _i64, _i64, _ptr, _i64, _i64,
-                                  _int, _ptr, _ptr, _ptr, _i64, _i64, _ptr],
+                                  _int, _ptr, _ptr, _ptr, _i64, _i64, _ptr, _ptr],
 }
 
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}

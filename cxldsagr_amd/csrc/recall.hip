@@ -17,6 +17,7 @@
 // over the pool's slots, the role CUB's radix sort plays in the reference
 // (operators/deepseek_v32/indexer/csrc/echo_sparse_recall.cuh:191).
 #include <cstring>
+#include <mutex>
 #include <rocprim/device/device_radix_sort.hpp>
 
 #include "dsa_common.h"
@@ -28,6 +29,7 @@ namespace {
 constexpr int32_t kMissing = 0x7FFFFFFF;
 constexpr int kPage = 64;
 constexpr int kClassifyThreads = 1024;
+constexpr int kGatherBlocks = 128;
 
 enum Counter { kUnion = 0, kMisses = 1, kEvicted = 2, kCounters = 4 };
 enum StatusBits { kUnwritten = 4, kShortPool = 8 };
@@ -276,10 +278,33 @@ extern "C" int dsa_pool_workspace_bytes(int64_t slots, int64_t history_capacity,
 namespace dsa {
 namespace {
 
+// The event that orders a recall's gather after its assignment when the
+// gather runs on a stream of its own (one per device; a wait captures the
+// event's state when it is enqueued, so one event serves every call).
+hipEvent_t assign_event(int* rc) {
+  static std::mutex lock;
+  static hipEvent_t events[64] = {};
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) {
+    *rc = kLaunchFailed;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> guard(lock);
+  if (!events[device] && hipEventCreateWithFlags(&events[device], hipEventDisableTiming) != hipSuccess) {
+    events[device] = nullptr;
+    *rc = kLaunchFailed;
+  }
+  return events[device];
+}
+
 // One recall on `stream` (the steps in the header). keep_floor >= 0 also
 // keeps every slot stamped at or after it (a previous selection still being
 // read on another stream); candidate ids map to the candidate rows from
-// candidate_offset on.
+// candidate_offset on. A gather_stream other than `stream` takes the gather
+// of the missing records (after an event on `stream`), so that the next
+// recall's bookkeeping on `stream` overlaps it; the caller gives that next
+// recall another workspace and waits for the gather before reading the
+// records.
 int recall_impl(const int32_t* indices, int64_t n, const int32_t* page_table,
                 int64_t history_end, int64_t written, int64_t transient_start,
                 int64_t slots, const void* host, int64_t host_rows, void* records,
@@ -288,7 +313,7 @@ int recall_impl(const int32_t* indices, int64_t n, const int32_t* page_table,
                 int64_t chosen_stamp, void* workspace, int64_t workspace_bytes,
                 int64_t history_capacity, int union_checked, int64_t* stats,
                 int32_t* status, int32_t* physical, int64_t keep_floor,
-                int64_t candidate_offset, hipStream_t stream) {
+                int64_t candidate_offset, hipStream_t stream, hipStream_t gather_stream) {
   DSA_CHECK_ARG(n >= 0 && slots >= 1 && history_end >= 0 && written >= history_end,
                 "invalid recall shape");
   DSA_CHECK_ARG(history_end <= history_capacity, "history exceeds the planned workspace");
@@ -348,10 +373,24 @@ int recall_impl(const int32_t* indices, int64_t n, const int32_t* page_table,
                      stream, ws.sorted, ws.misses, ws.counters, h2d, d2h, priority, chosen_stamp,
                      ws.chosen, stats, status);
   if (host_rows > 0) {
+    // PCIe-bound: 128 work-groups (512 waves, one record each in flight)
+    // keep the link at its rate (64 do not) and leave most CUs to the
+    // kernels that overlap the copy.
     int64_t blocks = (history_end + 3) / 4;
-    if (blocks > 2048) blocks = 2048;
+    if (blocks > kGatherBlocks) blocks = kGatherBlocks;
     if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL(recall_gather, dim3((unsigned)blocks), dim3(256), 0, stream,
+    hipStream_t gs = stream;
+    if (gather_stream != stream) {
+      int erc = kOk;
+      hipEvent_t ev = assign_event(&erc);
+      if (erc != kOk || hipEventRecord(ev, stream) != hipSuccess ||
+          hipStreamWaitEvent(gather_stream, ev, 0) != hipSuccess) {
+        set_error("could not order the gather stream after the recall");
+        return kLaunchFailed;
+      }
+      gs = gather_stream;
+    }
+    hipLaunchKernelGGL(recall_gather, dim3((unsigned)blocks), dim3(256), 0, gs,
                        static_cast<const uint8_t*>(mapped), static_cast<uint8_t*>(records),
                        ws.misses, ws.chosen, ws.counters, record_bytes);
   }
@@ -377,7 +416,8 @@ extern "C" int dsa_pool_recall(const int32_t* indices, int64_t n, const int32_t*
   return dsa::recall_impl(indices, n, page_table, history_end, written, transient_start, slots, host,
                           host_rows, records, record_rows, record_bytes, h2d, d2h, priority,
                           protect_stamp, chosen_stamp, workspace, workspace_bytes,
-                          history_capacity, union_checked, stats, status, physical, -1, 0, stream);
+                          history_capacity, union_checked, stats, status, physical, -1, 0, stream,
+                          stream);
 }
 
 extern "C" int dsa_pool_recall_pipelined(
@@ -387,10 +427,10 @@ extern "C" int dsa_pool_recall_pipelined(
     int64_t* priority, int64_t protect_stamp, int64_t chosen_stamp, void* workspace,
     int64_t workspace_bytes, int64_t history_capacity, int union_checked, int64_t* stats,
     int32_t* status, int32_t* physical, int64_t keep_floor, int64_t candidate_offset,
-    hipStream_t stream) {
+    hipStream_t stream, hipStream_t gather_stream) {
   return dsa::recall_impl(indices, n, page_table, history_end, written, transient_start, slots, host,
                           host_rows, records, record_rows, record_bytes, h2d, d2h, priority,
                           protect_stamp, chosen_stamp, workspace, workspace_bytes,
                           history_capacity, union_checked, stats, status, physical, keep_floor,
-                          candidate_offset, stream);
+                          candidate_offset, stream, gather_stream ? gather_stream : stream);
 }

@@ -5,12 +5,18 @@ The reference's multi-user GR runner steps its users one after another per
 layer (``serving/persistent.py:56``; per user ``_consume`` of
 ``models/deepseek_v32/attention.py:201-235``: recall, then sparse MLA), so
 every user's PCIe recall is exposed. Here one layer of a round of users runs
-as a two-stream pipeline on the pool's device:
+as a three-stream pipeline on the pool's device:
 
 * compute stream: user u's indexer (quantise, logits, top-k) and candidate
   write, then user u - 1's sparse MLA over the pool;
-* recall stream: user u's exact recall, after user u's top-k and after user
-  u - 2's sparse MLA (the last reader of the slots user u may evict).
+* recall stream: user u's recall bookkeeping (union, victims, maps), after
+  user u's top-k and after user u - 2's copy (whose workspace it reuses);
+* copy stream: user u's copy of the missing records over PCIe, after user
+  u's bookkeeping and after user u - 1's sparse MLA. The copy kernel keeps
+  waves resident on every CU while the link drains, and the sparse MLA
+  kernel needs each SIMD's whole register file per wave, so the two would
+  not run side by side anyway: the copies and the MLAs alternate, and the
+  indexer and the recall bookkeeping of the next user hide under each copy.
 
 User u's recall keeps user u - 1's slots out of its victims (``keep_since``)
 while that user's MLA may still be reading them, and users alternate between
@@ -42,6 +48,8 @@ class MultiUserStep:
             raise ValueError("all sessions must share one token pool")
         self.layers, self.pool, self.device = list(layers), pool, pool.device
         self._recall_stream = torch.cuda.Stream(self.device)
+        self._copy_stream = torch.cuda.Stream(self.device)
+        pool.reserve_second_workspace()
 
     def transient_round(self, batches):
         """GR candidate step for every user: ``batches[u]`` is
@@ -63,9 +71,9 @@ class MultiUserStep:
             if any(len(x) != rows for x in batch):
                 raise ValueError("query batch inputs disagree in length")
         compute = torch.cuda.current_stream(self.device)
-        recall = self._recall_stream
+        recall, copy = self._recall_stream, self._copy_stream
         n = len(self.layers)
-        selected, recalled, done = ([torch.cuda.Event() for _ in range(n)] for _ in range(3))
+        selected, recalled, copied, done = ([torch.cuda.Event() for _ in range(n)] for _ in range(4))
         ids, physical, outs = [None] * n, [None] * n, [None] * n
         keep = None
         for u in range(n + 1):
@@ -79,17 +87,21 @@ class MultiUserStep:
                 selected[u].record(compute)
                 recall.wait_event(selected[u])
                 if u >= 2:
-                    recall.wait_event(done[u - 2])
+                    recall.wait_event(copied[u - 2])
+                if u >= 1:
+                    copy.wait_event(done[u - 1])
                 with torch.cuda.stream(recall):
                     physical[u] = pool.ensure(ids[u], layer.session, written=position + rows,
                                               transient_start=position, keep_since=keep,
-                                              candidate_offset=offset)
+                                              candidate_offset=offset, gather_stream=copy)
                 keep = pool.last_stamp
                 ids[u].record_stream(recall)
                 recalled[u].record(recall)
+                copied[u].record(copy)
             if u >= 1:
                 v = u - 1
                 compute.wait_event(recalled[v])
+                compute.wait_event(copied[v])
                 physical[v].record_stream(compute)
                 outs[v] = pool.attend(batches[v][3], physical[v], self.layers[v].scale)
                 done[v].record(compute)

@@ -74,6 +74,8 @@ class TokenPool:
         self.priority[0] = MISSING
         self.clock = 0
         self.last_stamp = None  # protect stamp of the latest recall
+        self._second_workspace = None  # for recalls whose copy runs on a gather stream
+        self._parity = 0
         nbytes = _native.ctypes.c_int64(0)
         _native.call("dsa_pool_workspace_bytes", slots, self.history_capacity,
                      _native.ctypes.byref(nbytes))
@@ -119,7 +121,7 @@ class TokenPool:
 
     # ---------------------------------------------------------------- recall
     def ensure(self, indices, session, *, written=None, transient_start=None, keep_since=None,
-               candidate_offset=0):
+               candidate_offset=0, gather_stream=None):
         """Exact recall of a logical selection; returns int32 physical pool ids.
 
         ``indices`` int32 ``[Q, K]`` on the pool device, ``-1`` padding. Ids
@@ -133,7 +135,12 @@ class TokenPool:
         of the victims, and ``candidate_offset`` moves this call's candidate
         rows by that many rows (``write_candidates(..., offset=...)``). The
         pool contents then differ from the sequential FIFO order; every id
-        still maps to a row holding its record.
+        still maps to a row holding its record. ``gather_stream`` (a
+        ``torch.cuda.Stream``) takes the copy of the missing records, after
+        the slot assignment on the current stream: readers of the records
+        wait for it, and calls with a gather stream alternate between two
+        workspaces, so a call may run while the previous call's copy does
+        (the caller waits for the copy before the one after).
         """
         if indices.dtype != torch.int32 or indices.device != self.device:
             raise ValueError("indices must be int32 tensors on the pool device")
@@ -164,8 +171,20 @@ class TokenPool:
         protect, chosen = self.clock, self.clock + 1
         self.clock += 2
         self.last_stamp = protect
-        pipelined = keep_since is not None or candidate_offset != 0
-        extra = (keep_since if keep_since is not None else -1, candidate_offset) if pipelined else ()
+        pipelined = keep_since is not None or candidate_offset != 0 or gather_stream is not None
+        workspace = self.workspace
+        extra = ()
+        if pipelined:
+            gather = 0
+            if gather_stream is not None:
+                self.reserve_second_workspace()
+                self._parity ^= 1
+                workspace = self._second_workspace if self._parity else self.workspace
+                gather = gather_stream.cuda_stream
+            extra = (keep_since if keep_since is not None else -1, candidate_offset)
+            tail = (_native.stream_of(self.device), gather)
+        else:
+            tail = (_native.stream_of(self.device),)
         with torch.cuda.device(self.device):
             _native.call(
                 "dsa_pool_recall_pipelined" if pipelined else "dsa_pool_recall",
@@ -174,12 +193,17 @@ class TokenPool:
                 self.slots, _native.ptr(self.host), self.host_capacity,
                 _native.ptr(self.records), self.record_pages * PAGE_SIZE, RECORD_BYTES,
                 _native.ptr(self.h2d), _native.ptr(self.d2h), _native.ptr(self.priority),
-                protect, chosen, _native.ptr(self.workspace), self.workspace.numel(),
+                protect, chosen, _native.ptr(workspace), workspace.numel(),
                 self.history_capacity, union_checked, _native.ptr(self.stats),
-                _native.ptr(self.status), _native.ptr(physical), *extra,
-                _native.stream_of(self.device),
+                _native.ptr(self.status), _native.ptr(physical), *extra, *tail,
             )
         return physical
+
+    def reserve_second_workspace(self):
+        """Allocate the workspace that recalls with a gather stream alternate
+        with (done once, outside any pipelined round)."""
+        if self._second_workspace is None:
+            self._second_workspace = torch.empty_like(self.workspace)
 
     def attend(self, q, physical, scale, value_dim=512):
         """Sparse MLA over recalled pool records (``sparse_mla_from_pool``)."""

@@ -267,7 +267,11 @@ int dsa_pool_recall(const int32_t* indices, int64_t n, const int32_t* page_table
  * slots + 1 + candidate_offset + id - transient_start (alternate halves of the
  * candidate rows between users in flight). The victims then differ from the
  * sequential FIFO order; every selected id still maps to a row holding its
- * record. With keep_floor = -1 and candidate_offset = 0 it is dsa_pool_recall.
+ * record. gather_stream (null: `stream`) takes the gather of the missing
+ * records, ordered after the slot assignment on `stream`; the next recall on
+ * `stream` may then run while it copies, given another workspace, and readers
+ * of the records wait for gather_stream. With keep_floor = -1,
+ * candidate_offset = 0 and no gather stream it is dsa_pool_recall.
  */
 int dsa_pool_recall_pipelined(const int32_t* indices, int64_t n, const int32_t* page_table,
                               int64_t history_end, int64_t written, int64_t transient_start,
@@ -277,7 +281,8 @@ int dsa_pool_recall_pipelined(const int32_t* indices, int64_t n, const int32_t* 
                               int64_t chosen_stamp, void* workspace, int64_t workspace_bytes,
                               int64_t history_capacity, int union_checked, int64_t* stats,
                               int32_t* status, int32_t* physical, int64_t keep_floor,
-                              int64_t candidate_offset, hipStream_t stream);
+                              int64_t candidate_offset, hipStream_t stream,
+                              hipStream_t gather_stream);
 
 #ifdef __cplusplus
 }
