@@ -34,6 +34,12 @@ SIGNATURES = {
     "dsa_topk_workspace_bytes": [_i64, ctypes.POINTER(ctypes.c_int64)],
     "dsa_topk_radix_split": [_ptr, _i64, _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr, _i64, _ptr],
     "dsa_topk_radix_split_static": [_ptr, _i64, _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr],
+    "dsa_indexer_logits_fp8_counted": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64,
+                                       _i64, _ptr, _ptr, _ptr, _ptr],
+    "dsa_topk_radix_digits": [_ptr, _i64, _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr, _i64, _ptr],
+    "dsa_indexer_topk_workspace_bytes": [_i64, _i64, ctypes.POINTER(ctypes.c_int64)],
+    "dsa_indexer_topk_fp8": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _ptr,
+                             _ptr, _i64, _ptr, _ptr, _i64, _ptr, _i64, _ptr],
     "dsa_kv_pack_fp8": [_ptr, _i64, _i64, _ptr, _i64, _ptr, _ptr, _ptr],
     "dsa_layer_prologue_fp8": [_ptr, _i64, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _ptr, _ptr,
                                _ptr, _i64, _i64, _ptr, _i64, _ptr, _ptr, _ptr],

@@ -60,6 +60,22 @@ constexpr int kKLoads = kKBytes / (64 * 16);       // DMA instructions for the k
 constexpr int kSLoads = kStageKeys / 64;           // DMA instructions for the key scales
 constexpr int kStageBytes = kKBytes + kStageKeys * 4;  // + the stage's key scales
 constexpr int kDigits = 4;                         // e4m3 digits of the folded query
+// Radix-digit counts for the top-k (optional output): per query row, the
+// number of its scores in [0, columns) by the top 11 bits of their radix key
+// (the top-k's level-0 digit). A work-group counts its rows in LDS as two
+// 16-bit counters per word - digit d in half d >> 10 of word d & 1023, so
+// neighbouring digits (the crowded ones) sit in different words - and adds
+// the nonzero ones to the global counts at the end. A split covers at most
+// kMaxSplitKeys keys, so a counter cannot carry into its neighbour.
+constexpr int kDigitBins = 2048;
+constexpr int kDigitShift = 21;
+constexpr int64_t kMaxSplitKeys = 65535 / kStageKeys * kStageKeys;
+constexpr uint32_t kNegInfDigit = 0x007FFFFFu >> kDigitShift;  // radix key of -inf, top 11 bits
+
+__device__ __forceinline__ uint32_t score_digit(float v) {
+  const uint32_t b = __float_as_uint(v);
+  return ((b & 0x80000000u) ? ~b : (b | 0x80000000u)) >> kDigitShift;
+}
 
 
 // f(integral_constant<int, I>) for every I of the sequence, in order.
@@ -112,12 +128,19 @@ __device__ __forceinline__ float reduce_scatter4(const float part[4]) {
   return fold16(a0, a1);                      // row g: key group g
 }
 
+template <bool kCount>
 __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
     const uint8_t* __restrict__ q, const uint8_t* __restrict__ k, const float* __restrict__ w,
     const float* __restrict__ kscale, const int32_t* __restrict__ starts,
     const int32_t* __restrict__ ends, int64_t query_start, int64_t rows, int64_t columns,
-    int64_t ldo, int64_t keys_per_split, const float* __restrict__ q_fold, float* __restrict__ out) {
+    int64_t ldo, int64_t keys_per_split, const float* __restrict__ q_fold, float* __restrict__ out,
+    uint32_t* __restrict__ digit_counts) {
   __shared__ __align__(16) uint8_t ring[kRing][kStageBytes];
+  // Packed 16-bit digit counts of the block's rows: digit d of row i is half
+  // d >> 10 of word i * kDigitBins / 2 + (d & 1023).
+  constexpr int kBinWords = kQueriesPerBlock * kDigitBins / 2;
+  constexpr int kBinVecs = kBinWords / (4 * kThreads);  // 16-byte LDS accesses per thread
+  __shared__ __align__(16) uint32_t bins[kCount ? kBinWords : 4];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -129,6 +152,15 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
   if (kb >= ldo) return;  // a padding split (whole work-group, before any barrier)
   const int64_t ke = kb + keys_per_split < ldo ? kb + keys_per_split : ldo;
   const float neg_inf = -__builtin_inff();
+  // Keys of this split that the digit counts cover.
+  const int64_t count_end = ke < columns ? ke : columns;
+  if constexpr (kCount) {
+    // Ordered before the first count by the first stage's barrier (or the
+    // barrier before the flush when there are no stages).
+#pragma unroll
+    for (int i = 0; i < kBinVecs; ++i)
+      reinterpret_cast<v4u*>(bins)[i * kThreads + tid] = v4u{0u, 0u, 0u, 0u};
+  }
 
   // Largest causal end among this block's queries: keys at or beyond it
   // are -inf for every row and need no MFMA work.
@@ -355,6 +387,17 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
     for (int s = 0; s < kRing - 1; ++s) issue(s);
   }
 
+  // Digit counts of the previous half-stage's scores, issued under the next
+  // half-stage's MFMAs (lane bit j of pend_ok: query j's score counts).
+  float pend_v[kQueriesPerWave] = {};
+  uint32_t pend_ok = 0;
+  auto count_pending = [&](int j) {
+    if constexpr (kCount) {
+      const uint32_t d = score_digit(pend_v[j]);
+      const uint32_t inc = ((pend_ok >> j) & 1u) << ((d >> 10) << 4);
+      atomicAdd(&bins[(4 * wave + j) * (kDigitBins / 2) + (d & 1023)], inc);
+    }
+  };
   for (int s = 0; s < stages; ++s) {
     // Wave 0's loads of stage s have landed; stage s - 1 is free.
     if (wave == 0) wait_dma<(kKLoads + kSLoads) * (kRing - 2)>();
@@ -427,6 +470,7 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
         const bool refill = i % kQueriesPerWave == kQueriesPerWave - 1 && i / kQueriesPerWave + 2 < 4;
         if (refill) b[(i / kQueriesPerWave) & 1] = load_b(i / kQueriesPerWave + 2);
         epilogue(i - 1);
+        if (i <= kQueriesPerWave) count_pending(i - 1);
         // One MFMA, then the FMAs of one accumulator of the previous unit,
         // four times (five MFMAs with a key group's linear one): the results
         // read were issued a full unit earlier, and the VALU work runs under
@@ -453,6 +497,10 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
         const float total = reduce_scatter4(part[j]);
         const bool visible = key >= qs[j] && key < qe[j];
         const float v = visible ? total * ks : neg_inf;
+        if constexpr (kCount) {
+          pend_v[j] = v;
+          pend_ok = (pend_ok & ~(1u << j)) | ((qw + j < rows && key < count_end) ? 1u << j : 0u);
+        }
         if (wave == 0) {
           staged[s & 1][j][kHalfKeys * hf + lane] = v;
         } else if (qw + j < rows && key < ke) {
@@ -461,6 +509,8 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
       }
     }
   }
+#pragma unroll
+  for (int j = 0; j < kQueriesPerWave; ++j) count_pending(j);
   if (stages > 0) {
     lds_barrier();  // wave 0's last rows are staged
     if (wave == 1 + (stages - 1) % (kWaves - 1)) store_staged(stages - 1);
@@ -477,6 +527,30 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
       for (int64_t key = tail + lane; key < ke; key += 64) out[qi * ldo + key] = neg_inf;
     }
   }
+  if constexpr (kCount) {
+    __syncthreads();  // the zeroing above, also with no stages
+    if (tail < count_end && tid < kQueriesPerBlock && q0 + tid < rows)
+      atomicAdd(&bins[tid * (kDigitBins / 2) + (kNegInfDigit & 1023)],
+                (uint32_t)(count_end - tail) << ((kNegInfDigit >> 10) << 4));
+    __syncthreads();
+    // Every word read at once; each nonzero half adds its count to the
+    // global counts of its digit.
+    v4u words[kBinVecs];
+#pragma unroll
+    for (int i = 0; i < kBinVecs; ++i) words[i] = reinterpret_cast<const v4u*>(bins)[i * kThreads + tid];
+#pragma unroll
+    for (int i = 0; i < kBinVecs; ++i) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t c = words[i][e];
+        if (c == 0) continue;
+        const int w = 4 * (i * kThreads + tid) + e;
+        uint32_t* dst = digit_counts + (q0 + w / (kDigitBins / 2)) * kDigitBins + w % (kDigitBins / 2);
+        if (c & 0xFFFFu) atomicAdd(dst, c & 0xFFFFu);
+        if (c >> 16) atomicAdd(dst + kDigitBins / 2, c >> 16);
+      }
+    }
+  }
 }
 
 }  // namespace
@@ -488,7 +562,7 @@ namespace {
 int logits_launch(const void* q, const void* k, const float* weights, const float* kscale,
                   const int32_t* starts, const int32_t* ends, int64_t query_start, int64_t rows,
                   int64_t columns, int64_t ldo, const float* q_fold, float* out,
-                  hipStream_t stream) {
+                  uint32_t* digit_counts, hipStream_t stream) {
   DSA_CHECK_ARG(rows >= 0 && columns >= 1, "logits requires nonempty K");
   DSA_CHECK_ARG(ldo >= columns, "output row stride must cover every column");
   DSA_CHECK_ARG(query_start >= 0 && query_start + rows <= columns,
@@ -509,6 +583,7 @@ int logits_launch(const void* q, const void* k, const float* weights, const floa
   if (splits < 1) splits = 1;
   int64_t per = (ldo + splits - 1) / splits;
   per = (per + kStageKeys - 1) / kStageKeys * kStageKeys;
+  if (digit_counts && per > kMaxSplitKeys) per = kMaxSplitKeys;  // 16-bit LDS counters
   splits = (ldo + per - 1) / per;
   // Work-groups are dealt to the eight XCDs round-robin by linear id
   // (x + splits * y): with a multiple of 8 splits every query group of one
@@ -517,10 +592,11 @@ int logits_launch(const void* q, const void* k, const float* weights, const floa
   if (splits >= 8) splits = (splits + 7) / 8 * 8;
   DSA_CHECK_ARG(qgroups < 65536, "too many query rows for one launch");
   DSA_CHECK_ARG(ldo < 0x7FFFFFFF - 64, "the logits row stride must fit int32");
-  hipLaunchKernelGGL(logits_fp8_mfma, dim3((unsigned)splits, (unsigned)qgroups), dim3(kThreads),
-                     0, stream, static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(k),
-                     weights, kscale, starts, ends, query_start, rows, columns, ldo, per, q_fold,
-                     out);
+  hipLaunchKernelGGL(digit_counts ? logits_fp8_mfma<true> : logits_fp8_mfma<false>,
+                     dim3((unsigned)splits, (unsigned)qgroups), dim3(kThreads), 0, stream,
+                     static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(k), weights,
+                     kscale, starts, ends, query_start, rows, columns, ldo, per, q_fold, out,
+                     digit_counts);
   DSA_CHECK_LAUNCH("indexer logits");
   return kOk;
 }
@@ -534,7 +610,7 @@ extern "C" int dsa_indexer_logits_fp8(const void* q, const void* k, const float*
                                       int64_t columns, int64_t ldo, float* out,
                                       hipStream_t stream) {
   return dsa::logits_launch(q, k, weights, kscale, starts, ends, query_start, rows, columns, ldo,
-                            nullptr, out, stream);
+                            nullptr, out, nullptr, stream);
 }
 
 extern "C" int dsa_indexer_logits_fp8_folded(const void* q, const void* k, const float* weights,
@@ -545,5 +621,49 @@ extern "C" int dsa_indexer_logits_fp8_folded(const void* q, const void* k, const
                                              hipStream_t stream) {
   DSA_CHECK_ARG(rows == 0 || q_fold != nullptr, "null pointer");
   return dsa::logits_launch(q, k, weights, kscale, starts, ends, query_start, rows, columns, ldo,
-                            q_fold, out, stream);
+                            q_fold, out, nullptr, stream);
+}
+
+extern "C" int dsa_indexer_logits_fp8_counted(const void* q, const void* k, const float* weights,
+                                              const float* kscale, const int32_t* starts,
+                                              const int32_t* ends, int64_t query_start,
+                                              int64_t rows, int64_t columns, int64_t ldo,
+                                              const float* q_fold, float* out,
+                                              uint32_t* digit_counts, hipStream_t stream) {
+  DSA_CHECK_ARG(rows == 0 || (digit_counts != nullptr &&
+                              reinterpret_cast<uintptr_t>(digit_counts) % 4 == 0),
+                "digit counts must be a 4-byte aligned device pointer");
+  return dsa::logits_launch(q, k, weights, kscale, starts, ends, query_start, rows, columns, ldo,
+                            q_fold, out, digit_counts, stream);
+}
+
+
+// Logits with their radix-digit counts, then the exact top-k that starts from
+// those counts instead of a histogram pass over the scores (the counts are
+// zeroed again by the top-k). The scores are still written in full.
+extern "C" int dsa_indexer_topk_fp8(const void* q, const void* k, const float* weights,
+                                    const float* kscale, const int32_t* starts,
+                                    const int32_t* ends, int64_t query_start, int64_t rows,
+                                    int64_t columns, int64_t ldo, const float* q_fold,
+                                    float* scores, int64_t topk, float* values,
+                                    int32_t* indices, int64_t out_ld, void* workspace,
+                                    int64_t workspace_bytes, hipStream_t stream) {
+  using namespace dsa;
+  DSA_CHECK_ARG(topk >= 1 && topk <= 2048, "k must be an integer in [1, 2048]");
+  DSA_CHECK_ARG(rows >= 0 && columns >= 1, "logits requires nonempty K");
+  DSA_CHECK_ARG(out_ld >= (topk < columns ? topk : columns), "output row stride too small");
+  if (rows == 0) return kOk;
+  DSA_CHECK_ARG(values && indices, "null pointer");
+  int64_t needed = 0;
+  const int status_bytes = dsa_indexer_topk_workspace_bytes(rows, columns, &needed);
+  if (status_bytes != kOk) return status_bytes;
+  DSA_CHECK_ARG(workspace != nullptr && reinterpret_cast<uintptr_t>(workspace) % 8 == 0 &&
+                    workspace_bytes >= needed,
+                "indexer top-k workspace too small or misaligned");
+  // The workspace starts with the [rows][2048] digit counts.
+  const int status = logits_launch(q, k, weights, kscale, starts, ends, query_start, rows, columns,
+                                   ldo, q_fold, scores, static_cast<uint32_t*>(workspace), stream);
+  if (status != kOk) return status;
+  return dsa_topk_radix_digits(scores, rows, columns, ldo, topk, values, indices, out_ld, workspace,
+                               workspace_bytes, stream);
 }

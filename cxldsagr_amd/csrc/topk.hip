@@ -76,6 +76,7 @@ struct Shared {
   uint32_t digit;
   uint32_t above;
   uint32_t bucket;
+  uint32_t total;
 };
 
 // Find the bucket d holding the `remaining`-th largest element: the suffix
@@ -108,6 +109,7 @@ __device__ void find_bucket(Shared& sh, uint32_t remaining) {
     total += s;
   }
   incl += before;
+  if (tid == 0) sh.total = total;
   // Suffix counts: elements in bins strictly above this thread's pair.
   const uint32_t above_pair = total - incl;
   const uint32_t s1 = above_pair + h1;  // count at or above bin 2t+1
@@ -263,6 +265,105 @@ __device__ bool counting_sort(Shared& sh, int count) {
   return true;
 }
 
+// Sorts the `count` unique keys sh.sel[0 .. count) in place, descending:
+// counting sort, or when a bucket is crowded, a bitonic network (padding
+// keys are 0). Thread t holds positions 2t and 2t + 1 in registers;
+// partners at stride 1 are in the same thread, strides 2..64 in the same
+// wave, strides >= 128 in LDS. Ends with a barrier.
+__device__ __forceinline__ void sort_selected(Shared& sh, int count) {
+  const int tid = threadIdx.x;
+  if (!counting_sort(sh, count)) {
+    int padded = 2;
+    while (padded < count) padded <<= 1;
+    for (int i = count + tid; i < padded; i += kThreads) sh.sel[i] = 0;
+    __syncthreads();
+    const bool active = 2 * tid < padded;
+    uint64_t x0 = active ? sh.sel[2 * tid] : 0;
+    uint64_t x1 = active ? sh.sel[2 * tid + 1] : 0;
+    const int p0 = 2 * tid;
+    const int lane = tid & 63;
+    // Compare-exchange of a pair (lo at the lower position): the larger key
+    // goes first inside descending blocks.
+    auto order = [](uint64_t& lo, uint64_t& hi, bool descending) {
+      const bool swap = (lo < hi) == descending;
+      const uint64_t a = lo, b = hi;
+      lo = swap ? b : a;
+      hi = swap ? a : b;
+    };
+    // Strides 2..16: partner lane ^ kM (kM = stride / 2), fetched by DPP; the
+    // lane keeps the larger key iff it holds the lower position of a
+    // descending block (or the upper of an ascending one).
+    auto exchange_dpp = [&](auto m_tag, int size) {
+      constexpr int kM = decltype(m_tag)::value;
+      const bool desc = (p0 & size) == 0;
+      const bool keep_max = ((lane & kM) == 0) == desc;
+      const uint64_t y0 = lane_xor64<kM>(x0);
+      const uint64_t y1 = lane_xor64<kM>(x1);
+      x0 = ((x0 < y0) == keep_max) ? y0 : x0;
+      x1 = ((x1 < y1) == keep_max) ? y1 : x1;
+    };
+    // Strides 32 and 64 (lane ^ 16, lane ^ 32): one row-swap permute of (x0,
+    // x1) leaves every lane holding a whole pair - lanes with the distance bit
+    // clear get x0 of lanes l and l + kM, the others x1 of lanes l - kM and l -
+    // so the exchange happens in-lane and a second permute restores the layout.
+    auto exchange_swap = [&](auto m_tag, int size) {
+      constexpr int kM = decltype(m_tag)::value;
+      auto swap32 = [](uint32_t& a, uint32_t& b) {
+        const auto r = kM == 16 ? __builtin_amdgcn_permlane16_swap(a, b, false, false)
+                                : __builtin_amdgcn_permlane32_swap(a, b, false, false);
+        a = r[0];
+        b = r[1];
+      };
+      uint32_t a_lo = (uint32_t)x0, a_hi = (uint32_t)(x0 >> 32);
+      uint32_t b_lo = (uint32_t)x1, b_hi = (uint32_t)(x1 >> 32);
+      swap32(a_lo, b_lo);
+      swap32(a_hi, b_hi);
+      // The pair's lower position: 2l (x0 of lane l) or 2 (l - kM) + 1.
+      const int first = (lane & kM) ? 2 * ((tid & ~63) + lane - kM) + 1 : p0;
+      uint64_t lo = ((uint64_t)a_hi << 32) | a_lo;
+      uint64_t hi = ((uint64_t)b_hi << 32) | b_lo;
+      order(lo, hi, (first & size) == 0);
+      a_lo = (uint32_t)lo;
+      a_hi = (uint32_t)(lo >> 32);
+      b_lo = (uint32_t)hi;
+      b_hi = (uint32_t)(hi >> 32);
+      swap32(a_lo, b_lo);
+      swap32(a_hi, b_hi);
+      x0 = ((uint64_t)a_hi << 32) | a_lo;
+      x1 = ((uint64_t)b_hi << 32) | b_lo;
+    };
+    for (int size = 2; size <= padded; size <<= 1) {
+      // Strides 128 .. size / 2 through LDS.
+      for (int stride = size >> 1; stride >= 128; stride >>= 1) {
+        const bool desc = (p0 & size) == 0;
+        if (active) {
+          sh.sel[p0] = x0;
+          sh.sel[p0 + 1] = x1;
+        }
+        __syncthreads();
+        const uint64_t y0 = active ? sh.sel[p0 ^ stride] : 0;
+        const uint64_t y1 = active ? sh.sel[(p0 + 1) ^ stride] : 0;
+        const bool keep_max = ((p0 & stride) == 0) == desc;
+        x0 = ((x0 < y0) == keep_max) ? y0 : x0;
+        x1 = ((x1 < y1) == keep_max) ? y1 : x1;
+        __syncthreads();
+      }
+      if (size >= 128) exchange_swap(std::integral_constant<int, 32>{}, size);
+      if (size >= 64) exchange_swap(std::integral_constant<int, 16>{}, size);
+      if (size >= 32) exchange_dpp(std::integral_constant<int, 8>{}, size);
+      if (size >= 16) exchange_dpp(std::integral_constant<int, 4>{}, size);
+      if (size >= 8) exchange_dpp(std::integral_constant<int, 2>{}, size);
+      if (size >= 4) exchange_dpp(std::integral_constant<int, 1>{}, size);
+      order(x0, x1, (p0 & size) == 0);
+    }
+    if (active) {
+      sh.sel[p0] = x0;
+      sh.sel[p0 + 1] = x1;
+    }
+    __syncthreads();
+  }
+}
+
 // Calls f(value, column) for every element of the row, each thread with four
 // 16-byte loads in flight.
 template <typename F>
@@ -296,6 +397,73 @@ __device__ __forceinline__ void for_each_element(const float* row, int64_t cols,
   } else {
     for (int64_t j = threadIdx.x; j < cols; j += kThreads) f(row[j], j);
   }
+}
+
+// The keys of the level-0 bucket (the `prefix >> shift` digit) still to be
+// split, `remaining` of them wanted: with the bucket's keys in sh.buf[0 ..
+// nbuf), further digits (11/10/11/11/10 bits) narrow it to exactly
+// `remaining` keys, which are appended to sh.sel after its sh.n_sel keys.
+__device__ __forceinline__ void refine_buffer(Shared& sh, uint64_t prefix, int shift, uint32_t remaining,
+                              bool resolved, uint32_t nbuf) {
+  const int tid = threadIdx.x;
+  for (int level = 1; level < kLevels && !resolved; ++level) {
+    clear_hist(sh);
+    __syncthreads();
+    const int s = kShift[level];
+    const uint64_t mask = (1ull << kWidth[level]) - 1;
+    for (uint32_t i = tid; i < nbuf; i += kThreads) {
+      const uint64_t key = sh.buf[i];
+      if ((key >> shift) == (prefix >> shift)) atomicAdd(&my_hist(sh)[(key >> s) & mask], 1u);
+    }
+    __syncthreads();
+    find_bucket(sh, remaining);
+    prefix |= (uint64_t)sh.digit << s;
+    shift = s;
+    remaining -= sh.above;
+    resolved = sh.bucket == remaining;
+    __syncthreads();
+  }
+  for (uint32_t i = tid; i < nbuf; i += kThreads) {
+    const uint64_t key = sh.buf[i];
+    const bool take = (key >> shift) >= (prefix >> shift);
+    const uint32_t slot = wave_slot(&sh.n_sel, take);
+    if (take && slot < kMaxK) sh.sel[slot] = key;
+  }
+}
+
+// The same when the bucket is too large for LDS: each further digit is
+// histogrammed over the row itself, and a last pass over the row appends
+// every key at or above the final prefix (all `count` of them, so sh.sel
+// starts empty).
+__device__ __forceinline__ void refine_from_row(Shared& sh, const float* row, int64_t cols, bool vec, uint64_t prefix,
+                                int shift, uint32_t remaining, bool resolved) {
+  for (int level = 1; level < kLevels && !resolved; ++level) {
+    clear_hist(sh);
+    __syncthreads();
+    const int s = kShift[level];
+    const uint64_t mask = (1ull << kWidth[level]) - 1;
+    const uint64_t want = prefix >> shift;
+    const int cur = shift;
+    for_each_element(row, cols, vec, [&](float v, int64_t i) {
+      const uint64_t key = composite(v, i);
+      if ((key >> cur) == want) atomicAdd(&my_hist(sh)[(key >> s) & mask], 1u);
+    });
+    __syncthreads();
+    find_bucket(sh, remaining);
+    prefix |= (uint64_t)sh.digit << s;
+    shift = s;
+    remaining -= sh.above;
+    resolved = sh.bucket == remaining;
+    __syncthreads();
+  }
+  const uint64_t floor = prefix >> shift;
+  const int cur = shift;
+  for_each_element(row, cols, vec, [&](float v, int64_t i) {
+    const uint64_t key = composite(v, i);
+    const bool take = (key >> cur) >= floor;
+    const uint32_t slot = wave_slot(&sh.n_sel, take);
+    if (take && slot < kMaxK) sh.sel[slot] = key;
+  });
 }
 
 // Row elements in batches: each thread gets kBatch elements per call of f
@@ -387,22 +555,17 @@ struct Resident {
   }
 };
 
-// Work-group (r, h) of a grid (rows, parts) selects and sorts the top
-// min(count, columns of its part) keys of row r's part h. With one part that
-// is the answer. With two (columns split at a multiple of 4 near the middle),
-// each part stores its sorted keys in the workspace and topk_merge, launched
-// next on the same stream, merges them.
+// The work-group selects and sorts the top min(count, columns of its part)
+// keys of row r's part `part` of `parts`. With one part that is the answer.
+// With two (columns split at a multiple of 4 near the middle), each part
+// stores its sorted keys in the workspace and topk_merge, launched next on
+// the same stream, merges them.
 template <int kResidentVec>
-__global__ __launch_bounds__(kThreads, 1) void topk_rows(const float* __restrict__ scores,
-                                                        int64_t all_cols, int64_t ld, int total_count,
-                                                        float* __restrict__ values,
-                                                        int32_t* __restrict__ ids,
-                                                        int64_t out_ld, uint64_t* ws_keys) {
-  __shared__ Shared sh;
+__device__ __forceinline__ void select_row(Shared& sh, const float* __restrict__ scores, int64_t all_cols,
+                           int64_t ld, int total_count, float* __restrict__ values,
+                           int32_t* __restrict__ ids, int64_t out_ld, uint64_t* ws_keys,
+                           int64_t r, int part, int parts) {
   const int tid = threadIdx.x;
-  const int64_t r = blockIdx.x;
-  const int part = blockIdx.y;
-  const int parts = gridDim.y;
   const int64_t part_cols = parts == 1 ? all_cols : ((((all_cols + 1) >> 1) + 3) & ~(int64_t)3);
   const int64_t col0 = part * part_cols;
   const int64_t cols = part_cols < all_cols - col0 ? part_cols : all_cols - col0;
@@ -600,155 +763,14 @@ __global__ __launch_bounds__(kThreads, 1) void topk_rows(const float* __restrict
       }
       __syncthreads();
       const uint32_t nbuf = sh.n_buf < kRefineCap ? sh.n_buf : kRefineCap;
-      for (int level = 1; level < kLevels && !resolved; ++level) {
-        clear_hist(sh);
-        __syncthreads();
-        const int s = kShift[level];
-        const uint64_t mask = (1ull << kWidth[level]) - 1;
-        for (uint32_t i = tid; i < nbuf; i += kThreads) {
-          const uint64_t key = sh.buf[i];
-          if ((key >> shift) == (prefix >> shift)) atomicAdd(&my_hist(sh)[(key >> s) & mask], 1u);
-        }
-        __syncthreads();
-        find_bucket(sh, remaining);
-        prefix |= (uint64_t)sh.digit << s;
-        shift = s;
-        remaining -= sh.above;
-        resolved = sh.bucket == remaining;
-        __syncthreads();
-      }
-      for (uint32_t i = tid; i < nbuf; i += kThreads) {
-        const uint64_t key = sh.buf[i];
-        const bool take = (key >> shift) >= (prefix >> shift);
-        const uint32_t slot = wave_slot(&sh.n_sel, take);
-        if (take && slot < kMaxK) sh.sel[slot] = key;
-      }
+      refine_buffer(sh, prefix, shift, remaining, resolved, nbuf);
     } else {
-      for (int level = 1; level < kLevels && !resolved; ++level) {
-        clear_hist(sh);
-        __syncthreads();
-        const int s = kShift[level];
-        const uint64_t mask = (1ull << kWidth[level]) - 1;
-        const uint64_t want = prefix >> shift;
-        const int cur = shift;
-        for_each_element(row, cols, vec, [&](float v, int64_t i) {
-          const uint64_t key = composite(v, i);
-          if ((key >> cur) == want) atomicAdd(&my_hist(sh)[(key >> s) & mask], 1u);
-        });
-        __syncthreads();
-        find_bucket(sh, remaining);
-        prefix |= (uint64_t)sh.digit << s;
-        shift = s;
-        remaining -= sh.above;
-        resolved = sh.bucket == remaining;
-        __syncthreads();
-      }
-      const uint64_t floor = prefix >> shift;
-      const int cur = shift;
-      for_each_element(row, cols, vec, [&](float v, int64_t i) {
-        const uint64_t key = composite(v, i);
-        const bool take = (key >> cur) >= floor;
-        const uint32_t slot = wave_slot(&sh.n_sel, take);
-        if (take && slot < kMaxK) sh.sel[slot] = key;
-      });
+      refine_from_row(sh, row, cols, vec, prefix, shift, remaining, resolved);
     }
   }
   __syncthreads();
 
-  // ---- sort `count` keys, descending: counting sort, or when a bucket is
-  // crowded, a bitonic network (padding keys are 0). Thread t holds
-  // positions 2t and 2t + 1 in registers; partners at stride 1 are in the
-  // same thread, strides 2..64 in the same wave, strides >= 128 in LDS.
-  if (!counting_sort(sh, count)) {
-  int padded = 2;
-  while (padded < count) padded <<= 1;
-  for (int i = count + tid; i < padded; i += kThreads) sh.sel[i] = 0;
-  __syncthreads();
-  const bool active = 2 * tid < padded;
-  uint64_t x0 = active ? sh.sel[2 * tid] : 0;
-  uint64_t x1 = active ? sh.sel[2 * tid + 1] : 0;
-  const int p0 = 2 * tid;
-  const int lane = tid & 63;
-  // Compare-exchange of a pair (lo at the lower position): the larger key
-  // goes first inside descending blocks.
-  auto order = [](uint64_t& lo, uint64_t& hi, bool descending) {
-    const bool swap = (lo < hi) == descending;
-    const uint64_t a = lo, b = hi;
-    lo = swap ? b : a;
-    hi = swap ? a : b;
-  };
-  // Strides 2..16: partner lane ^ kM (kM = stride / 2), fetched by DPP; the
-  // lane keeps the larger key iff it holds the lower position of a
-  // descending block (or the upper of an ascending one).
-  auto exchange_dpp = [&](auto m_tag, int size) {
-    constexpr int kM = decltype(m_tag)::value;
-    const bool desc = (p0 & size) == 0;
-    const bool keep_max = ((lane & kM) == 0) == desc;
-    const uint64_t y0 = lane_xor64<kM>(x0);
-    const uint64_t y1 = lane_xor64<kM>(x1);
-    x0 = ((x0 < y0) == keep_max) ? y0 : x0;
-    x1 = ((x1 < y1) == keep_max) ? y1 : x1;
-  };
-  // Strides 32 and 64 (lane ^ 16, lane ^ 32): one row-swap permute of (x0,
-  // x1) leaves every lane holding a whole pair - lanes with the distance bit
-  // clear get x0 of lanes l and l + kM, the others x1 of lanes l - kM and l -
-  // so the exchange happens in-lane and a second permute restores the layout.
-  auto exchange_swap = [&](auto m_tag, int size) {
-    constexpr int kM = decltype(m_tag)::value;
-    auto swap32 = [](uint32_t& a, uint32_t& b) {
-      const auto r = kM == 16 ? __builtin_amdgcn_permlane16_swap(a, b, false, false)
-                              : __builtin_amdgcn_permlane32_swap(a, b, false, false);
-      a = r[0];
-      b = r[1];
-    };
-    uint32_t a_lo = (uint32_t)x0, a_hi = (uint32_t)(x0 >> 32);
-    uint32_t b_lo = (uint32_t)x1, b_hi = (uint32_t)(x1 >> 32);
-    swap32(a_lo, b_lo);
-    swap32(a_hi, b_hi);
-    // The pair's lower position: 2l (x0 of lane l) or 2 (l - kM) + 1.
-    const int first = (lane & kM) ? 2 * ((tid & ~63) + lane - kM) + 1 : p0;
-    uint64_t lo = ((uint64_t)a_hi << 32) | a_lo;
-    uint64_t hi = ((uint64_t)b_hi << 32) | b_lo;
-    order(lo, hi, (first & size) == 0);
-    a_lo = (uint32_t)lo;
-    a_hi = (uint32_t)(lo >> 32);
-    b_lo = (uint32_t)hi;
-    b_hi = (uint32_t)(hi >> 32);
-    swap32(a_lo, b_lo);
-    swap32(a_hi, b_hi);
-    x0 = ((uint64_t)a_hi << 32) | a_lo;
-    x1 = ((uint64_t)b_hi << 32) | b_lo;
-  };
-  for (int size = 2; size <= padded; size <<= 1) {
-    // Strides 128 .. size / 2 through LDS.
-    for (int stride = size >> 1; stride >= 128; stride >>= 1) {
-      const bool desc = (p0 & size) == 0;
-      if (active) {
-        sh.sel[p0] = x0;
-        sh.sel[p0 + 1] = x1;
-      }
-      __syncthreads();
-      const uint64_t y0 = active ? sh.sel[p0 ^ stride] : 0;
-      const uint64_t y1 = active ? sh.sel[(p0 + 1) ^ stride] : 0;
-      const bool keep_max = ((p0 & stride) == 0) == desc;
-      x0 = ((x0 < y0) == keep_max) ? y0 : x0;
-      x1 = ((x1 < y1) == keep_max) ? y1 : x1;
-      __syncthreads();
-    }
-    if (size >= 128) exchange_swap(std::integral_constant<int, 32>{}, size);
-    if (size >= 64) exchange_swap(std::integral_constant<int, 16>{}, size);
-    if (size >= 32) exchange_dpp(std::integral_constant<int, 8>{}, size);
-    if (size >= 16) exchange_dpp(std::integral_constant<int, 4>{}, size);
-    if (size >= 8) exchange_dpp(std::integral_constant<int, 2>{}, size);
-    if (size >= 4) exchange_dpp(std::integral_constant<int, 1>{}, size);
-    order(x0, x1, (p0 & size) == 0);
-  }
-  if (active) {
-    sh.sel[p0] = x0;
-    sh.sel[p0 + 1] = x1;
-  }
-  __syncthreads();
-  }
+  sort_selected(sh, count);
 
   float* vout = values + r * out_ld;
   int32_t* iout = ids + r * out_ld;
@@ -771,6 +793,18 @@ __global__ __launch_bounds__(kThreads, 1) void topk_rows(const float* __restrict
     const uint32_t col = ~(uint32_t)key + (uint32_t)col0;
     mine[i] = (key & 0xFFFFFFFF00000000ull) | (uint64_t)(~col);
   }
+}
+
+// Work-group (r, h) of a grid (rows, parts): select_row for row r, part h.
+template <int kResidentVec>
+__global__ __launch_bounds__(kThreads, 1) void topk_rows(const float* __restrict__ scores,
+                                                        int64_t all_cols, int64_t ld, int total_count,
+                                                        float* __restrict__ values,
+                                                        int32_t* __restrict__ ids,
+                                                        int64_t out_ld, uint64_t* ws_keys) {
+  __shared__ Shared sh;
+  select_row<kResidentVec>(sh, scores, all_cols, ld, total_count, values, ids, out_ld, ws_keys,
+                           blockIdx.x, blockIdx.y, gridDim.y);
 }
 
 // Merge path over the two descending key lists of a row (keys are unique):
@@ -818,6 +852,434 @@ __global__ __launch_bounds__(kThreads, 1) void topk_merge(const uint64_t* __rest
   }
 }
 
+
+// ---- exact top-k from precomputed level-0 digit counts.
+//
+// Workspace of R rows (columns read in P parts by the selection launch):
+//   counts    u32 [R][kBins]  digit counts (added by the caller, zeroed here)
+//   threshold u32 [R][8]      {valid, digit, above, bucket, top digit}
+//   fill      u32 [R]         candidates listed so far (zero on entry and exit)
+//   lists     u64 [R][kListCap]  the row's keys at or above the threshold
+//                                digit (composite keys), in no order
+// Counts and fill are zero on entry and exit; the rest is written before it
+// is read.
+// Selection work-groups: wave 0 reads the row's counts while waves 1-15 read
+// kSelectVec float4 per thread of the row part (34,560 columns).
+constexpr int kSelectVec = 9;
+constexpr int kSelectDataThreads = kThreads - 64;
+constexpr int kListCap = kMaxK + kRefineCap;  // candidates a row may list
+constexpr int kWaveCap = 1024;                // candidates a wave stages in LDS
+constexpr uint32_t kOverflow = 0x40000000u;   // added to a row's fill by an overflowing part
+constexpr int kSortCap = kListCap;  // candidates the one-pass counting sort takes
+constexpr int kSortBins = 4096;     // its linear buckets
+constexpr uint32_t kSortBucketMax = 128;  // keys per bucket it ranks by comparison
+constexpr int kSortPerThread = kSortCap / kThreads;
+constexpr int kSortEager = 4;  // key slots per thread loaded before the row's count is known
+
+struct DigitWorkspace {
+  uint32_t* counts;
+  uint32_t* threshold;
+  uint32_t* fill;
+  uint64_t* lists;
+  int parts;
+};
+
+int64_t select_parts(int64_t columns) {
+  const int64_t span = 4 * (int64_t)kSelectVec * kSelectDataThreads;
+  return (columns + span - 1) / span;
+}
+
+int64_t digit_workspace_bytes(int64_t rows, int64_t columns) {
+  (void)columns;
+  const int64_t fill = (rows * 4 + 7) & ~(int64_t)7;
+  return rows * ((int64_t)kBins * 4 + 32) + fill + rows * (int64_t)kListCap * 8;
+}
+
+DigitWorkspace digit_workspace(void* base, int64_t rows, int64_t columns) {
+  DigitWorkspace ws;
+  ws.parts = (int)select_parts(columns);
+  ws.counts = static_cast<uint32_t*>(base);
+  ws.threshold = ws.counts + rows * kBins;
+  ws.fill = ws.threshold + rows * 8;
+  ws.lists = reinterpret_cast<uint64_t*>(ws.fill + ((rows + 1) & ~(int64_t)1));
+  return ws;
+}
+
+struct Threshold {
+  uint32_t digit;   // level-0 digit whose bucket holds the count-th largest key
+  uint32_t above;   // keys in higher digits (< count)
+  uint32_t bucket;  // keys in that digit (above + bucket >= count)
+  uint32_t top;     // highest digit with a key
+  uint32_t total;   // sum of the counts
+};
+
+// The level-0 threshold of a row from its kBins digit counts, computed by
+// one wave without barriers: lane l holds digits 32l .. 32l + 31.
+__device__ __forceinline__ Threshold row_threshold(const uint32_t* __restrict__ row_counts,
+                                                   uint32_t count) {
+  const int lane = threadIdx.x & 63;
+  uint32_t c[32];
+  const uint4* src = reinterpret_cast<const uint4*>(row_counts + 32 * lane);
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const uint4 x = src[q];
+    c[4 * q] = x.x;
+    c[4 * q + 1] = x.y;
+    c[4 * q + 2] = x.z;
+    c[4 * q + 3] = x.w;
+  }
+  uint32_t sum = 0;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) sum += c[j];
+  // Keys in lanes >= this one (higher lanes hold higher digits).
+  uint32_t incl = sum;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t o = __shfl_down(incl, d);
+    if (lane + d < 64) incl += o;
+  }
+  Threshold t{0u, 0u, 0u, 0u, (uint32_t)__shfl(incl, 0)};
+  const uint32_t above_lane = incl - sum;
+  const bool mine = above_lane < count && incl >= count;
+  uint32_t digit = 0, above = 0, bucket = 0, top = 0, acc = above_lane;
+#pragma unroll
+  for (int j = 31; j >= 0; --j) {
+    if (mine && acc < count && acc + c[j] >= count) {
+      digit = 32 * lane + j;
+      above = acc;
+      bucket = c[j];
+    }
+    if (top == 0 && c[j]) top = 32 * lane + j + 1;  // + 1: 0 means none yet
+    acc += c[j];
+  }
+  const uint64_t m = __builtin_amdgcn_ballot_w64(mine);
+  if (m) {
+    const int leader = __builtin_ffsll((long long)m) - 1;
+    t.digit = __builtin_amdgcn_readlane(digit, leader);
+    t.above = __builtin_amdgcn_readlane(above, leader);
+    t.bucket = __builtin_amdgcn_readlane(bucket, leader);
+  }
+  const uint64_t nonempty = __builtin_amdgcn_ballot_w64(sum != 0);
+  if (nonempty) {
+    const int highest = 63 - __builtin_clzll(nonempty);
+    t.top = __builtin_amdgcn_readlane(top, highest) - 1;
+  }
+  return t;
+}
+
+// Exclusive prefix over the wave of per-lane counts below 64, and the total.
+__device__ __forceinline__ uint32_t wave_prefix(uint32_t n, uint32_t* total) {
+  uint32_t pre = 0, tot = 0;
+#pragma unroll
+  for (int bit = 0; bit < 6; ++bit) {
+    const uint64_t m = __builtin_amdgcn_ballot_w64((n >> bit) & 1u);
+    pre += __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0)) << bit;
+    tot += (uint32_t)__builtin_popcountll(m) << bit;
+  }
+  *total = tot;
+  return pre;
+}
+
+struct SelectShared {
+  uint64_t staged[kThreads / 64][kWaveCap];
+  uint32_t wave_count[kThreads / 64];
+  uint32_t digit, total, listed;
+};
+
+// Work-group (r, p) of a grid (rows, parts): reads part p of row r once and
+// lists its candidates - keys at or above the row's threshold digit - when
+// the row's candidates fit kListCap: each wave stages its own in LDS in
+// column order (positions from ballots, no atomics); one atomic on the row's
+// fill then places the part's candidates in the row's list, where the waves
+// copy them in whole lines. Part 0 also stores the row's threshold record.
+__global__ __launch_bounds__(kThreads, 1) void topk_digit_select(const float* __restrict__ scores,
+                                                                int64_t cols, int64_t ld, int count,
+                                                                int64_t part_cols,
+                                                                DigitWorkspace ws) {
+  __shared__ SelectShared ss;
+  __shared__ uint32_t list_base;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t r = blockIdx.x;
+  const int part = blockIdx.y;
+  const int64_t col0 = (int64_t)part * part_cols;
+  const uint32_t n = (uint32_t)(part_cols < cols - col0 ? part_cols : cols - col0);
+  const float* row = scores + r * ld + col0;
+  const bool vec = (reinterpret_cast<uintptr_t>(row) & 15) == 0;
+  // Slot e of data thread dt = tid - 64 (waves 1-15): column
+  // 4 ((e / 4) kSelectDataThreads + dt) + e % 4 of the part.
+  const int dt = tid - 64;
+  auto column = [dt](int e) {
+    return 4u * ((uint32_t)(e >> 2) * kSelectDataThreads + (uint32_t)dt) + (uint32_t)(e & 3);
+  };
+  uint32_t bits[4 * kSelectVec];
+  if (wave == 0) {
+    const Threshold t = row_threshold(ws.counts + r * kBins, (uint32_t)count);
+    if (lane == 0) {
+      ss.digit = t.digit;
+      ss.total = t.total;
+      ss.listed = t.above + t.bucket <= (uint32_t)kListCap;
+      if (part == 0) {
+        uint32_t* rec = ws.threshold + r * 8;
+        rec[0] = t.total == (uint32_t)cols;
+        rec[1] = t.digit;
+        rec[2] = t.above;
+        rec[3] = t.bucket;
+        rec[4] = t.top;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4 * kSelectVec; ++e) bits[e] = 0;
+  } else {
+#pragma unroll
+    for (int d = 0; d < kSelectVec; ++d) {
+      const uint32_t c = column(4 * d);
+      if (vec && c + 3 < n) {
+        const float4 x = reinterpret_cast<const float4*>(row)[c >> 2];
+        bits[4 * d] = __float_as_uint(x.x);
+        bits[4 * d + 1] = __float_as_uint(x.y);
+        bits[4 * d + 2] = __float_as_uint(x.z);
+        bits[4 * d + 3] = __float_as_uint(x.w);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bits[4 * d + e] = c + e < n ? __float_as_uint(row[c + e]) : 0u;
+      }
+    }
+  }
+  __syncthreads();
+  // Rows whose counts do not sum to the row, or whose candidates do not fit
+  // the list, are selected by topk_digit_finish from their scores.
+  if (ss.total != (uint32_t)cols || !ss.listed) return;
+  const uint32_t d0 = ss.digit;
+  const uint32_t floor_key = d0 << 21;
+  // A non-negative threshold (d0 >= 1024) compares the raw bits as signed
+  // integers: negative values are below it, non-negative ones order by bits.
+  const bool nonnegative = d0 >= 1024;
+  const int32_t floor_bits = (int32_t)((d0 - 1024) << 21);
+  const uint32_t not_col0 = ~(uint32_t)col0;
+  uint64_t* staged = ss.staged[wave];
+  uint32_t off = 0;  // wave-uniform
+#pragma unroll
+  for (int e = 0; e < 4 * kSelectVec; ++e) {
+    const uint32_t c = column(e);
+    uint32_t key;
+    bool hit;
+    if (nonnegative) {
+      key = bits[e] | 0x80000000u;
+      hit = (int32_t)bits[e] >= floor_bits;
+    } else {
+      key = radix_key(__uint_as_float(bits[e]));
+      hit = key >= floor_key;
+    }
+    hit = hit && wave != 0 && c < n;
+    const uint64_t m = __builtin_amdgcn_ballot_w64(hit);
+    const uint32_t pos = off + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+    if (hit && pos < (uint32_t)kWaveCap) staged[pos] = ((uint64_t)key << 32) | (uint64_t)(not_col0 - c);
+    off += (uint32_t)__builtin_popcountll(m);
+  }
+  if (lane == 0) ss.wave_count[wave] = off;
+  __syncthreads();
+  uint32_t before = 0, total = 0;
+  bool overflow = false;
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; ++w) {
+    const uint32_t cw = ss.wave_count[w];
+    before += w < wave ? cw : 0u;
+    total += cw;
+    overflow |= cw > (uint32_t)kWaveCap;
+  }
+  if (tid == 0) list_base = atomicAdd(&ws.fill[r], overflow ? kOverflow : total);
+  __syncthreads();
+  const uint32_t base = list_base;
+  if (overflow || base + total > (uint32_t)kListCap) return;  // the fill tells the finish
+  uint64_t* list = ws.lists + r * kListCap + base + before;
+  for (uint32_t i = lane; i < off; i += 64) list[i] = staged[i];
+}
+
+// LDS of topk_digit_finish: its one-pass counting sort, or (fallback) the
+// refine-and-sort state of select_row.
+struct FinishSort {
+  uint64_t sorted[kSortCap];
+  uint64_t out[kMaxK];
+  uint32_t start[kSortBins];   // keys in higher buckets
+  uint32_t cursor[kSortBins];  // bucket counts, then scatter cursors
+  uint32_t wave_sums[kThreads / 64];
+  uint32_t crowded;
+};
+union FinishShared {
+  Shared sh;
+  FinishSort fs;
+};
+
+// One work-group per row, after topk_digit_select. Zeroes the row's counts
+// and fill, then sorts the listed candidates (every key at or above the
+// threshold digit, held kSortPerThread per thread) by one counting sort over
+// kSortBins linear buckets of their radix keys between the threshold digit
+// and the top digit, and writes the first `count` of them. With a bucket of
+// more than kSortBucketMax keys, or an incomplete list, it splits the
+// threshold digit's keys first (in LDS, or over the row when they exceed
+// kRefineCap or were not listed) and sorts the `count` keys as select_row
+// does. A row whose counts do not sum to its columns runs select_row over
+// its scores.
+__global__ __launch_bounds__(kThreads, 1) void topk_digit_finish(const float* __restrict__ scores,
+                                                                int64_t cols, int64_t ld,
+                                                                int total_count,
+                                                                float* __restrict__ values,
+                                                                int32_t* __restrict__ ids,
+                                                                int64_t out_ld, DigitWorkspace ws,
+                                                                bool listed) {
+  __shared__ FinishShared lds;
+  __shared__ uint32_t info[6];  // valid, digit, above, bucket, top, fill
+  FinishSort& fs = lds.fs;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t r = blockIdx.x;
+  const int count = total_count < cols ? total_count : (int)cols;
+  uint32_t* row_counts = ws.counts + r * kBins;
+  const uint64_t* list = ws.lists + r * kListCap;
+  // One round of loads: the threshold record, the fill and the first
+  // kSortEager key slots of every thread (the list is that long whatever
+  // its fill, so these loads stay inside it).
+  uint64_t key[kSortPerThread];
+#pragma unroll
+  for (int j = 0; j < kSortEager; ++j) key[j] = list[tid + j * kThreads];
+  if (!listed) {
+    // No selection launch ran: the threshold comes from the counts here.
+    if (tid < 64) {
+      const Threshold t = row_threshold(row_counts, (uint32_t)count);
+      if (lane == 0) {
+        info[0] = t.total == (uint32_t)cols;
+        info[1] = t.digit;
+        info[2] = t.above;
+        info[3] = t.bucket;
+        info[4] = t.top;
+        info[5] = 0;
+      }
+    }
+  } else if (tid < 5) {
+    info[tid] = ws.threshold[r * 8 + tid];
+  } else if (tid == 5) {
+    info[5] = ws.fill[r];
+  }
+  for (int i = tid; i < kSortBins; i += kThreads) fs.cursor[i] = 0;
+  if (tid == 0) fs.crowded = 0;
+  __syncthreads();
+  for (int i = tid; i < kBins; i += kThreads) row_counts[i] = 0;
+  if (tid == 0) ws.fill[r] = 0;
+  if (count >= cols || !info[0]) {
+    select_row<kResidentVecSmall>(lds.sh, scores, cols, ld, total_count, values, ids, out_ld,
+                                  nullptr, r, 0, 1);
+    return;
+  }
+  const uint32_t d0 = info[1], above = info[2], bucket = info[3], top = info[4];
+  const uint32_t n = above + bucket;
+  const bool complete = listed && info[5] == n;
+  float* vout = values + r * out_ld;
+  int32_t* iout = ids + r * out_ld;
+  auto emit = [&](int i, uint64_t k) {
+    const uint32_t b = key_bits((uint32_t)(k >> 32));
+    vout[i] = __uint_as_float(b);
+    const bool finite = (b & 0x7F800000u) != 0x7F800000u;
+    iout[i] = finite ? (int32_t)(~(uint32_t)k) : -1;
+  };
+  if (complete) {
+    if (n > (uint32_t)(kSortEager * kThreads)) {
+#pragma unroll
+      for (int j = kSortEager; j < kSortPerThread; ++j) key[j] = list[tid + j * kThreads];
+    }
+    // Linear buckets over the radix keys [d0 << 21, (top + 1) << 21),
+    // descending order = descending bucket, then descending key.
+    const uint32_t lo = d0 << 21;
+    const uint32_t span = ((top + 1) << 21) - lo;  // top >= d0; 0 stands for 2^32
+    const int bits = 32 - __builtin_clz((span - 1) | 1u);
+    const int shift = bits > 12 ? bits - 12 : 0;
+    // (Clamped: keys outside the range only come with counts that disagree
+    // with the scores, and must not index outside the buckets.)
+    auto bucket_of = [lo, shift](uint64_t k) {
+      return min(((uint32_t)(k >> 32) - lo) >> shift, (uint32_t)kSortBins - 1);
+    };
+#pragma unroll
+    for (int j = 0; j < kSortPerThread; ++j)
+      if (tid + j * kThreads < (int)n) atomicAdd(&fs.cursor[bucket_of(key[j])], 1u);
+    __syncthreads();
+    // Thread t owns buckets 4t .. 4t + 3; start = keys in higher buckets.
+    uint32_t c4[4], own = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      c4[j] = fs.cursor[4 * tid + j];
+      own += c4[j];
+      if (c4[j] > kSortBucketMax) fs.crowded = 1;
+    }
+    uint32_t incl = own;  // keys in buckets of this and higher threads of the wave
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const uint32_t o = __shfl_down(incl, d);
+      if (lane + d < 64) incl += o;
+    }
+    if (lane == 0) fs.wave_sums[wave] = incl;
+    __syncthreads();
+    uint32_t higher = incl - own;
+    for (int w = wave + 1; w < kThreads / 64; ++w) higher += fs.wave_sums[w];
+#pragma unroll
+    for (int j = 3; j >= 0; --j) {
+      fs.start[4 * tid + j] = higher;
+      fs.cursor[4 * tid + j] = higher;
+      higher += c4[j];
+    }
+    __syncthreads();
+    if (!fs.crowded) {
+#pragma unroll
+      for (int j = 0; j < kSortPerThread; ++j)
+        if (tid + j * kThreads < (int)n) fs.sorted[atomicAdd(&fs.cursor[bucket_of(key[j])], 1u)] = key[j];
+      __syncthreads();
+      // Rank inside the bucket; bucket b spans [start[b], start[b - 1]).
+      for (uint32_t i = tid; i < n; i += kThreads) {
+        const uint64_t k = fs.sorted[i];
+        const uint32_t b = bucket_of(k);
+        const uint32_t b0 = fs.start[b], b1 = b ? fs.start[b - 1] : n;
+        uint32_t rank = b0;
+        for (uint32_t j = b0; j < b1; ++j) rank += fs.sorted[j] > k ? 1u : 0u;
+        if (rank < (uint32_t)count) fs.out[rank] = k;
+      }
+      __syncthreads();
+      for (int i = tid; i < count; i += kThreads) emit(i, fs.out[i]);
+      return;
+    }
+    __syncthreads();  // before the fallback reuses the LDS
+  }
+  // Fallback: split the threshold digit's keys to exactly `count` keys, then sort.
+  Shared& sh = lds.sh;
+  const uint64_t prefix = (uint64_t)d0 << kShift[0];
+  const uint32_t remaining = (uint32_t)count - above;
+  if (tid == 0) {
+    sh.n_sel = 0;
+    sh.n_buf = 0;
+  }
+  __syncthreads();
+  if (complete && bucket <= (uint32_t)kRefineCap) {
+#pragma unroll
+    for (int j = 0; j < kSortPerThread; ++j) {
+      const bool live = tid + j * kThreads < (int)n;
+      const bool is_above = live && (key[j] >> kShift[0]) > d0;
+      const bool in_bucket = live && !is_above;
+      const uint32_t slot_above = wave_slot(&sh.n_sel, is_above);
+      const uint32_t slot_bucket = wave_slot(&sh.n_buf, in_bucket);
+      if (is_above && slot_above < (uint32_t)kMaxK) sh.sel[slot_above] = key[j];
+      if (in_bucket && slot_bucket < (uint32_t)kRefineCap) sh.buf[slot_bucket] = key[j];
+    }
+    __syncthreads();
+    refine_buffer(sh, prefix, kShift[0], remaining, bucket == remaining, bucket);
+  } else {
+    const float* row = scores + r * ld;
+    refine_from_row(sh, row, cols, (reinterpret_cast<uintptr_t>(row) & 15) == 0, prefix,
+                    kShift[0], remaining, bucket == remaining);
+  }
+  __syncthreads();
+  sort_selected(sh, count);
+  for (int i = tid; i < count; i += kThreads) emit(i, sh.sel[i]);
+}
 }  // namespace
 }  // namespace dsa
 
@@ -838,6 +1300,49 @@ extern "C" int dsa_topk_radix(const float* scores, int64_t rows, int64_t columns
                                                              : topk_rows<kResidentVecLarge>;
   hipLaunchKernelGGL(kernel, dim3((unsigned)rows, 1), dim3(kThreads), 0, stream, scores, columns,
                      ld, (int)count, values, indices, out_ld, nullptr);
+  DSA_CHECK_LAUNCH("exact top-k");
+  return kOk;
+}
+
+
+extern "C" int dsa_indexer_topk_workspace_bytes(int64_t rows, int64_t columns, int64_t* bytes) {
+  using namespace dsa;
+  DSA_CHECK_ARG(rows >= 0 && rows < 0x7FFFFFFF && columns >= 1 && columns < 0x7FFFFFFF &&
+                    bytes != nullptr,
+                "invalid indexer top-k workspace query");
+  *bytes = digit_workspace_bytes(rows, columns);
+  return kOk;
+}
+
+extern "C" int dsa_topk_radix_digits(const float* scores, int64_t rows, int64_t columns,
+                                     int64_t ld, int64_t k, float* values, int32_t* indices,
+                                     int64_t out_ld, void* workspace, int64_t workspace_bytes,
+                                     hipStream_t stream) {
+  using namespace dsa;
+  DSA_CHECK_ARG(columns >= 1, "scores must have nonempty visible tokens");
+  DSA_CHECK_ARG(k >= 1 && k <= kMaxK, "k must be an integer in [1, 2048]");
+  DSA_CHECK_ARG(ld >= columns && rows >= 0, "invalid score layout");
+  DSA_CHECK_ARG(columns < (int64_t)0x7FFFFFFF, "column count must fit int32");
+  const int64_t count = k < columns ? k : columns;
+  DSA_CHECK_ARG(out_ld >= count, "output row stride too small");
+  if (rows == 0) return kOk;
+  DSA_CHECK_ARG(scores && values && indices, "null pointer");
+  DSA_CHECK_ARG(rows < 0x7FFFFFFF, "too many rows");
+  DSA_CHECK_ARG(workspace != nullptr && reinterpret_cast<uintptr_t>(workspace) % 8 == 0 &&
+                    workspace_bytes >= digit_workspace_bytes(rows, columns),
+                "indexer top-k workspace too small or misaligned");
+  const DigitWorkspace ws = digit_workspace(workspace, rows, columns);
+  // Rows of more than 64 parts are split over their scores by the finish
+  // kernel alone (no selection launch).
+  const bool listed = ws.parts <= 64;
+  if (count < columns && listed) {
+    const int64_t part_cols = ((columns + ws.parts - 1) / ws.parts + 3) & ~(int64_t)3;
+    hipLaunchKernelGGL(topk_digit_select, dim3((unsigned)rows, (unsigned)ws.parts), dim3(kThreads),
+                       0, stream, scores, columns, ld, (int)count, part_cols, ws);
+    DSA_CHECK_LAUNCH("exact top-k");
+  }
+  hipLaunchKernelGGL(topk_digit_finish, dim3((unsigned)rows), dim3(kThreads), 0, stream, scores,
+                     columns, ld, (int)count, values, indices, out_ld, ws, listed);
   DSA_CHECK_LAUNCH("exact top-k");
   return kOk;
 }

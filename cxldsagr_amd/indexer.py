@@ -8,6 +8,9 @@ validation messages and output layouts):
   (resident branch; the fused ECHO prefetch branch ``:412-483`` is replaced by
   the top-k-driven gather in ``cxldsagr_amd.token_pool``)
 * ``exact_topk``      - ``operators/deepseek_v32/indexer/selection.py:62-113``
+* ``logits_topk``     - ``logits`` then ``exact_topk`` as the indexer step of
+  ``models/deepseek_v32/attention.py:338-363`` calls them, fused through the
+  logits kernel's radix-digit counts
 
 All work runs in hand-written gfx950 kernels (``csrc/quantize.hip``,
 ``csrc/logits.hip``, ``csrc/topk.hip``) on the caller's current stream, with
@@ -161,19 +164,66 @@ def logits(q, k, weights, kscale, query_start, prefetch=None, *, _bounds=None,
     ``_q_fold`` (f32 ``[Q, 4, 128]``, from the layer prologue) carries the
     partial folded queries the kernel would otherwise form; same result bits.
     """
+    if type(_pad_to_stride) is not bool:
+        raise ValueError("_pad_to_stride must be boolean")
+    if prefetch is not None:
+        raise NotImplementedError(
+            "fused ECHO prefetch is replaced by the top-k-driven gather (token_pool)"
+        )
+    args, q_fold, output, _operands = _logits_launch_args(q, k, weights, kscale, query_start,
+                                                          _bounds, _q_fold)
+    device = q.device
+    with torch.cuda.device(device):
+        if q_fold is None:
+            _native.call("dsa_indexer_logits_fp8", *args, _native.ptr(output),
+                         _native.stream_of(device))
+        else:
+            _native.call("dsa_indexer_logits_fp8_folded", *args, _native.ptr(q_fold),
+                         _native.ptr(output), _native.stream_of(device))
+    return output if _pad_to_stride else output[:, :len(k)]
+
+
+def logits_topk(q, k, weights, kscale, query_start, topk, *, _bounds=None, _q_fold=None):
+    """``logits`` then ``exact_topk`` of its logical ``[Q, N]`` view, fused.
+
+    The logits kernel also counts each row's scores by the top 11 bits of their
+    radix key, and the top-k starts from those counts instead of its own
+    histogram pass over the scores (the coarse score buckets of the reference's
+    fused ECHO kernel, ``indexer/csrc/echo_logits.cuh:497-561``, put to the
+    selection instead of the prefetch). Returns ``(scores, values, indices)``:
+    the padded score matrix of ``logits(..., _pad_to_stride=True)`` and the
+    ``exact_topk(scores[:, :N], topk)`` outputs, bit for bit the unfused ones.
+    This is the indexer step of ``models/deepseek_v32/attention.py:338-363``.
+    """
+    if type(topk) is not int or not 1 <= topk <= 2048:
+        raise ValueError("k must be an integer in [1, 2048]")
+    args, q_fold, scores, _operands = _logits_launch_args(q, k, weights, kscale, query_start,
+                                                          _bounds, _q_fold)
+    rows, columns, device = len(q), len(k), q.device
+    count = min(topk, columns)
+    values = torch.empty((rows, count), dtype=torch.float32, device=device)
+    indices = torch.empty((rows, count), dtype=torch.int32, device=device)
+    with torch.cuda.device(device):
+        stream = _native.stream_of(device)
+        workspace = _digit_workspace(device, stream, rows, columns)
+        _native.call("dsa_indexer_topk_fp8", *args, _native.ptr(q_fold), _native.ptr(scores), topk,
+                     _native.ptr(values), _native.ptr(indices), count, _native.ptr(workspace),
+                     workspace.numel(), stream)
+    return scores, values, indices
+
+
+def _logits_launch_args(q, k, weights, kscale, query_start, bounds, q_fold):
+    """Validation of ``echo.py:299-330`` and the kernel arguments up to ``ldo``;
+    returns ``(args, q_fold, output, operands)`` with the padded output
+    allocated; ``operands`` holds the (possibly realigned) inputs the pointers
+    in ``args`` refer to, to be kept alive until the launch."""
     if q.ndim != 3 or q.shape[1:] != (64, 128) or not q.is_cuda or len(q) < 1:
         raise ValueError("ECHO requires nonempty CUDA Q[query,64,128]")
     if k.ndim != 2 or k.shape[1] != 128 or len(k) < 1:
         raise ValueError("ECHO requires nonempty K[token,128]")
     rows, columns, device = len(q), len(k), q.device
-    if type(_pad_to_stride) is not bool:
-        raise ValueError("_pad_to_stride must be boolean")
     if type(query_start) is not int or not 0 <= query_start <= columns - rows:
         raise ValueError("query_start must place all query rows inside the visible KV sequence")
-    if prefetch is not None:
-        raise NotImplementedError(
-            "fused ECHO prefetch is replaced by the top-k-driven gather (token_pool)"
-        )
     _native.require_gfx950(device, "fp8 MQA logits")
     for tensor, shape, dtype, name in (
         (q, (rows, 64, 128), torch.float8_e4m3fn, "q"),
@@ -183,28 +233,21 @@ def logits(q, k, weights, kscale, query_start, prefetch=None, *, _bounds=None,
     ):
         _check_tensor(tensor, shape, dtype, device, name)
     starts = ends = None
-    if _bounds is not None:
-        starts, ends = _bounds
+    if bounds is not None:
+        starts, ends = bounds
         _check_tensor(starts, (rows,), torch.int32, device, "starts")
         _check_tensor(ends, (rows,), torch.int32, device, "ends")
-    if _q_fold is not None:
-        _check_tensor(_q_fold, (rows, 4, 128), torch.float32, device, "_q_fold")
-        if _q_fold.data_ptr() % 16:
-            _q_fold = _q_fold.clone()
+    if q_fold is not None:
+        _check_tensor(q_fold, (rows, 4, 128), torch.float32, device, "_q_fold")
+        if q_fold.data_ptr() % 16:
+            q_fold = q_fold.clone()
     # The kernel reads q, k and weights in 16-byte units.
     q, k, weights = (t if t.data_ptr() % 16 == 0 else t.clone() for t in (q, k, weights))
     width = padded_columns(columns)
     output = torch.empty((rows, width), dtype=torch.float32, device=device)
     args = [_native.ptr(q), _native.ptr(k), _native.ptr(weights), _native.ptr(kscale),
             _native.ptr(starts), _native.ptr(ends), query_start, rows, columns, width]
-    with torch.cuda.device(device):
-        if _q_fold is None:
-            _native.call("dsa_indexer_logits_fp8", *args, _native.ptr(output),
-                         _native.stream_of(device))
-        else:
-            _native.call("dsa_indexer_logits_fp8_folded", *args, _native.ptr(_q_fold),
-                         _native.ptr(output), _native.stream_of(device))
-    return output if _pad_to_stride else output[:, :columns]
+    return args, q_fold, output, (q, k, weights)
 
 
 def exact_topk(scores, k):
@@ -261,6 +304,22 @@ def exact_topk(scores, k):
 # Per (device, stream) workspace of the two-part top-k (the sorted half lists
 # of every row), reused by all stream-ordered calls on that stream.
 _TOPK_WORKSPACES = {}
+
+# Per (device, stream) workspace of ``logits_topk`` (radix-digit counts, list
+# lengths and key lists): zero-filled when allocated; every fused call leaves
+# the counts and lengths zero again.
+_DIGIT_WORKSPACES = {}
+
+
+def _digit_workspace(device, stream, rows, columns):
+    key = (device.index, stream.value)
+    workspace = _DIGIT_WORKSPACES.get(key)
+    needed = ctypes.c_int64()
+    _native.call("dsa_indexer_topk_workspace_bytes", rows, columns, ctypes.byref(needed))
+    if workspace is None or workspace.numel() < needed.value:
+        workspace = torch.zeros(needed.value, dtype=torch.uint8, device=device)
+        _DIGIT_WORKSPACES[key] = workspace
+    return workspace
 
 
 def _topk_workspace(device, stream, rows):

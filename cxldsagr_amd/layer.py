@@ -8,8 +8,9 @@ Follows the stage order of the reference's ``EchoAttentionRunner._forward``
 2. quantise the new tokens' index K straight into the resident index cache
    (``attention.py:323-326``; A3);
 3. fp8 logits with the causal ``-inf`` tail over the aligned score storage
-   (``attention.py:338-353``; A4);
-4. exact top-k (``attention.py:358-370``; A6);
+   (``attention.py:338-353``; A4), counting each row's scores by radix digit;
+4. exact top-k from those counts (``attention.py:358-370``; A6), fused with
+   step 3 through ``indexer.logits_topk``;
 5. append the new tokens' KV records (quantise-on-append into the fp8 paged
    cache, or a bf16 copy) (``attention.py:400-401``);
 6. sparse MLA over the selection (``attention.py:201-235``; A7).
@@ -107,9 +108,8 @@ class DSALayer:
         q8, _, weights = indexer.quantize_index_folded(index_q, weights)
         indexer.quantize_into(index_k, self.index_keys[position:end],
                               self.index_scales[position:end])
-        scores = indexer.logits(q8, self.index_keys[:end], weights, self.index_scales[:end],
-                                position, _pad_to_stride=end >= self.topk)
-        _, ids = indexer.exact_topk(scores, self.topk)
+        _, _, ids = indexer.logits_topk(q8, self.index_keys[:end], weights,
+                                        self.index_scales[:end], position, self.topk)
         return TokenSelection(ids)
 
     def consume(self, q, selection, kv, position):
@@ -180,9 +180,9 @@ class DSALayer:
                                   self.index_scales[position:end])
             q8, _, folded = indexer.quantize_index_folded(index_q, weights)
             self._append_kv(kv, position)
-        scores = indexer.logits(q8, self.index_keys[:end], folded, self.index_scales[:end],
-                                position, _pad_to_stride=end >= self.topk, _q_fold=q_fold)
-        _, ids = indexer.exact_topk(scores, self.topk)
+        _, _, ids = indexer.logits_topk(q8, self.index_keys[:end], folded,
+                                        self.index_scales[:end], position, self.topk,
+                                        _q_fold=q_fold)
         selection = TokenSelection(ids)
         out = self._attend(q, ids, end)
         self.written = end
@@ -267,9 +267,8 @@ class OffloadDSALayer:
             raise ValueError("query batch exceeds the layer capacity or inputs disagree in length")
         q8, _, folded = indexer.quantize_index_folded(index_q, weights)
         indexer.quantize_into(index_k, self.index_keys[position:end], self.index_scales[position:end])
-        scores = indexer.logits(q8, self.index_keys[:end], folded, self.index_scales[:end],
-                                position, _pad_to_stride=end >= self.topk)
-        _, ids = indexer.exact_topk(scores, self.topk)
+        _, _, ids = indexer.logits_topk(q8, self.index_keys[:end], folded,
+                                        self.index_scales[:end], position, self.topk)
         return ids
 
     def consume(self, q, ids, *, written, transient_start=None):

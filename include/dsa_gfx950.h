@@ -139,6 +139,66 @@ int dsa_topk_radix_split_static(const float* scores, int64_t rows, int64_t colum
                                 int64_t k, float* values, int32_t* indices, int64_t out_ld,
                                 hipStream_t stream);
 
+/*
+ * A4, dsa_indexer_logits_fp8 (q_fold NULL) or dsa_indexer_logits_fp8_folded
+ * (q_fold given) with the same output bits, that also adds to digit_counts
+ * (uint32 [rows, 2048], 4-byte aligned) the number of each row's scores in
+ * columns [0, columns) by the top 11 bits of their fp32 radix key (the
+ * counts dsa_topk_radix_digits takes; masked and -inf columns included).
+ * The counts are added, so they start from zero for a fresh histogram.
+ * Replaces the same logits() (echo.py:299-410) with the per-query coarse
+ * score buckets of the reference's ECHO kernel
+ * (indexer/csrc/echo_logits.cuh:497-561) at the top-k's digit width.
+ */
+int dsa_indexer_logits_fp8_counted(const void* q, const void* k, const float* weights,
+                                   const float* kscale, const int32_t* starts,
+                                   const int32_t* ends, int64_t query_start, int64_t rows,
+                                   int64_t columns, int64_t ldo, const float* q_fold, float* out,
+                                   uint32_t* digit_counts, hipStream_t stream);
+
+/*
+ * A6 given the level-0 radix histogram: same contract and results as
+ * dsa_topk_radix. The workspace (dsa_indexer_topk_workspace_bytes(rows,
+ * columns, &bytes), 8-byte aligned, all zero before the first use) starts with
+ * uint32 [rows, 2048] digit counts, which the caller adds for each row before
+ * the call: the number of the row's scores in columns [0, columns) whose
+ * fp32 radix key (bits | 0x80000000 for non-negative values, ~bits for
+ * negative ones) has each value of its top 11 bits, as
+ * dsa_indexer_logits_fp8_counted accumulates them. A first launch reads each
+ * row once over several work-groups and lists only its keys at or above the
+ * digit where the count-th largest key lies; a second launch, one
+ * work-group per row, splits that digit's keys, sorts and writes the row.
+ * The call leaves the whole workspace all zero again except the key lists.
+ * A row whose counts do not sum to `columns` runs the full selection over its
+ * scores (same results). Replaces the same exact_topk (selection.py:62-113);
+ * the counts follow the per-query coarse score buckets of the reference's
+ * ECHO kernel (indexer/csrc/echo_logits.cuh:497-561). Calls that overlap on
+ * different streams need distinct workspaces.
+ */
+int dsa_indexer_topk_workspace_bytes(int64_t rows, int64_t columns, int64_t* bytes);
+int dsa_topk_radix_digits(const float* scores, int64_t rows, int64_t columns, int64_t ld, int64_t k,
+                          float* values, int32_t* indices, int64_t out_ld, void* workspace,
+                          int64_t workspace_bytes, hipStream_t stream);
+
+/*
+ * A4 + A6 fused: dsa_indexer_logits_fp8_counted into scores [rows, ldo]
+ * with the start of the workspace as its digit counts, then
+ * dsa_topk_radix_digits over scores[:, 0:columns) with that workspace: the
+ * same scores, values and indices as the two calls logits then
+ * dsa_topk_radix. Workspace as for dsa_topk_radix_digits (all zero before
+ * the first use; the counts and lengths are zero again after every call).
+ * Calls that overlap on different streams need distinct workspaces. Replaces the
+ * reference's logits() followed by exact_topk() in the indexer step
+ * (models/deepseek_v32/attention.py:338-363, echo.py:299-410,
+ * selection.py:62-113).
+ */
+int dsa_indexer_topk_fp8(const void* q, const void* k, const float* weights, const float* kscale,
+                         const int32_t* starts, const int32_t* ends, int64_t query_start,
+                         int64_t rows, int64_t columns, int64_t ldo, const float* q_fold,
+                         float* scores, int64_t topk, float* values, int32_t* indices,
+                         int64_t out_ld, void* workspace, int64_t workspace_bytes,
+                         hipStream_t stream);
+
 
 /*
  * A8 producer - pack bf16 [tokens, 576] (512 latent + 64 RoPE) into the

@@ -16,6 +16,14 @@ Pinned by ``tests/test_oracle_logits_topk.py``: values equal ``torch.topk`` bit-
 ids equal torch's stable descending argsort on rows without signed zeros, the
 reference's known answers (all-equal rows -> ``arange``, masked rows -> -1, the
 signed-zero/extreme-value row), and a brute-force Python sort on small rows.
+
+``digit_counts`` is the level-0 histogram of a radix selection over these keys
+(per row, the count of keys by their top 11 bits): what FlashInfer's radix
+top-k histograms first and, at a coarser width, the per-query score buckets
+of the reference's ECHO logits kernel (``indexer/csrc/echo_logits.cuh:497-561``).
+Pinned by the same test file: counts sum to the columns, a per-element Python
+loop on small rows, and the bucket where the descending suffix count first
+reaches ``k`` holds the ``k``-th value of ``exact_topk``.
 """
 
 import numpy as np
@@ -44,3 +52,16 @@ def exact_topk(scores, k):
     ids = order.astype(np.int32)
     ids[~np.isfinite(values)] = -1
     return values, ids
+
+
+DIGIT_BITS = 11
+
+
+def digit_counts(scores):
+    """float32 [R, C] -> int64 [R, 2048]: per row, keys by ``radix_key >> 21``."""
+    keys = radix_keys(np.asarray(scores, dtype=np.float32)) >> np.uint32(32 - DIGIT_BITS)
+    rows = keys.shape[0]
+    counts = np.zeros((rows, 1 << DIGIT_BITS), dtype=np.int64)
+    for r in range(rows):
+        counts[r] = np.bincount(keys[r].astype(np.int64), minlength=1 << DIGIT_BITS)
+    return counts

@@ -126,3 +126,34 @@ def test_topk_brute_force_python_sort():
     for r in range(4):
         order = sorted(range(50), key=lambda j: (-scores[r, j], j))[:20]
         assert ids[r].tolist() == order
+
+
+def test_digit_counts_pins():
+    """Counts sum to the columns; equal a per-element loop over the float bits
+    (struct, no numpy views); the suffix count reaches k in the bucket that
+    holds exact_topk's k-th value."""
+    import struct
+
+    rng = np.random.default_rng(9)
+    scores = (rng.standard_normal((5, 700)) * rng.choice([1e-30, 1.0, 1e30], (5, 700))).astype(np.float32)
+    scores[0, ::7] = -np.inf
+    scores[1, :300] = 0.0
+    scores[1, 300:310] = -0.0
+    scores[2, 5] = np.nan
+    scores[3, 9] = np.inf
+    counts = topk.digit_counts(scores)
+    assert counts.shape == (5, 2048) and (counts.sum(axis=1) == 700).all()
+    for r in range(2):
+        loop = [0] * 2048
+        for v in scores[r].tolist():
+            (b,) = struct.unpack("<I", struct.pack("<f", v))
+            key = (~b & 0xFFFFFFFF) if b >> 31 else (b | 0x80000000)
+            loop[key >> 21] += 1
+        assert counts[r].tolist() == loop
+    for k in (1, 17, 350, 700):
+        values, _ = topk.exact_topk(scores, k)
+        for r in range(5):
+            suffix = np.cumsum(counts[r][::-1])[::-1]  # keys at or above each bucket
+            bucket = int(np.nonzero(suffix >= k)[0].max())
+            kth = topk.radix_keys(values[r, k - 1:k])[0] >> 21
+            assert bucket == kth
