@@ -980,6 +980,8 @@ __device__ __forceinline__ uint32_t wave_prefix(uint32_t n, uint32_t* total) {
   return pre;
 }
 
+typedef uint32_t v4u32 __attribute__((ext_vector_type(4)));
+
 struct SelectShared {
   uint64_t staged[kThreads / 64][kWaveCap];
   uint32_t wave_count[kThreads / 64];
@@ -1032,19 +1034,24 @@ __global__ __launch_bounds__(kThreads, 1) void topk_digit_select(const float* __
 #pragma unroll
     for (int e = 0; e < 4 * kSelectVec; ++e) bits[e] = 0;
   } else {
+    // Raw buffer loads over the part's n columns: dwords past the end read
+    // as 0 (the hardware's range check), so every load is unconditional and
+    // the waits for them can follow the loads in order.
+    const __amdgpu_buffer_rsrc_t part_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(row), (short)0, (int)(n * 4), 0x00020000);
+    if (vec) {
 #pragma unroll
-    for (int d = 0; d < kSelectVec; ++d) {
-      const uint32_t c = column(4 * d);
-      if (vec && c + 3 < n) {
-        const float4 x = reinterpret_cast<const float4*>(row)[c >> 2];
-        bits[4 * d] = __float_as_uint(x.x);
-        bits[4 * d + 1] = __float_as_uint(x.y);
-        bits[4 * d + 2] = __float_as_uint(x.z);
-        bits[4 * d + 3] = __float_as_uint(x.w);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) bits[4 * d + e] = c + e < n ? __float_as_uint(row[c + e]) : 0u;
+      for (int d = 0; d < kSelectVec; ++d) {
+        const v4u32 x = __builtin_amdgcn_raw_buffer_load_b128(part_rsrc, (int)(column(4 * d) * 4), 0, 0);
+        bits[4 * d] = x.x;
+        bits[4 * d + 1] = x.y;
+        bits[4 * d + 2] = x.z;
+        bits[4 * d + 3] = x.w;
       }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4 * kSelectVec; ++e)
+        bits[e] = __builtin_amdgcn_raw_buffer_load_b32(part_rsrc, (int)(column(e) * 4), 0, 0);
     }
   }
   __syncthreads();
@@ -1060,23 +1067,26 @@ __global__ __launch_bounds__(kThreads, 1) void topk_digit_select(const float* __
   const uint32_t not_col0 = ~(uint32_t)col0;
   uint64_t* staged = ss.staged[wave];
   uint32_t off = 0;  // wave-uniform
-#pragma unroll
-  for (int e = 0; e < 4 * kSelectVec; ++e) {
-    const uint32_t c = column(e);
-    uint32_t key;
-    bool hit;
-    if (nonnegative) {
-      key = bits[e] | 0x80000000u;
-      hit = (int32_t)bits[e] >= floor_bits;
-    } else {
-      key = radix_key(__uint_as_float(bits[e]));
-      hit = key >= floor_key;
-    }
-    hit = hit && wave != 0 && c < n;
+  auto stage = [&](int e, uint32_t key, bool hit) {
     const uint64_t m = __builtin_amdgcn_ballot_w64(hit);
     const uint32_t pos = off + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
-    if (hit && pos < (uint32_t)kWaveCap) staged[pos] = ((uint64_t)key << 32) | (uint64_t)(not_col0 - c);
+    if (hit && pos < (uint32_t)kWaveCap) staged[pos] = ((uint64_t)key << 32) | (uint64_t)(not_col0 - column(e));
     off += (uint32_t)__builtin_popcountll(m);
+  };
+  if (wave != 0) {  // wave 0 holds no keys
+    if (nonnegative && d0 > 1024) {
+      // Above +0.0: one signed compare per key, and the zeros read past the
+      // part's end can never pass it.
+#pragma unroll
+      for (int e = 0; e < 4 * kSelectVec; ++e)
+        stage(e, bits[e] | 0x80000000u, (int32_t)bits[e] >= floor_bits);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4 * kSelectVec; ++e) {
+        const uint32_t key = radix_key(__uint_as_float(bits[e]));
+        stage(e, key, key >= floor_key && column(e) < n);
+      }
+    }
   }
   if (lane == 0) ss.wave_count[wave] = off;
   __syncthreads();
