@@ -85,12 +85,45 @@ def event_time_us(torch, fn, iters):
     return start.elapsed_time(stop) * 1e3 / iters
 
 
+def indexer_stage_calls(layer, tokens, topk, q8, folded, q_fold):
+    """The two launches of the layer's indexer step (``indexer.logits_topk``)
+    as separate calls: logits with their radix-digit counts, then the top-k
+    that starts from the counts. Returns (logits_fn, topk_fn, ids)."""
+    import ctypes
+
+    import torch
+
+    from cxldsagr_amd import _native, indexer
+
+    device = q8.device
+    rows, width = len(q8), indexer.padded_columns(tokens)
+    scores = torch.empty(rows, width, device=device)
+    ids = torch.empty(rows, min(topk, tokens), dtype=torch.int32, device=device)
+    values = torch.empty(rows, min(topk, tokens), device=device)
+    needed = ctypes.c_int64()
+    _native.call("dsa_indexer_topk_workspace_bytes", rows, tokens, ctypes.byref(needed))
+    workspace = torch.zeros(needed.value, dtype=torch.uint8, device=device)
+    keys, kscale = layer.index_keys[:tokens], layer.index_scales[:tokens]
+    history = tokens - rows
+
+    def logits_fn():
+        _native.call("dsa_indexer_logits_fp8_counted", _native.ptr(q8), _native.ptr(keys),
+                     _native.ptr(folded), _native.ptr(kscale), None, None, history, rows, tokens,
+                     width, _native.ptr(q_fold), _native.ptr(scores), _native.ptr(workspace),
+                     _native.stream_of(device))
+
+    def topk_fn():
+        _native.call("dsa_topk_radix_digits", _native.ptr(scores), rows, tokens, width, topk,
+                     _native.ptr(values), _native.ptr(ids), ids.shape[1], _native.ptr(workspace),
+                     workspace.numel(), _native.stream_of(device))
+
+    return logits_fn, topk_fn, ids
+
+
 def in_layer_stage_us(torch, layer, history, tokens, topk, iters, args):
     """Average duration of each stage of the layer step, from HIP events recorded
-    between its launches on the current stream (the same calls, in the same
+    between its launches on the current stream (the same launches, in the same
     order, as DSALayer.forward with the fused prologue)."""
-    from cxldsagr_amd import indexer
-
     index_q, index_k, weights, mla_q, kv = args
     if not layer._fused_prologue_applies(index_q, index_k, weights, kv):
         raise RuntimeError("bench expects the fused layer prologue")
@@ -98,16 +131,18 @@ def in_layer_stage_us(torch, layer, history, tokens, topk, iters, args):
     stream = torch.cuda.current_stream()
     marks = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
              for _ in range(iters)]
+    layer.written = history
+    q8, folded, q_fold = layer._prologue(index_q, index_k, weights, kv, history)
+    logits_fn, topk_fn, ids = indexer_stage_calls(layer, tokens, topk, q8, folded, q_fold)
     torch.cuda.synchronize()
     for ev in marks:
         layer.written = history
         ev[0].record(stream)
-        q8, folded, q_fold = layer._prologue(index_q, index_k, weights, kv, history)
+        layer._prologue(index_q, index_k, weights, kv, history)
         ev[1].record(stream)
-        scores = indexer.logits(q8, layer.index_keys[:tokens], folded, layer.index_scales[:tokens],
-                                history, _pad_to_stride=tokens >= topk, _q_fold=q_fold)
+        logits_fn()
         ev[2].record(stream)
-        _, ids = indexer.exact_topk(scores, topk)
+        topk_fn()
         ev[3].record(stream)
         layer._attend(mla_q, ids, tokens)
         ev[4].record(stream)
@@ -209,10 +244,14 @@ def main():
     _, ids = indexer.exact_topk(scores, topk)
     torch.cuda.synchronize()
 
+    # Isolated stages: the counted top-k consumes its counts, so the indexer
+    # step is timed as the pair; the unfused logits and top-k beside it.
     stages = {
         "quantize_q": lambda: indexer.quantize_index_folded(index_q, weights),
-        "logits": lambda: indexer.logits(q8, keys, w_eff, kscale, history, _pad_to_stride=True),
-        "topk": lambda: indexer.exact_topk(scores, topk),
+        "logits_topk": lambda: indexer.logits_topk(q8, keys, w_eff, kscale, history, topk),
+        "logits_unfused": lambda: indexer.logits(q8, keys, w_eff, kscale, history,
+                                                 _pad_to_stride=True),
+        "topk_unfused": lambda: indexer.exact_topk(scores, topk),
         "pack_kv": lambda: attention.pack_kv_fp8(kv_new, layer.kv_cache, layer.page_table,
                                                  token_offset=history),
         "sparse_mla": lambda: attention.sparse_mla_fp8_paged(
@@ -225,7 +264,7 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     if args.only is not None:
-        fn = step if args.only == "layer" else stages[{"mla": "sparse_mla"}.get(args.only, args.only)]
+        fn = step if args.only == "layer" else stages[{"mla": "sparse_mla", "topk": "logits_topk", "logits": "logits_unfused"}.get(args.only, args.only)]
         for _ in range(args.warmup):
             fn()
         us = event_time_us(torch, fn, args.steps)
@@ -285,7 +324,7 @@ def main():
                     "peak": PEAKS["bf16_TFLOPs"], "unit": "TFLOP/s"}
     else:
         achieved = topk_bytes / kernel_us["topk"] / 1e3
-        roofline = {"kernel": "dsa_topk_radix", "bound": "hbm", "achieved": achieved,
+        roofline = {"kernel": "dsa_topk_radix_digits", "bound": "hbm", "achieved": achieved,
                     "peak": PEAKS["hbm_GBps"], "unit": "GB/s"}
     roofline["achieved"] = round(roofline["achieved"], 1)
     roofline["frac"] = round(achieved / roofline["peak"], 4)

@@ -1102,7 +1102,10 @@ __global__ __launch_bounds__(kThreads, 1) void topk_digit_select(const float* __
   if (tid == 0) list_base = atomicAdd(&ws.fill[r], overflow ? kOverflow : total);
   __syncthreads();
   const uint32_t base = list_base;
-  if (overflow || base + total > (uint32_t)kListCap) return;  // the fill tells the finish
+  // (The fill tells the finish. Compared without a sum that could wrap: a
+  // fill that is not zero on entry - a workspace reused with another row
+  // count - must not place the list anywhere but inside it.)
+  if (overflow || base > (uint32_t)kListCap || total > (uint32_t)kListCap - base) return;
   uint64_t* list = ws.lists + r * kListCap + base + before;
   for (uint32_t i = lane; i < off; i += 64) list[i] = staged[i];
 }

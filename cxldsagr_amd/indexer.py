@@ -306,19 +306,24 @@ def exact_topk(scores, k):
 _TOPK_WORKSPACES = {}
 
 # Per (device, stream) workspace of ``logits_topk`` (radix-digit counts, list
-# lengths and key lists): zero-filled when allocated; every fused call leaves
-# the counts and lengths zero again.
+# fill and key lists) and the row count of its last call: zero-filled when
+# allocated; every fused call leaves the counts and fill of its layout zero.
 _DIGIT_WORKSPACES = {}
 
 
 def _digit_workspace(device, stream, rows, columns):
+    """The (device, stream) workspace of the fused indexer step. Its layout
+    depends on the row count, and a call only restores the zeros of its own
+    layout, so a call with another row count zeroes it first."""
     key = (device.index, stream.value)
-    workspace = _DIGIT_WORKSPACES.get(key)
+    workspace, layout_rows = _DIGIT_WORKSPACES.get(key, (None, None))
     needed = ctypes.c_int64()
     _native.call("dsa_indexer_topk_workspace_bytes", rows, columns, ctypes.byref(needed))
     if workspace is None or workspace.numel() < needed.value:
         workspace = torch.zeros(needed.value, dtype=torch.uint8, device=device)
-        _DIGIT_WORKSPACES[key] = workspace
+    elif layout_rows != rows:
+        workspace.zero_()
+    _DIGIT_WORKSPACES[key] = (workspace, rows)
     return workspace
 
 

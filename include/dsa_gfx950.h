@@ -168,7 +168,11 @@ int dsa_indexer_logits_fp8_counted(const void* q, const void* k, const float* we
  * row once over several work-groups and lists only its keys at or above the
  * digit where the count-th largest key lies; a second launch, one
  * work-group per row, splits that digit's keys, sorts and writes the row.
- * The call leaves the whole workspace all zero again except the key lists.
+ * The call leaves the counts and the list fill all zero again. The layout
+ * depends on `rows`: before a call with another row count than the last one,
+ * zero the workspace again (a workspace that is not all zero where the
+ * layout needs it costs the selection from the counts - those rows are
+ * selected from their scores - never the results or memory outside it).
  * A row whose counts do not sum to `columns` runs the full selection over its
  * scores (same results). Replaces the same exact_topk (selection.py:62-113);
  * the counts follow the per-query coarse score buckets of the reference's
@@ -186,7 +190,8 @@ int dsa_topk_radix_digits(const float* scores, int64_t rows, int64_t columns, in
  * dsa_topk_radix_digits over scores[:, 0:columns) with that workspace: the
  * same scores, values and indices as the two calls logits then
  * dsa_topk_radix. Workspace as for dsa_topk_radix_digits (all zero before
- * the first use; the counts and lengths are zero again after every call).
+ * the first use with a given row count; the counts and fill are zero again
+ * after every call).
  * Calls that overlap on different streams need distinct workspaces. Replaces the
  * reference's logits() followed by exact_topk() in the indexer step
  * (models/deepseek_v32/attention.py:338-363, echo.py:299-410,

@@ -208,9 +208,11 @@ def test_logits_topk_equals_unfused(gpu, rows, columns, query_start, topk, ragge
         assert torch.equal(scores.view(torch.int32), plain.view(torch.int32))
         assert torch.equal(got_values.view(torch.int32), values.view(torch.int32))
         assert torch.equal(got_ids, ids)
-    # The counts (the workspace's first rows * 8192 bytes) are zero again.
-    assert indexer._DIGIT_WORKSPACES
-    assert not any(w[:rows * 2048 * 4].any() for w in indexer._DIGIT_WORKSPACES.values())
+    # The counts of this stream's workspace (its first rows * 8192 bytes) are zero again.
+    from cxldsagr_amd import _native
+
+    workspace, layout_rows = indexer._DIGIT_WORKSPACES[(gpu.index, _native.stream_of(gpu).value)]
+    assert layout_rows == rows and not workspace[:rows * 2048 * 4].any()
     # Parity with the oracle's top-k of the same scores.
     ref_values, ref_ids = otopk.exact_topk(plain[:, :columns].cpu().numpy(), topk)
     np.testing.assert_array_equal(got_ids.cpu().numpy(), ref_ids)
@@ -233,3 +235,27 @@ def test_logits_topk_rejections(gpu):
                      _native.ptr(s), None, None, 296, 4, 300, 512, None, _native.ptr(scores), 2048,
                      _native.ptr(values), _native.ptr(ids), 300, _native.ptr(short), short.numel(),
                      _native.stream_of(gpu))
+
+
+def test_digits_topk_workspace_reused_across_row_counts(gpu):
+    """One workspace for calls whose row counts change (its layout depends on
+    them): a call after one with fewer rows finds the earlier call's lists
+    where its counts and fill go. Given the zeroing on a layout change (what
+    ``logits_topk`` does), every call selects from its counts; without it the
+    rows whose counts read stale select from their scores, with the same
+    results."""
+    columns, k = 65664, 2048
+    workspace, _ = _workspace(128, columns, gpu)
+    generator = torch.Generator(device="cuda").manual_seed(12)
+    for zero in (True, False):
+        for rows in (128, 5, 3, 40, 16, 128):
+            scores = torch.randn(rows, columns, device=gpu, generator=generator)
+            values, ids = _one_part_topk(scores, columns, k)
+            if zero:
+                workspace.zero_()
+            counts = workspace[:rows * 2048 * 4].view(torch.int32).view(rows, 2048)
+            counts += torch.from_numpy(otopk.digit_counts(scores.cpu().numpy()).astype(np.int32)).to(gpu)
+            got_values, got_ids = _digits_topk(scores, columns, k, workspace)
+            assert torch.equal(got_values.view(torch.int32), values.view(torch.int32)), (zero, rows)
+            assert torch.equal(got_ids, ids), (zero, rows)
+            assert not counts.any()
