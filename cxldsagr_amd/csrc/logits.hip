@@ -14,16 +14,19 @@
 //   head-weighted ReLU sum uses relu(s) = (s + |s|) / 2: the |s| half is 16
 //   in-lane FMAs per key per query (|s| is a free source modifier), and the
 //   linear half, sum_h w_h s_h / 2 = k . q' with q' = sum_h w_h q_h / 2, is
-//   one more MFMA per 16 keys for all four queries of a wave, with q' held
-//   as four e4m3 digits (q' to ~2^-17 of its largest element). The four lane
+//   one more MFMA per 16 keys for both queries of a wave, with q' held as
+//   four e4m3 digits (q' to ~2^-17 of its largest element). The four lane
 //   rows are then combined with a reduce-scatter on the gfx950 row-swap
 //   permutes (v_permlane32_swap, v_permlane16_swap) so lane l ends with key
 //   l of a 64-key pass: one coalesced 256-byte row store.
 // * The epilogue of one (query, 16-key) unit runs while the four MFMAs of the
 //   next unit execute (explicitly interleaved).
-// * Work-group: 4 waves (one per SIMD, so Q of 4 queries stays in registers
-//   and each B operand read from LDS feeds 16 MFMAs) x 4 queries = 16
-//   queries; the key range is split so the grid is about one work-group per CU.
+// * Work-group: 8 waves (two per SIMD) x 2 queries = 16 queries; the key
+//   range is split so the grid is about one work-group per CU. Q of a wave's
+//   two queries stays in registers (under 256 VGPRs, so two waves fit a
+//   SIMD) and each B operand read from LDS feeds 9 MFMAs. With one wave per
+//   SIMD the MFMA pipe idles while the wave runs its epilogue and row tail;
+//   the second wave issues MFMAs in those gaps.
 // * K stages (128 keys x 128 B, plus the 128 key scales) arrive by LDS DMA
 //   (global_load_lds_dwordx4 / _dword) into a ring kRing - 1 stages ahead,
 //   with the 16-byte chunks of each key XOR-swizzled by (key & 7) against
@@ -32,7 +35,7 @@
 // * Loads and stores never share a wave: vmcnt counts both, and with stores
 //   pending it no longer says which loads are done. Wave 0 issues every DMA
 //   (and waits on vmcnt for them) but stores nothing; its rows go through LDS
-//   to waves 1-3, which store their own rows and wave 0's in turn.
+//   to waves 1-7, which store their own rows and wave 0's in turn.
 #include <utility>
 
 #include "dsa_common.h"
@@ -48,8 +51,8 @@ typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
 constexpr int kHeads = 64;
 constexpr int kDim = 128;
-constexpr int kWaves = 4;
-constexpr int kQueriesPerWave = 4;
+constexpr int kWaves = 8;
+constexpr int kQueriesPerWave = 2;
 constexpr int kQueriesPerBlock = kWaves * kQueriesPerWave;
 constexpr int kStageKeys = 128;                    // keys per DMA stage and barrier
 constexpr int kHalfKeys = 64;                      // keys per compute pass (lane = key)
@@ -184,13 +187,14 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
   const int64_t qw = q0 + wave * kQueriesPerWave;
 
   // Linear half of the head sum: sum_h (w_h / 2) s_h = k . q' with
-  // q' = sum_h (w_h / 2) q_h, formed here in fp32 (lane 16j + c: query j,
-  // dims 8c .. 8c + 7) and written as kDigits e4m3 digits, digit d at scale
+  // q' = sum_h (w_h / 2) q_h, formed here in fp32 (lane 32j + c: query j,
+  // dims 4c .. 4c + 3) and written as kDigits e4m3 digits, digit d at scale
   // 2^(E_j - 4d) (|q'| < 2^(E_j + 8)): each digit holds the residual of the
   // ones before it to within half an e4m3 ulp, so the four carry q' to about
   // 2^-17 of its largest element. In the MFMA operand, row 4d + j is digit d
-  // of query j; its C row then sits in lane group d, register j, so the
-  // reduction over lane groups that sums head partials also sums the digits.
+  // of query j (rows 4d + 2 and 4d + 3 are zero); its C row then sits in lane
+  // group d, register j, so the reduction over lane groups that sums head
+  // partials also sums the digits.
   //
   // Load order: the inputs of q' and the head weights first, then the query
   // operands (the bulk of the bytes), so that forming q' waits only for its
@@ -198,35 +202,32 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
   __shared__ __align__(16) uint8_t digits[kWaves][kQueriesPerWave][kDigits][kDim];
   v8i qd;
   float fl[kQueriesPerWave];
-  const int fj = lane >> 4;
-  const int fc = lane & 15;
+  static_assert(kQueriesPerWave == 2, "the fold maps 32 lanes x 4 dims to a query");
+  const int fj = lane >> 5;
+  const int fc = lane & 31;
   const bool flive = qw + fj < rows;
   const int64_t fqc = flive ? qw + fj : 0;
   // q' in four partial sums over heads 16g .. 16g + 15 (each one fmaf chain
   // from 0 in increasing head order), then 0.5 (((p0 + p1) + p2) + p3): the
   // same bits whether the partials come from the layer prologue (q_fold,
   // [rows][4][128]) or are formed here.
-  float pg[4][8];
-  uint2 codes[kHeads];
+  float pg[4][4];
+  uint32_t codes[kHeads];
   v4f w4;
   if (q_fold) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const v4f* src = reinterpret_cast<const v4f*>(q_fold + (fqc * 4 + g) * kDim + 8 * fc);
-      const v4f a = src[0], b = src[1];
+      const v4f a = *reinterpret_cast<const v4f*>(q_fold + (fqc * 4 + g) * kDim + 4 * fc);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        pg[g][i] = flive ? a[i] : 0.0f;
-        pg[g][4 + i] = flive ? b[i] : 0.0f;
-      }
+      for (int i = 0; i < 4; ++i) pg[g][i] = flive ? a[i] : 0.0f;
     }
   } else {
-    // All 64 heads' codes in flight at once; the weights of heads 4c ..
-    // 4c + 3 per lane.
-    const uint8_t* qrow = q + fqc * kHeads * kDim + 8 * fc;
+    // All 64 heads' codes in flight at once; the weights of heads 4m ..
+    // 4m + 3 per lane (m = lane % 16, the lane's place in its 16-lane row).
+    const uint8_t* qrow = q + fqc * kHeads * kDim + 4 * fc;
 #pragma unroll
-    for (int h = 0; h < kHeads; ++h) codes[h] = *reinterpret_cast<const uint2*>(qrow + h * kDim);
-    w4 = *reinterpret_cast<const v4f*>(w + fqc * kHeads + 4 * fc);
+    for (int h = 0; h < kHeads; ++h) codes[h] = *reinterpret_cast<const uint32_t*>(qrow + h * kDim);
+    w4 = *reinterpret_cast<const v4f*>(w + fqc * kHeads + 4 * (fc & 15));
   }
 #pragma unroll
   for (int j = 0; j < kQueriesPerWave; ++j) {
@@ -262,7 +263,7 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
 #pragma unroll
       for (int g = 0; g < 4; ++g)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) pg[g][i] = 0.0f;
+        for (int i = 0; i < 4; ++i) pg[g][i] = 0.0f;
       // Each head's weight broadcast along the 16-lane row by DPP
       // (row_newbcast).
       auto add_head = [&](auto head) {
@@ -270,65 +271,55 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
         const float wb = __int_as_float(
             __builtin_amdgcn_update_dpp(0, __float_as_int(w4[h & 3]), 0x150 + (h >> 2), 0xF, 0xF, false));
         const float wh = flive ? wb : 0.0f;
-        const v2f x0 = __builtin_amdgcn_cvt_pk_f32_fp8(codes[h].x, false);
-        const v2f x1 = __builtin_amdgcn_cvt_pk_f32_fp8(codes[h].x, true);
-        const v2f x2 = __builtin_amdgcn_cvt_pk_f32_fp8(codes[h].y, false);
-        const v2f x3 = __builtin_amdgcn_cvt_pk_f32_fp8(codes[h].y, true);
+        const v2f x0 = __builtin_amdgcn_cvt_pk_f32_fp8(codes[h], false);
+        const v2f x1 = __builtin_amdgcn_cvt_pk_f32_fp8(codes[h], true);
         float* p = pg[h >> 4];
         p[0] = fmaf(wh, x0[0], p[0]);
         p[1] = fmaf(wh, x0[1], p[1]);
         p[2] = fmaf(wh, x1[0], p[2]);
         p[3] = fmaf(wh, x1[1], p[3]);
-        p[4] = fmaf(wh, x2[0], p[4]);
-        p[5] = fmaf(wh, x2[1], p[5]);
-        p[6] = fmaf(wh, x3[0], p[6]);
-        p[7] = fmaf(wh, x3[1], p[7]);
       };
       for_each_index(add_head, std::make_integer_sequence<int, kHeads>{});
     }
-    float qp[8];
+    float qp[4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) qp[i] = 0.5f * (((pg[0][i] + pg[1][i]) + pg[2][i]) + pg[3][i]);
+    for (int i = 0; i < 4; ++i) qp[i] = 0.5f * (((pg[0][i] + pg[1][i]) + pg[2][i]) + pg[3][i]);
     float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(qp[i]));
+    for (int i = 0; i < 4; ++i) amax = fmaxf(amax, fabsf(qp[i]));
 #pragma unroll
-    for (int m = 8; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 16));
+    for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
     int ex = 0;
     (void)frexpf(amax, &ex);  // amax < 2^ex (ex = 0 for amax = 0)
     const int e0 = ex - 8;
 #pragma unroll
     for (int d = 0; d < kDigits; ++d) {
       const int e = e0 - 4 * d;
-      uint32_t lo = 0, hi = 0;
-      lo = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(qp[0], -e), ldexpf(qp[1], -e), lo, false);
-      lo = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(qp[2], -e), ldexpf(qp[3], -e), lo, true);
-      hi = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(qp[4], -e), ldexpf(qp[5], -e), hi, false);
-      hi = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(qp[6], -e), ldexpf(qp[7], -e), hi, true);
-      *reinterpret_cast<uint2*>(&digits[wave][j][d][8 * c]) = make_uint2(lo, hi);
-      const v2f y0 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
-      const v2f y1 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
-      const v2f y2 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
-      const v2f y3 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+      uint32_t code = 0;
+      code = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(qp[0], -e), ldexpf(qp[1], -e), code, false);
+      code = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(qp[2], -e), ldexpf(qp[3], -e), code, true);
+      *reinterpret_cast<uint32_t*>(&digits[wave][j][d][4 * c]) = code;
+      const v2f y0 = __builtin_amdgcn_cvt_pk_f32_fp8(code, false);
+      const v2f y1 = __builtin_amdgcn_cvt_pk_f32_fp8(code, true);
       qp[0] -= ldexpf(y0[0], e);
       qp[1] -= ldexpf(y0[1], e);
       qp[2] -= ldexpf(y1[0], e);
       qp[3] -= ldexpf(y1[1], e);
-      qp[4] -= ldexpf(y2[0], e);
-      qp[5] -= ldexpf(y2[1], e);
-      qp[6] -= ldexpf(y3[0], e);
-      qp[7] -= ldexpf(y3[1], e);
     }
-    // A operand: lane l holds row l % 16 = 4d + j', dims 32 (l / 16) .. + 31.
+    // A operand: lane l holds row l % 16 = 4d + j', dims 32 (l / 16) .. + 31;
+    // rows j' >= 2 (no query) are zero.
     const int jr = lane & 3, dr = (lane & 15) >> 2, blk = lane >> 4;
-    const v4u lo = *reinterpret_cast<const v4u*>(&digits[wave][jr][dr][32 * blk]);
-    const v4u hi = *reinterpret_cast<const v4u*>(&digits[wave][jr][dr][32 * blk + 16]);
+    const bool jlive = jr < kQueriesPerWave;
+    const int jc = jlive ? jr : 0;
+    v4u lo = *reinterpret_cast<const v4u*>(&digits[wave][jc][dr][32 * blk]);
+    v4u hi = *reinterpret_cast<const v4u*>(&digits[wave][jc][dr][32 * blk + 16]);
+    if (!jlive) lo = hi = v4u{0u, 0u, 0u, 0u};
     qd = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
     // C rows of lane group g = digit g: register r (query r) is scaled by
     // 2^(E_r - 4g).
 #pragma unroll
     for (int r = 0; r < kQueriesPerWave; ++r)
-      fl[r] = ldexpf(1.0f, __builtin_amdgcn_readlane(e0, 16 * r) - 4 * group);
+      fl[r] = ldexpf(1.0f, __builtin_amdgcn_readlane(e0, 32 * r) - 4 * group);
   }
 
   // DMA plan (wave 0 only): K chunk p = 64 i + lane of a stage (load i) is
@@ -395,7 +386,7 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
     if constexpr (kCount) {
       const uint32_t d = score_digit(pend_v[j]);
       const uint32_t inc = ((pend_ok >> j) & 1u) << ((d >> 10) << 4);
-      atomicAdd(&bins[(4 * wave + j) * (kDigitBins / 2) + (d & 1023)], inc);
+      atomicAdd(&bins[(kQueriesPerWave * wave + j) * (kDigitBins / 2) + (d & 1023)], inc);
     }
   };
   for (int s = 0; s < stages; ++s) {
@@ -424,7 +415,7 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
         const v4u hi = lds_v4u(base + (((2 * group + 1) ^ (key & 7)) << 4));
         return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
       };
-      // Units i = 4u + j (key group u, query j): the MFMAs of unit i are issued
+      // Units i = 2u + j (key group u, query j): the MFMAs of unit i are issued
       // before the epilogue of unit i - 1.
       constexpr int kUnits = 4 * kQueriesPerWave;
       float part[kQueriesPerWave][4];
@@ -432,7 +423,7 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
       b[0] = load_b(0);
       b[1] = load_b(1);
       v4f acc[2][4];
-      v4f acc_lin[2];  // linear half of key group u (parity u & 1), all four queries
+      v4f acc_lin[2];  // linear half of key group u (parity u & 1), both queries
       auto mfmas = [&](int i) {
         const int u = i / kQueriesPerWave, j = i % kQueriesPerWave;
 #pragma unroll
