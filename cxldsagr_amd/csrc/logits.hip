@@ -75,9 +75,17 @@ constexpr int kDigitShift = 21;
 constexpr int64_t kMaxSplitKeys = 65535 / kStageKeys * kStageKeys;
 constexpr uint32_t kNegInfDigit = 0x007FFFFFu >> kDigitShift;  // radix key of -inf, top 11 bits
 
-__device__ __forceinline__ uint32_t score_digit(float v) {
+// The count word and half of a score's digit, d = radix(v) >> 21: for v >= 0
+// (sign clear) d = 1024 + bits 21-30 of v, for v < 0 d = 1023 - bits 21-30,
+// so the word d & 1023 is those bits, flipped when the sign is set, and the
+// half d >> 10 is the sign's complement.
+__device__ __forceinline__ uint32_t digit_word(float v) {
   const uint32_t b = __float_as_uint(v);
-  return ((b & 0x80000000u) ? ~b : (b | 0x80000000u)) >> kDigitShift;
+  const uint32_t flip = (uint32_t)((int32_t)b >> 31) & 1023u;
+  return ((b >> kDigitShift) & 1023u) ^ flip;
+}
+__device__ __forceinline__ uint32_t digit_half_shift(float v) {
+  return (~__float_as_uint(v) >> 27) & 16u;  // 16 for the upper half
 }
 
 
@@ -146,7 +154,7 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
   __shared__ __align__(16) uint32_t bins[kCount ? kBinWords : 4];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int group = lane >> 4;
   const int col = lane & 15;
@@ -178,6 +186,48 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
   if (max_end > columns) max_end = columns;
   const int64_t kend = ke < max_end ? ke : max_end;
   const int stages = kend > kb ? (int)((kend - kb + kStageKeys - 1) / kStageKeys) : 0;
+
+  // DMA plan (wave 0 only): K chunk p = 64 i + lane of a stage (load i) is
+  // key 8i + lane / 8, stored chunk lane % 8 = logical chunk ^ (key & 7); then
+  // 4-byte loads of the stage's key scales (key 64 i + lane). Keys past the
+  // end re-read the last key (their columns are -inf), and stages past the
+  // end key 0.
+  const uint32_t ring_base = (uint32_t)(uintptr_t)&ring[0][0];
+  const int lane_key = lane >> 3;
+  const uint32_t lane_chunk = 16u * (uint32_t)((lane & 7) ^ (lane_key & 7));
+  const uint32_t lane_off = (uint32_t)lane_key * kDim + lane_chunk;
+  auto issue = [&](int s) {
+    const uint32_t slot_base = ring_base + (uint32_t)(s % kRing) * kStageBytes;
+    const bool live = s < stages;
+    const int64_t key0 = live ? kb + (int64_t)s * kStageKeys : 0;
+    const int32_t last = live ? (int32_t)(columns - 1 - key0) : 0;  // >= 0: key0 < columns
+    const uint8_t* kbase = k + key0 * kDim;
+    if (last >= kStageKeys - 1) {
+      // A whole stage: every lane offset is a constant and the per-load
+      // steps go into the scalar base (no vector arithmetic per load).
+#pragma unroll
+      for (int i = 0; i < kKLoads; ++i) dma16_s(kbase + 1024 * i, lane_off, slot_base + i * 1024);
+#pragma unroll
+      for (int i = 0; i < kSLoads; ++i)
+        dma4_s(kscale + key0 + 64 * i, 4u * (uint32_t)lane, slot_base + kKBytes + 256 * i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kKLoads; ++i) {
+        const int32_t key = min(8 * i + lane_key, last);
+        dma16_s(kbase, (uint32_t)key * kDim + lane_chunk, slot_base + i * 1024);
+      }
+#pragma unroll
+      for (int i = 0; i < kSLoads; ++i)
+        dma4_s(kscale + key0, 4u * (uint32_t)min(64 * i + lane, last), slot_base + kKBytes + 256 * i);
+    }
+  };
+  // The first stages' keys are on their way while the query operands load
+  // (wave 0's loads complete in issue order, the DMA first).
+  if (wave == 0) {
+#pragma unroll
+    for (int s = 0; s < kRing - 1; ++s) issue(s);
+  }
+
 
   // Per-wave query operands and head weights (lane rows: heads 16t + 4g + r).
   // Key positions fit int32 (the launcher checks ldo < 2^31).
@@ -322,40 +372,6 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
       fl[r] = ldexpf(1.0f, __builtin_amdgcn_readlane(e0, 32 * r) - 4 * group);
   }
 
-  // DMA plan (wave 0 only): K chunk p = 64 i + lane of a stage (load i) is
-  // key 8i + lane / 8, stored chunk lane % 8 = logical chunk ^ (key & 7); then
-  // 4-byte loads of the stage's key scales (key 64 i + lane). Keys past the
-  // end re-read the last key (their columns are -inf), and stages past the
-  // end key 0.
-  const uint32_t ring_base = (uint32_t)(uintptr_t)&ring[0][0];
-  const int lane_key = lane >> 3;
-  const uint32_t lane_chunk = 16u * (uint32_t)((lane & 7) ^ (lane_key & 7));
-  const uint32_t lane_off = (uint32_t)lane_key * kDim + lane_chunk;
-  auto issue = [&](int s) {
-    const uint32_t slot_base = ring_base + (uint32_t)(s % kRing) * kStageBytes;
-    const bool live = s < stages;
-    const int64_t key0 = live ? kb + (int64_t)s * kStageKeys : 0;
-    const int32_t last = live ? (int32_t)(columns - 1 - key0) : 0;  // >= 0: key0 < columns
-    const uint8_t* kbase = k + key0 * kDim;
-    if (last >= kStageKeys - 1) {
-      // A whole stage: every lane offset is a constant and the per-load
-      // steps go into the scalar base (no vector arithmetic per load).
-#pragma unroll
-      for (int i = 0; i < kKLoads; ++i) dma16_s(kbase + 1024 * i, lane_off, slot_base + i * 1024);
-#pragma unroll
-      for (int i = 0; i < kSLoads; ++i)
-        dma4_s(kscale + key0 + 64 * i, 4u * (uint32_t)lane, slot_base + kKBytes + 256 * i);
-    } else {
-#pragma unroll
-      for (int i = 0; i < kKLoads; ++i) {
-        const int32_t key = min(8 * i + lane_key, last);
-        dma16_s(kbase, (uint32_t)key * kDim + lane_chunk, slot_base + i * 1024);
-      }
-#pragma unroll
-      for (int i = 0; i < kSLoads; ++i)
-        dma4_s(kscale + key0, 4u * (uint32_t)min(64 * i + lane, last), slot_base + kKBytes + 256 * i);
-    }
-  };
   // Wave 0's finished rows, [stage parity][query][key].
   __shared__ __align__(16) float staged[2][kQueriesPerWave][kStageKeys];
   auto store_staged = [&](int st) {
@@ -370,13 +386,9 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
     }
   };
 
-  // All compiler-visible global loads must be complete before the DMA wait
-  // accounting starts.
+  // All compiler-visible global loads (and the first stages' DMA) complete
+  // here: from now on wave 0's vmcnt counts DMA only.
   __builtin_amdgcn_s_waitcnt(0x0F70);
-  if (wave == 0) {
-#pragma unroll
-    for (int s = 0; s < kRing - 1; ++s) issue(s);
-  }
 
   // Digit counts of the previous half-stage's scores, issued under the next
   // half-stage's MFMAs (lane bit j of pend_ok: query j's score counts).
@@ -384,9 +396,8 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
   uint32_t pend_ok = 0;
   auto count_pending = [&](int j) {
     if constexpr (kCount) {
-      const uint32_t d = score_digit(pend_v[j]);
-      const uint32_t inc = ((pend_ok >> j) & 1u) << ((d >> 10) << 4);
-      atomicAdd(&bins[(kQueriesPerWave * wave + j) * (kDigitBins / 2) + (d & 1023)], inc);
+      const uint32_t inc = ((pend_ok >> j) & 1u) << digit_half_shift(pend_v[j]);
+      atomicAdd(&bins[(kQueriesPerWave * wave + j) * (kDigitBins / 2) + digit_word(pend_v[j])], inc);
     }
   };
   for (int s = 0; s < stages; ++s) {
@@ -452,10 +463,19 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
         asm volatile("" : "+v"(p));
         part[j][u] = p;
       };
+      // The wave's priority falls as it moves through the stage (3 and 2 in
+      // the first pass, 1 and 0 in the second). Of the two waves on a SIMD the
+      // one behind then wins the issue arbitration, and both reach the
+      // barrier at about the same time; by age alone the older wave runs
+      // ahead and the younger one finishes the stage with the SIMD to itself.
+      if (hf == 0) __builtin_amdgcn_s_setprio(3); else __builtin_amdgcn_s_setprio(1);
       mfmas(0);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 1; i < kUnits; ++i) {
+        if (i == kUnits / 2) {
+          if (hf == 0) __builtin_amdgcn_s_setprio(2); else __builtin_amdgcn_s_setprio(0);
+        }
         mfmas(i);
         // b[u & 1] is free once the last query of group u has its MFMAs issued.
         const bool refill = i % kQueriesPerWave == kQueriesPerWave - 1 && i / kQueriesPerWave + 2 < 4;
@@ -481,6 +501,7 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
       epilogue(kUnits - 1);
 
       const int32_t key = (int32_t)(key0 + lane);
+      const bool full = key0 + kHalfKeys <= ke;  // no lane past the split's end
       const float ks = *(const float __attribute__((address_space(3)))*)(uintptr_t)(
           stage + kKBytes + 4 * (kHalfKeys * hf + lane));
 #pragma unroll
@@ -494,7 +515,7 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
         }
         if (wave == 0) {
           staged[s & 1][j][kHalfKeys * hf + lane] = v;
-        } else if (qw + j < rows && key < ke) {
+        } else if (qw + j < rows && (full || key < ke)) {
           out[(qw + j) * ldo + key] = v;
         }
       }
