@@ -378,3 +378,219 @@ extern "C" int dsa_layer_prologue_fp8(const void* q, int64_t q_rows, const float
   DSA_CHECK_LAUNCH("layer prologue");
   return kOk;
 }
+
+namespace dsa {
+namespace {
+
+// Indexer input producers: the indexer half of the reference's projection
+// step after its two GEMMs (models/deepseek_v32/projections.py:114-121,
+// 236-244; rotary.py:47-56). Index K rows get LayerNorm (fp32, rounded to
+// bf16), both index Q and index K rows get the non-interleaved RoPE on dims
+// [0, 64) (dim i pairs with dim i + 32; real = a cos - b sin, imag = b cos +
+// a sin, every product and sum rounded to fp32, the result to bf16), then the
+// A1 quantiser. Contraction into FMAs is off in these functions so that each
+// operation rounds as the reference's separate elementwise ops do.
+//
+// A row of 128 is held by 16 lanes, 8 consecutive values each (lane `part`:
+// dims 8 part .. 8 part + 7), as in quantize_rows_d128.
+
+__device__ __forceinline__ float round_bf16(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
+// Sum of a row in a fixed order: each lane's 8 values left to right, then
+// pairwise across the 16 lanes at distance 8, 4, 2, 1 (every lane ends with
+// the same bits).
+__device__ __forceinline__ float row_sum_d128(const float v[8]) {
+#pragma clang fp contract(off)
+  float s = v[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) s = s + v[i];
+#pragma unroll
+  for (int offset = 8; offset > 0; offset >>= 1) s = s + __shfl_xor(s, offset, 16);
+  return s;
+}
+
+// LayerNorm over the row: mean and variance by row_sum_d128, rstd = 1 /
+// sqrt(var + eps) (correctly rounded), y = ((x - mean) rstd) w + b, then bf16.
+__device__ __forceinline__ void layer_norm_d128(float v[8], int part, const float* __restrict__ w,
+                                                const float* __restrict__ b, float eps) {
+#pragma clang fp contract(off)
+  const float mean = row_sum_d128(v) * 0.0078125f;
+  float d[8], sq[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    d[i] = v[i] - mean;
+    sq[i] = d[i] * d[i];
+  }
+  const float var = row_sum_d128(sq) * 0.0078125f;
+  const float rstd = 1.0f / __builtin_sqrtf(var + eps);
+  const float4 w0 = *reinterpret_cast<const float4*>(w + 8 * part);
+  const float4 w1 = *reinterpret_cast<const float4*>(w + 8 * part + 4);
+  const float4 b0 = *reinterpret_cast<const float4*>(b + 8 * part);
+  const float4 b1 = *reinterpret_cast<const float4*>(b + 8 * part + 4);
+  const float ws[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+  const float bs[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = round_bf16((d[i] * rstd) * ws[i] + bs[i]);
+}
+
+// Non-interleaved RoPE on dims [0, 64): dim i < 32 (lanes 0-3) pairs with
+// dim i + 32 (lanes 4-7, same slot, lane part ^ 4). `trig`: the token's row
+// of the table, cos of the 32 angles then their sin (16-byte aligned).
+__device__ __forceinline__ void rope_d128(float v[8], int part, const float* __restrict__ trig) {
+#pragma clang fp contract(off)
+  float other[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) other[i] = __shfl_xor(v[i], 4, 16);
+  if (part < 8) {
+    const int d0 = 8 * (part & 3);
+    const float4 c0 = *reinterpret_cast<const float4*>(trig + d0);
+    const float4 c1 = *reinterpret_cast<const float4*>(trig + d0 + 4);
+    const float4 s0 = *reinterpret_cast<const float4*>(trig + 32 + d0);
+    const float4 s1 = *reinterpret_cast<const float4*>(trig + 36 + d0);
+    const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+    const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float x = v[i] * cs[i];
+      const float y = other[i] * sn[i];
+      v[i] = round_bf16(part < 4 ? x - y : x + y);
+    }
+  }
+}
+
+struct RopeTable {
+  const float* cos_sin;   // [table_rows, 64]
+  const int32_t* rows;    // table row of each token, or null: token t uses row t
+  int64_t table_rows;
+};
+
+// One block of 16 produced rows: load, [LayerNorm], RoPE, quantise (UE8M0),
+// store codes and scale; for index Q rows (fold_out set) the head weight
+// ((head * pre) * scale) * post. `rows_per_token` rows share a RoPE row.
+template <bool kLayerNorm>
+__device__ __forceinline__ QuantLane produce_rows_d128(
+    int64_t block, const uint16_t* __restrict__ x, int64_t rows, int64_t rows_per_token,
+    const RopeTable rope, const float* __restrict__ ln_w, const float* __restrict__ ln_b,
+    float eps, uint8_t* __restrict__ y, float* __restrict__ scales,
+    const float* __restrict__ head, float pre, float post, float* __restrict__ fold_out,
+    int32_t* __restrict__ status) {
+#pragma clang fp contract(off)
+  const int64_t row = (block * 256 + threadIdx.x) >> 4;
+  const int part = threadIdx.x & 15;
+  const bool live = row < rows;
+  uint4 raw = make_uint4(0, 0, 0, 0);
+  if (live) raw = *reinterpret_cast<const uint4*>(x + row * 128 + part * 8);
+  const uint32_t words[4] = {raw.x, raw.y, raw.z, raw.w};
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = bf16_to_f32(words[i] & 0xFFFFu);
+    v[2 * i + 1] = bf16_to_f32(words[i] >> 16);
+  }
+  if constexpr (kLayerNorm) layer_norm_d128(v, part, ln_w, ln_b, eps);
+  const int64_t token = (live ? row : 0) / rows_per_token;
+  int64_t trow = rope.rows ? (int64_t)rope.rows[token] : token;
+  if (trow < 0 || trow >= rope.table_rows) {
+    if (live && part == 0 && status) atomicOr(status, 2);
+    trow = 0;
+  }
+  rope_d128(v, part, rope.cos_sin + trow * 64);
+
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t a = __float_as_uint(v[i]) & 0x7FFFFFFFu;
+    m = m > a ? m : a;
+  }
+  m = max_abs_bits_reduce<16>(m);
+  if (!live) return QuantLane{0, 0, 0.0f};
+  const float scale = scale_from_amax_bits(m, true);
+  const float inverse = 1.0f / scale;
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) lo |= quantize_one(v[i], scale, inverse, true) << (8 * i);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) hi |= quantize_one(v[4 + i], scale, inverse, true) << (8 * i);
+  *reinterpret_cast<uint2*>(y + row * 128 + part * 8) = make_uint2(lo, hi);
+  float fold = 0.0f;
+  if (fold_out) fold = ((head[row] * pre) * scale) * post;
+  if (part == 0) {
+    scales[row] = scale;
+    if (fold_out) fold_out[row] = fold;
+  }
+  return QuantLane{lo, hi, fold};
+}
+
+// Blocks [0, nq): index Q rows (RoPE, quantise, weight fold, partial folded
+// queries); [nq, nq + nk): index K rows (LayerNorm, RoPE, quantise into the
+// resident cache); the rest: new KV tokens into the fp8 paged cache.
+__global__ __launch_bounds__(256) void index_producer(
+    const uint16_t* __restrict__ q, int64_t q_rows, const float* __restrict__ head, float pre,
+    float post, uint8_t* __restrict__ q_codes, float* __restrict__ q_scales,
+    float* __restrict__ w_folded, float* __restrict__ q_fold, const uint16_t* __restrict__ k,
+    int64_t k_rows, const float* __restrict__ ln_w, const float* __restrict__ ln_b, float eps,
+    uint8_t* __restrict__ k_codes, float* __restrict__ k_scales, const RopeTable rope,
+    const uint16_t* __restrict__ kv, int64_t token_offset, const int32_t* __restrict__ page_table,
+    int64_t pages, uint8_t* __restrict__ cache, int32_t* __restrict__ status, int64_t nq,
+    int64_t nk) {
+  const int64_t b = blockIdx.x;
+  if (b < nq) {
+    const QuantLane mine = produce_rows_d128<false>(b, q, q_rows, 64, rope, nullptr, nullptr, 0.0f,
+                                                    q_codes, q_scales, head, pre, post, w_folded,
+                                                    status);
+    if (q_fold) fold_partial(b, mine, q_fold);
+  } else if (b < nq + nk) {
+    produce_rows_d128<true>(b - nq, k, k_rows, 1, rope, ln_w, ln_b, eps, k_codes, k_scales,
+                            nullptr, 0.0f, 0.0f, nullptr, status);
+  } else {
+    pack_tokens(b - nq - nk, kv, k_rows, token_offset, page_table, pages, cache, status);
+  }
+}
+
+}  // namespace
+}  // namespace dsa
+
+extern "C" int dsa_index_producer_fp8(
+    const void* q_proj, int64_t tokens, const float* head_logits, float head_pre_scale,
+    float head_post_scale, const void* k_proj, const float* norm_weight, const float* norm_bias,
+    float norm_eps, const float* cos_sin, int64_t table_rows, const int32_t* rope_rows,
+    void* q_codes, float* q_scales, float* weights_out, float* q_fold, void* k_codes,
+    float* k_scales, const void* kv, int64_t token_offset, const int32_t* page_table,
+    int64_t pages, void* cache, int32_t* status, hipStream_t stream) {
+  using namespace dsa;
+  DSA_CHECK_ARG(tokens >= 0 && table_rows >= 0 && token_offset >= 0 && pages >= 0,
+                "invalid producer shape");
+  if (tokens == 0) return kOk;
+  DSA_CHECK_ARG(tokens < (int64_t)1 << 24, "too many tokens for one producer launch");
+  DSA_CHECK_ARG(q_proj && head_logits && k_proj && norm_weight && norm_bias && cos_sin &&
+                    q_codes && q_scales && weights_out && k_codes && k_scales,
+                "null pointer");
+  DSA_CHECK_ARG(table_rows >= 1 && (rope_rows != nullptr || table_rows >= tokens),
+                "the RoPE table must hold a row per token");
+  DSA_CHECK_ARG(__builtin_isfinite(norm_eps) && norm_eps >= 0.0f, "norm eps must be finite and >= 0");
+  const auto aligned = [](const void* p, uintptr_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; };
+  DSA_CHECK_ARG(aligned(q_proj, 16) && aligned(k_proj, 16) && aligned(cos_sin, 16) &&
+                    aligned(norm_weight, 16) && aligned(norm_bias, 16) && aligned(q_codes, 8) &&
+                    aligned(k_codes, 8) && (q_fold == nullptr || aligned(q_fold, 4)),
+                "producer inputs, the RoPE table and norm parameters must be 16-byte aligned, "
+                "codes 8-byte aligned");
+  const bool pack = kv != nullptr;
+  if (pack) {
+    DSA_CHECK_ARG(page_table && cache, "null page table or cache");
+    DSA_CHECK_ARG(token_offset + tokens <= pages * 64, "tokens exceed the paged cache");
+    DSA_CHECK_ARG(aligned(kv, 16) && aligned(cache, 16), "kv and cache must be 16-byte aligned");
+  }
+  const int64_t nq = (tokens * 64 * 16 + 255) / 256;
+  const int64_t nk = (tokens * 16 + 255) / 256;
+  const int64_t nt = pack ? (tokens + 3) / 4 : 0;
+  const RopeTable rope{cos_sin, rope_rows, table_rows};
+  hipLaunchKernelGGL(index_producer, dim3((unsigned)(nq + nk + nt)), dim3(256), 0, stream,
+                     static_cast<const uint16_t*>(q_proj), tokens * 64, head_logits,
+                     head_pre_scale, head_post_scale, static_cast<uint8_t*>(q_codes), q_scales,
+                     weights_out, q_fold, static_cast<const uint16_t*>(k_proj), tokens,
+                     norm_weight, norm_bias, norm_eps, static_cast<uint8_t*>(k_codes), k_scales,
+                     rope, static_cast<const uint16_t*>(kv), token_offset, page_table, pages,
+                     static_cast<uint8_t*>(cache), status, nq, nk);
+  DSA_CHECK_LAUNCH("index producer");
+  return kOk;
+}

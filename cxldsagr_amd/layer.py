@@ -188,6 +188,36 @@ class DSALayer:
         self.written = end
         return out, selection
 
+    def forward_projected(self, projection, projected, q, kv):
+        """``forward`` from the indexer's GEMM outputs (``projections.IndexProjected``).
+
+        One producer launch (``projections.index_producer``: K LayerNorm,
+        both RoPEs, both quantisations, the weight fold, the index-cache write
+        and, for the fp8 paged cache, the new KV records) takes the place of
+        the prologue; then the fused logits/top-k and sparse MLA as in
+        ``forward``. ``projection`` is the layer's ``IndexerProjection``.
+        """
+        position = self.written
+        rows = len(q)
+        end = position + rows
+        if (end > self.capacity or len(kv) != rows or projected.q_proj.shape[0] != rows
+                or projected.k_proj.shape[0] != rows):
+            raise ValueError("query batch exceeds the layer capacity or inputs disagree in length")
+        paged = self.kv_format == "fp8_paged"
+        q8, _, folded, _, _, q_fold = projection.produce(
+            projected, index_keys=self.index_keys[position:end],
+            index_scales=self.index_scales[position:end], q_fold=True,
+            kv=kv if paged else None, kv_cache=self.kv_cache, page_table=self.page_table,
+            token_offset=position)
+        if not paged:
+            self._append_kv(kv, position)
+        _, _, ids = indexer.logits_topk(q8, self.index_keys[:end], folded,
+                                        self.index_scales[:end], position, self.topk,
+                                        _q_fold=q_fold)
+        out = self._attend(q, ids, end)
+        self.written = end
+        return out, TokenSelection(ids)
+
 
 class OffloadDSALayer:
     """One layer of one session whose KV records live in a bounded HBM token pool.

@@ -240,6 +240,41 @@ int dsa_layer_prologue_fp8(const void* q, int64_t q_rows, const float* weights, 
                            int64_t pages, void* cache, int32_t* status, hipStream_t stream);
 
 /*
+ * Indexer input producers: the indexer half of the projection step after
+ * its GEMMs, in one launch. Replaces, in the reference's project()
+ * (models/deepseek_v32/projections.py:182-257), the K LayerNorm of
+ * _project_index_k (:114-121), apply_rope_pair(index_q, index_k, angles,
+ * interleaved=False) (:236-238; rotary.py:47-56,69-85), the two
+ * quantize_index calls (:239-240) and the weight scaling (:241-242), and
+ * the runner's index-cache write (models/deepseek_v32/attention.py:323-326).
+ *
+ * q_proj: bf16 [tokens, 64, 128] (index_wq output); k_proj: bf16
+ * [tokens, 128] (index_wk output); head_logits: f32 [tokens, 64]
+ * (weights_proj output); weights_out[t,h] = ((head_logits * pre) *
+ * q_scale) * post (the model's pre = 64^-1/2, post = 128^-1/2).
+ * K: y = LayerNorm(k_proj) with norm_weight/norm_bias f32 [128], norm_eps,
+ * rounded to bf16. Q and K: RoPE on dims [0, 64), dim i with dim i + 32,
+ * cos/sin from row rope_rows[t] (or t when rope_rows is NULL) of cos_sin
+ * f32 [table_rows, 64] (32 cos then 32 sin), rounded to bf16; then the A1
+ * quantiser with UE8M0 scales. Outputs: q_codes e4m3 [tokens, 64, 128],
+ * q_scales f32 [tokens, 64], weights_out f32 [tokens, 64], optional q_fold
+ * f32 [tokens, 4, 128] (as dsa_layer_prologue_fp8), k_codes e4m3
+ * [tokens, 128] and k_scales f32 [tokens] (the index cache rows). With kv
+ * non-NULL the new KV tokens bf16 [tokens, 576] are also packed into the fp8
+ * paged cache at token_offset (as dsa_kv_pack_fp8). status (optional,
+ * int32): bit 0 a page outside the cache, bit 1 a RoPE row outside the
+ * table (row 0 used instead).
+ */
+int dsa_index_producer_fp8(const void* q_proj, int64_t tokens, const float* head_logits,
+                           float head_pre_scale, float head_post_scale, const void* k_proj,
+                           const float* norm_weight, const float* norm_bias, float norm_eps,
+                           const float* cos_sin, int64_t table_rows, const int32_t* rope_rows,
+                           void* q_codes, float* q_scales, float* weights_out, float* q_fold,
+                           void* k_codes, float* k_scales, const void* kv, int64_t token_offset,
+                           const int32_t* page_table, int64_t pages, void* cache,
+                           int32_t* status, hipStream_t stream);
+
+/*
  * A7 - sparse MLA over flat bf16 records. Replaces sparse_mla /
  * sparse_mla_from_pool (FlashMLA flash_mla_sparse_fwd),
  * operators/deepseek_v32/attention/device_only/mla.py:90-115 and
