@@ -434,3 +434,52 @@ extern "C" int dsa_pool_recall_pipelined(
                           history_capacity, union_checked, stats, status, physical, keep_floor,
                           candidate_offset, stream, gather_stream ? gather_stream : stream);
 }
+
+namespace dsa {
+namespace {
+
+// Release of a session's host rows from one layer's pool maps
+// (cache/sparse_token_pool.py:697-710, release_ids): every host row of the
+// session's pages that is resident frees its slot (d2h = MISSING, priority
+// -1) and becomes MISSING in h2d. h2d and d2h are inverse on live entries, so
+// no two threads touch the same slot.
+__global__ void release_rows(const int32_t* __restrict__ page_table, int64_t pages,
+                             int64_t host_rows, int32_t* __restrict__ h2d,
+                             int64_t* __restrict__ d2h, int64_t* __restrict__ priority,
+                             int64_t slots, int32_t* __restrict__ status) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= pages * kPage) return;
+  const int64_t page = page_table[t / kPage];
+  const int64_t row = page * kPage + t % kPage;
+  if (page < 0 || row >= host_rows) {
+    if (status) atomicOr(status, 1);
+    return;
+  }
+  const int32_t slot = h2d[row];
+  if (slot == kMissing) return;
+  if (slot >= 1 && slot <= slots) {
+    d2h[slot] = kMissing;
+    priority[slot] = -1;
+  } else if (status) {
+    atomicOr(status, 1);
+  }
+  h2d[row] = kMissing;
+}
+
+}  // namespace
+}  // namespace dsa
+
+extern "C" int dsa_pool_release_rows(const int32_t* page_table, int64_t pages, int64_t host_rows,
+                                     int32_t* h2d, int64_t* d2h, int64_t* priority,
+                                     int64_t slots, int32_t* status, hipStream_t stream) {
+  using namespace dsa;
+  DSA_CHECK_ARG(pages >= 0 && host_rows >= 0 && slots >= 1, "invalid release shape");
+  if (pages == 0) return kOk;
+  DSA_CHECK_ARG(pages * kPage < ((int64_t)1 << 40), "too many pages");
+  DSA_CHECK_ARG(page_table && h2d && d2h && priority, "null pointer");
+  const int64_t n = pages * kPage;
+  hipLaunchKernelGGL(release_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                     page_table, pages, host_rows, h2d, d2h, priority, slots, status);
+  DSA_CHECK_LAUNCH("pool release");
+  return kOk;
+}

@@ -282,7 +282,7 @@ class OffloadDSALayer:
             self.pool.write_candidates(kv)
             out = self.consume(q, ids, written=end, transient_start=position)
         else:
-            self.pool.write_history(self.session, kv)
+            self.pool.append_records(self.session, kv)
             out = self.consume(q, ids, written=end)
         return out, TokenSelection(ids)
 

@@ -41,6 +41,7 @@ class Session:
         self.capacity = len(pages) * PAGE_SIZE
         self.page_table = torch.tensor(pages, dtype=torch.int32, device=pool.device)
         self.written = 0
+        self.released = False
 
     def global_rows(self, start, stop):
         t = torch.arange(start, stop, dtype=torch.int64)
@@ -87,30 +88,77 @@ class TokenPool:
 
     # ------------------------------------------------------------- sessions
     def allocate_session(self, capacity):
+        if type(capacity) is not int or capacity < 1:
+            raise ValueError("capacity must be a positive integer")
         pages = (capacity + PAGE_SIZE - 1) // PAGE_SIZE
         if pages > len(self._free_pages):
             raise ValueError("host arena has too few free pages for this session")
         return Session(self, [self._free_pages.pop() for _ in range(pages)])
 
-    def write_history(self, session, kv_bf16, *, pack_buffer=None):
-        """Append bf16 ``[T, 576]`` history records to the session's host pages.
+    def write_history(self, session, kv_bf16):
+        """Append bf16 ``[T, 576]`` history records to the session's host pages
+        and wait for them (``append_records`` followed by a synchronisation
+        of the current stream: a setup path, after which the host arena may be
+        read on the CPU)."""
+        start = self.append_records(session, kv_bf16)
+        torch.cuda.current_stream(self.device).synchronize()
+        return start
 
-        The records are quantised to the 656-byte fp8 format on the GPU, then
-        copied device-to-host into the pinned arena (a setup path, not the
-        per-layer hot path).
+    def append_records(self, session, kv_bf16):
+        """Persistent append with write-back: bf16 ``[T, 576]`` records are
+        quantised into the 656-byte format and stored straight into the
+        session's pinned host pages by the pack kernel (zero-copy over PCIe,
+        on the current stream, no staging buffer and no host
+        synchronisation). The role of the reference's D2H write-back of
+        appended KV (``cache/sparse_token_pool.py:468-510``, a copy-stream
+        ``write_host`` that readers wait for): here the write is ordered on
+        the stream before any later recall that reads those rows. CPU reads of
+        ``host`` must synchronise first. Returns the first appended position.
         """
+        self._check_live(session)
         start, stop = session.written, session.written + len(kv_bf16)
         if stop > session.capacity or stop > self.history_capacity:
             raise ValueError("history exceeds the session capacity")
-        pages = (len(kv_bf16) + PAGE_SIZE - 1) // PAGE_SIZE
-        staging = torch.zeros((pages, PAGE_SIZE, RECORD_BYTES), dtype=torch.uint8,
-                              device=self.device)
-        table = torch.arange(pages, dtype=torch.int32, device=self.device)
-        attention.pack_kv_fp8(kv_bf16, staging, table)
-        flat = staging.view(-1, RECORD_BYTES)[: len(kv_bf16)].cpu()
-        self.host[session.global_rows(start, stop)] = flat
+        if (kv_bf16.dtype != torch.bfloat16 or kv_bf16.ndim != 2
+                or kv_bf16.shape[1] != attention.QK_DIM or kv_bf16.device != self.device):
+            raise ValueError(f"kv must be BF16 [T, {attention.QK_DIM}] on {self.device}")
+        if len(kv_bf16):
+            kv = kv_bf16.contiguous()
+            if kv.data_ptr() % 16:
+                kv = kv.clone()
+            with torch.cuda.device(self.device):
+                _native.call("dsa_kv_pack_fp8", _native.ptr(kv), len(kv), start,
+                             _native.ptr(session.page_table), self.host_capacity // PAGE_SIZE,
+                             _native.ptr(self.host), _native.ptr(self.status),
+                             _native.stream_of(self.device))
         session.written = stop
         return start
+
+    def release_session(self, session):
+        """Return a session's host pages to the arena and drop its rows from
+        the pool (``SharedSparseTokenPool.release_session`` /
+        ``release_ids``, ``cache/sparse_token_pool.py:697-780``): every
+        resident row frees its slot, so a later owner of the pages never sees
+        stale residency. Synchronises the current stream (the pool must be
+        quiescent, as in the reference)."""
+        self._check_live(session)
+        with torch.cuda.device(self.device):
+            _native.call("dsa_pool_release_rows", _native.ptr(session.page_table),
+                         len(session.host_pages), self.host_capacity, _native.ptr(self.h2d),
+                         _native.ptr(self.d2h), _native.ptr(self.priority), self.slots,
+                         _native.ptr(self.status), _native.stream_of(self.device))
+            torch.cuda.current_stream(self.device).synchronize()
+        self._free_pages.extend(reversed(session.host_pages))
+        session.released = True
+        session.written = 0
+
+    @property
+    def free_host_pages(self):
+        return len(self._free_pages)
+
+    def _check_live(self, session):
+        if session.pool is not self or session.released:
+            raise ValueError("session is released or belongs to another pool")
 
     def write_candidates(self, kv_bf16, offset=0):
         """Quantise transient candidate records into rows ``slots + 1 + offset ...``."""
@@ -144,6 +192,7 @@ class TokenPool:
         """
         if indices.dtype != torch.int32 or indices.device != self.device:
             raise ValueError("indices must be int32 tensors on the pool device")
+        self._check_live(session)
         written = session.written if written is None else written
         history = written if transient_start is None else transient_start
         if history > session.written:

@@ -22,12 +22,18 @@ gather ``records[chosen] = host[missing]`` (``sparse_token_cache.py:541-542``):
 6. physical ids: ``h2d`` of each history id, ``slots + 1 + id -
    transient_start`` for candidate ids, ``-1`` for padding.
 
+``release_ids`` restates the pool's release of a session's host rows
+(``cache/sparse_token_pool.py:697-710``): resident rows free their slots
+(``d2h`` MISSING, priority -1) and become MISSING in ``h2d``.
+
 Pinned by ``tests/test_oracle_recall.py``: the reference's recall known
 answer (``cache/tests/test_sparse_token_cache.py:9-36``), its map invariants
 (``cache/tests/test_sparse_token_pool.py:32-44``) and its independent
 free-first/minimum-priority victim-legality check
 (``cache/tests/test_sparse_recall_metadata.py:117-135``) over seeded random
-selection sequences.
+selection sequences; ``release_ids`` by the same map invariants after
+releases, by releasing rows that are not resident (no change) and by a
+recall after a release, which must fetch every released row again.
 """
 
 import numpy as np
@@ -136,3 +142,13 @@ def check_maps(pool):
     assert (pool.priority[1:][free] == -1).all()
     assert (pool.priority[live] < pool.clock).all()
     assert np.array_equal(pool.records[live], pool.host[pool.d2h[live]])
+
+
+def release_ids(pool, global_ids):
+    """Free the slots of resident host rows ``global_ids`` and unmap them."""
+    global_ids = np.asarray(global_ids, np.int64)
+    physical = pool.h2d[global_ids]
+    physical = physical[physical != MISSING]
+    pool.h2d[global_ids] = MISSING
+    pool.d2h[physical] = MISSING
+    pool.priority[physical] = -1

@@ -84,3 +84,42 @@ def test_transient_candidates_map_to_tail_rows():
     physical = recall.ensure(pool, sel, table, written=104, transient_start=100)
     assert physical[0, 1:].tolist() == [17, 18, -1, 20]
     assert np.array_equal(pool.records[physical[0, 0]], pool.host[0])
+
+
+def test_release_ids_frees_slots_and_forces_a_fresh_recall():
+    """release_ids (cache/sparse_token_pool.py:697-710): the released rows
+    leave h2d and their slots become free (d2h MISSING, priority -1), the map
+    invariants hold, rows that were not resident change nothing, other
+    sessions' residency is kept, and a recall of the released rows fetches
+    every one of them again into free slots."""
+    rng = np.random.default_rng(7)
+    pool = _pool_with_history(4 * 64, 128, seed=7)
+    table_a, table_b = np.array([0, 1]), np.array([2, 3])
+    sel_a = rng.integers(0, 128, (2, 30))
+    sel_b = rng.integers(0, 128, (2, 30))
+    recall.ensure(pool, sel_a, table_a, written=128)
+    recall.ensure(pool, sel_b, table_b, written=128)
+    b_rows = recall.logical_to_global(table_b, np.unique(sel_b))
+    b_slots = pool.h2d[b_rows].copy()
+    a_rows = recall.logical_to_global(table_a, np.arange(128))
+    resident_a = a_rows[pool.h2d[a_rows] != recall.MISSING]
+    freed = pool.h2d[resident_a].copy()
+    assert resident_a.size == np.unique(sel_a).size
+
+    recall.release_ids(pool, a_rows)
+    assert (pool.h2d[a_rows] == recall.MISSING).all()
+    assert (pool.d2h[freed] == recall.MISSING).all() and (pool.priority[freed] == -1).all()
+    np.testing.assert_array_equal(pool.h2d[b_rows], b_slots)
+    recall.check_maps(pool)
+
+    snapshot = pool.copy()
+    recall.release_ids(pool, a_rows)   # nothing resident any more: no change
+    for name in ("h2d", "d2h", "priority"):
+        np.testing.assert_array_equal(getattr(pool, name), getattr(snapshot, name))
+
+    before = pool.recalled
+    recall.ensure(pool, sel_a, table_a, written=128)
+    assert pool.recalled - before == np.unique(sel_a).size
+    assert set(pool.h2d[resident_a].tolist()) <= set(freed.tolist()) | set(
+        np.nonzero(snapshot.d2h == recall.MISSING)[0].tolist())
+    recall.check_maps(pool)
