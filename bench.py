@@ -244,9 +244,37 @@ def main():
     _, ids = indexer.exact_topk(scores, topk)
     torch.cuda.synchronize()
 
+    # The same layer from the indexer's GEMM outputs: the producer launch (K
+    # LayerNorm, RoPE of Q and K, quantisation, weight fold, index-cache
+    # write, KV pack) in place of the prologue. GEMM outputs are stand-ins of
+    # the right shapes (the index Q/K of the workload, head logits from its
+    # weights) with a unit LayerNorm and the YaRN table of the positions.
+    from cxldsagr_amd import projections
+
+    projection = projections.IndexerProjection(
+        torch.zeros(64 * 128, 16, dtype=torch.bfloat16, device=device),
+        torch.zeros(128, 16, dtype=torch.bfloat16, device=device),
+        torch.zeros(64, 16, device=device), torch.ones(128, device=device),
+        torch.zeros(128, device=device), projections.rotary_frequencies().to(device))
+    positions = torch.arange(history, tokens, dtype=torch.float32, device=device)
+    projected = projections.IndexProjected(index_q, index_k_new, weights * 8.0,
+                                           projections.rotary_table(positions,
+                                                                    projection.frequencies))
+
+    def projected_step():
+        layer.written = history
+        return layer.forward_projected(projection, projected, mla_q, kv_new)
+
+    def producer_stage():
+        return projection.produce(projected, index_keys=layer.index_keys[history:tokens],
+                                  index_scales=layer.index_scales[history:tokens], q_fold=True,
+                                  kv=kv_new, kv_cache=layer.kv_cache, page_table=layer.page_table,
+                                  token_offset=history)
+
     # Isolated stages: the counted top-k consumes its counts, so the indexer
     # step is timed as the pair; the unfused logits and top-k beside it.
     stages = {
+        "index_producer": producer_stage,
         "quantize_q": lambda: indexer.quantize_index_folded(index_q, weights),
         "logits_topk": lambda: indexer.logits_topk(q8, keys, w_eff, kscale, history, topk),
         "logits_unfused": lambda: indexer.logits(q8, keys, w_eff, kscale, history,
@@ -278,6 +306,9 @@ def main():
     layer_us = event_time_us(torch, step, args.steps)
 
     isolated_us = {name: event_time_us(torch, fn, args.steps) for name, fn in stages.items()}
+    projected_layer_us = event_time_us(torch, projected_step, args.steps)
+    step()  # leave the layer as the plain step left it
+    torch.cuda.synchronize()
     in_layer = in_layer_stage_us(torch, layer, history, tokens, topk, args.steps,
                                  (index_q, index_k_new, weights, mla_q, kv_new))
     # Kernel figures are the launches inside the layer step (the clock of the
@@ -289,6 +320,8 @@ def main():
     mla_flop = 2 * queries * topk * 128 * (576 + 512)
     gather_bytes = queries * topk * 656
     topk_bytes = queries * scores.stride(0) * 4 + queries * topk * 8
+    producer_bytes = ((queries * 64 + queries) * (256 + 128 + 4 + 256) + queries * 64 * 8
+                      + queries * 4 * 128 * 4 + queries * (1152 + 656))
     kernels = {
         "logits": {
             "us": round(kernel_us["logits"], 2),
@@ -307,6 +340,15 @@ def main():
             "gather_frac_hbm": round(gather_bytes / kernel_us["sparse_mla"] / 1e3 / PEAKS["hbm_GBps"], 4),
         },
         "prologue": {"us": round(kernel_us["prologue"], 2)},
+        # Algorithmic bytes of the producer launch: per 128-value row 256 B in,
+        # 128 B codes + 4 B scale out, 256 B of its RoPE row; per Q row 4 B head
+        # logit in + 4 B weight out; the partial folded queries; per KV token
+        # 1152 B in + 656 B out.
+        "index_producer": {
+            "us": round(isolated_us["index_producer"], 2),
+            "GBps": round(producer_bytes / isolated_us["index_producer"] / 1e3, 1),
+            "bytes": producer_bytes,
+        },
         "isolated_us": {name: round(us, 2) for name, us in isolated_us.items()},
     }
     dominant = max(("logits", "topk", "sparse_mla"), key=lambda k: kernel_us[k])
@@ -353,6 +395,9 @@ def main():
         },
         "roofline": roofline,
         "kernels": kernels,
+        # The same layer from the indexer's GEMM outputs (producer launch in
+        # place of the prologue); not the headline value.
+        "layer_from_gemm_outputs_us": round(projected_layer_us, 2),
     }
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(inputs, args.cpu_rows, topk)
@@ -560,8 +605,72 @@ def bench_config3(args):
         else:
             entry["pcie_GBps_over_layer"] = round(fetch_bytes / (entry["layer_us"] * 1e3), 2)
         rounds.append(entry)
+    reference = pcie_reference(pool)
+    del step, layers, pool
+    torch.cuda.synchronize()
     print(json.dumps({"config": 3, "users": users, "history": history, "queries": queries,
-                      "pool_slots": slots, "rounds": rounds, "pcie_reference": pcie_reference(pool)}))
+                      "pool_slots": slots, "rounds": rounds, "pcie_reference": reference,
+                      "serving": bench_serving(args, users, history, queries, topk)}))
+
+
+def bench_serving(args, users, history, queries, topk):
+    """The GR serving runner (``cxldsagr_amd.serving``) on config 3's users: a
+    host arena for three quarters of them, so that the LRU evicts; two passes
+    over the users (the second revisits). Per request: admission, history
+    prefill on a miss (index K into the resident cache, fp8 records written
+    straight into pinned host pages), the transient candidate step with its
+    exact recall. Reports per-pass request latencies, hits and fetched bytes
+    (the second pass visits the users in reverse order)."""
+    import torch
+
+    from cxldsagr_amd.serving import GRServingRunner
+    from cxldsagr_amd.token_pool import TokenPool
+    from cxldsagr_amd.workloads import make_layer_inputs
+
+    device = torch.device("cuda", 0)
+    cached = max(1, users * 3 // 4)
+    pool = TokenPool(cached * history, users * history // 4, device=device,
+                     candidate_slots=queries, history_capacity=history)
+
+    # Each user's projected history, generated once on the device (outside
+    # the timed requests; a miss then writes it into the caches).
+    histories = []
+    for u in range(users):
+        x = make_layer_inputs(history, queries, seed=args.seed + u)
+        histories.append([(x.index_k[:history].to(device), x.kv[:history].to(device))])
+        del x
+
+    def history_of(u):
+        return lambda: histories[u]
+
+    passes = []
+    with GRServingRunner([pool], topk=topk) as runner:
+        for p in range(2):
+            metrics = []
+            # The second pass visits the users in reverse order, so the most
+            # recent ones hit before the evicted ones come back.
+            for u in (range(users) if p == 0 else reversed(range(users))):
+                fresh = make_layer_inputs(0, queries, seed=(p + 10) * 1000 + u)
+                batch = [tuple(getattr(fresh, k).to(device) for k in
+                               ("index_q", "index_k", "weights", "mla_q", "kv"))]
+                result = runner.execute({"user_id": u, "signature": ("history", u),
+                                         "history_tokens": history, "history": history_of(u),
+                                         "candidates": batch})
+                metrics.append(result.metrics)
+            hits = [m for m in metrics if m["prefix_cache_hit"]]
+            passes.append({
+                "pass": p + 1,
+                "requests": len(metrics),
+                "hits": len(hits),
+                "evictions": sum(len(m["evicted_users"]) for m in metrics),
+                "latency_ms_mean": round(sum(m["latency_ms"] for m in metrics) / len(metrics), 2),
+                "prefix_ms_mean_on_miss": round(
+                    sum(m["prefix_ms"] for m in metrics if not m["prefix_cache_hit"])
+                    / max(1, len(metrics) - len(hits)), 2),
+                "extend_ms_mean": round(sum(m["extend_ms"] for m in metrics) / len(metrics), 2),
+                "fetch_bytes": sum(m["fetch_bytes"] for m in metrics),
+            })
+    return {"arena_users": cached, "pool_slots": users * history // 4, "passes": passes}
 
 
 if __name__ == "__main__":
