@@ -193,3 +193,35 @@ def test_release_session_frees_slots_and_pages(gpu):
     torch.cuda.synchronize()
     got = pool.records.view(-1, 656)[physical[0].long()]
     assert torch.equal(got.cpu(), pool.host[fresh.global_rows(0, 64)])
+
+
+def test_failed_requests_discard_the_session_and_budget_errors_evict_nothing(gpu):
+    """A request that fails after admission releases its session (the
+    reference runner's discard, serving/persistent.py:218-226); a request
+    larger than the arena raises before evicting anyone."""
+    from cxldsagr_amd.serving import CacheBudgetExceeded, GRServingRunner
+    from cxldsagr_amd.token_pool import TokenPool
+
+    pools = [TokenPool(2 * HISTORY, SLOTS, device=gpu, candidate_slots=QUERIES,
+                       history_capacity=HISTORY + QUERIES) for _ in range(LAYERS)]
+    users = Users(gpu)
+    with GRServingRunner(pools, topk=TOPK) as runner:
+        runner.execute({"user_id": 0, "signature": "h0", "history_tokens": HISTORY,
+                        "history": users.history(0), "candidates": users.candidates(0, 0)})
+        free = [pool.free_host_pages for pool in pools]
+        # History of the wrong length: fails after admission, session discarded.
+        with pytest.raises(ValueError, match="history length"):
+            runner.execute({"user_id": 1, "signature": "h1", "history_tokens": HISTORY - 64,
+                            "history": users.history(1), "candidates": users.candidates(1, 0)})
+        assert runner.lru.keys() == [0]
+        assert [pool.free_host_pages for pool in pools] == free
+        # More than the whole arena: refused, user 0 stays cached.
+        with pytest.raises(CacheBudgetExceeded):
+            runner.execute({"user_id": 2, "signature": "h2", "history_tokens": 2 * HISTORY + 64,
+                            "history": users.history(2), "candidates": users.candidates(2, 0)})
+        assert runner.lru.keys() == [0]
+        result = runner.execute({"user_id": 0, "signature": "h0", "history_tokens": HISTORY,
+                                 "history": None, "candidates": users.candidates(0, 1)})
+        assert result.metrics["prefix_cache_hit"]
+        for pool in pools:
+            assert pool.check_status() == 0
