@@ -149,10 +149,13 @@ def index_producer(q_proj, k_proj, head_logits, norm_weight, norm_bias, eps, cos
             raise ValueError(f"kv must be BF16 ({tokens}, {QK_DIM}) on {device}")
         if (kv_cache is None or kv_cache.dtype != torch.uint8 or kv_cache.ndim != 3
                 or tuple(kv_cache.shape[1:]) != (PAGE_TOKENS, RECORD_BYTES)
-                or not kv_cache.is_contiguous() or page_table is None
-                or page_table.dtype != torch.int32 or page_table.device != device):
+                or not kv_cache.is_contiguous() or kv_cache.device != device
+                or page_table is None or page_table.dtype != torch.int32
+                or page_table.device != device or not page_table.is_contiguous()):
             raise ValueError("kv needs a contiguous uint8 [pages, 64, 656] cache and an int32 "
                              "page table")
+        if page_table.numel() * PAGE_TOKENS < token_offset + tokens:
+            raise ValueError("page_table does not cover the appended tokens")
         kv = _aligned(kv.contiguous())
         pages = kv_cache.shape[0]
     if tokens == 0:

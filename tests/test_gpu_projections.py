@@ -184,3 +184,40 @@ def test_layer_forward_projected_equals_forward(gpu, kv_format):
         assert torch.equal(a.kv_cache, b.kv_cache)
     assert torch.equal(sel_a.token_ids, sel_b.token_ids)
     assert torch.equal(out_a.view(torch.int16), out_b.view(torch.int16))
+
+
+def test_projection_gemms_then_producer(gpu):
+    """IndexerProjection.project (library GEMMs: index_wq on qr, index_wk on x,
+    weights_proj on x in fp32, and the RoPE table of the positions) then
+    produce: the producer's outputs equal the oracle applied to the GEMM
+    outputs project returned."""
+    from cxldsagr_amd.projections import IndexerProjection, rotary_frequencies
+
+    tokens, dim, q_lora = 48, 512, 256
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(tokens, dim, generator=g).bfloat16().to(gpu)
+    qr = torch.randn(tokens, q_lora, generator=g).bfloat16().to(gpu)
+    projection = IndexerProjection(
+        (torch.randn(64 * 128, q_lora, generator=g) / 16).bfloat16().to(gpu),
+        (torch.randn(128, dim, generator=g) / 16).bfloat16().to(gpu),
+        (torch.randn(64, dim, generator=g) / 16).to(gpu),
+        (1 + 0.1 * torch.randn(128, generator=g)).to(gpu), (0.1 * torch.randn(128, generator=g)).to(gpu),
+        rotary_frequencies().to(gpu))
+    positions = torch.arange(1000, 1000 + tokens, dtype=torch.float32, device=gpu)
+    projected = projection.project(x, qr, positions)
+    assert tuple(projected.q_proj.shape) == (tokens, 64, 128)
+    assert tuple(projected.k_proj.shape) == (tokens, 128)
+    assert projected.head_logits.dtype == torch.float32
+    got = projection.produce(projected)
+    torch.cuda.synchronize()
+    ref = oproj.index_producer(_bits(projected.q_proj.cpu()), _bits(projected.k_proj.cpu()),
+                               projection.norm_weight.cpu().numpy(),
+                               projection.norm_bias.cpu().numpy(), 1e-6,
+                               projected.cos_sin.cpu().numpy(), np.arange(tokens),
+                               projected.head_logits.cpu().numpy())
+    _check(got, ref)
+    # The GEMMs are the reference's: F.linear on the same operands.
+    expect_q = torch.nn.functional.linear(qr, projection.index_wq).view(tokens, 64, 128)
+    assert torch.equal(projected.q_proj, expect_q)
+    expect_w = torch.nn.functional.linear(x.float(), projection.weights_proj)
+    assert torch.equal(projected.head_logits, expect_w)
