@@ -45,7 +45,7 @@ def parse_args():
     p.add_argument("--cpu-rows", type=int, default=128,
                    help="query rows of the CPU baseline sample (scaled to all rows)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    p.add_argument("--only", choices=["layer", "logits", "topk", "mla"], default=None,
+    p.add_argument("--only", choices=["layer", "logits", "topk", "mla", "producer"], default=None,
                    help="time only one stage (for profiler runs)")
     p.add_argument("--copy-calibration-mib", type=int, default=0,
                    help="first run one plain device copy of this many MiB (scales PMC byte "
@@ -292,7 +292,7 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     if args.only is not None:
-        fn = step if args.only == "layer" else stages[{"mla": "sparse_mla", "topk": "logits_topk", "logits": "logits_unfused"}.get(args.only, args.only)]
+        fn = step if args.only == "layer" else stages[{"mla": "sparse_mla", "topk": "logits_topk", "logits": "logits_unfused", "producer": "index_producer"}.get(args.only, args.only)]
         for _ in range(args.warmup):
             fn()
         us = event_time_us(torch, fn, args.steps)
