@@ -1247,13 +1247,21 @@ __global__ __launch_bounds__(kThreads, 1) void topk_digit_finish(const float* __
       for (int j = 0; j < kSortPerThread; ++j)
         if (tid + j * kThreads < (int)n) fs.sorted[atomicAdd(&fs.cursor[bucket_of(key[j])], 1u)] = key[j];
       __syncthreads();
-      // Rank inside the bucket; bucket b spans [start[b], start[b - 1]).
+      // Rank inside the bucket; bucket b spans [start[b], start[b - 1]). A
+      // bucket that starts at or past `count` holds no output key: its keys
+      // (most of the threshold digit's, typically) are not ranked.
       for (uint32_t i = tid; i < n; i += kThreads) {
         const uint64_t k = fs.sorted[i];
         const uint32_t b = bucket_of(k);
         const uint32_t b0 = fs.start[b], b1 = b ? fs.start[b - 1] : n;
-        uint32_t rank = b0;
-        for (uint32_t j = b0; j < b1; ++j) rank += fs.sorted[j] > k ? 1u : 0u;
+        if (b0 >= (uint32_t)count) continue;
+        uint32_t rank = b0, j = b0;
+        for (; j + 4 <= b1; j += 4) {
+          const uint64_t x0 = fs.sorted[j], x1 = fs.sorted[j + 1];
+          const uint64_t x2 = fs.sorted[j + 2], x3 = fs.sorted[j + 3];
+          rank += (x0 > k ? 1u : 0u) + (x1 > k ? 1u : 0u) + (x2 > k ? 1u : 0u) + (x3 > k ? 1u : 0u);
+        }
+        for (; j < b1; ++j) rank += fs.sorted[j] > k ? 1u : 0u;
         if (rank < (uint32_t)count) fs.out[rank] = k;
       }
       __syncthreads();
