@@ -983,15 +983,16 @@ __device__ __forceinline__ uint32_t wave_prefix(uint32_t n, uint32_t* total) {
 typedef uint32_t v4u32 __attribute__((ext_vector_type(4)));
 
 struct SelectShared {
-  uint64_t staged[kThreads / 64][kWaveCap];
+  uint32_t staged[kThreads / 64][2][kWaveCap + 1];  // [wave][score bits, column code][slot]
   uint32_t wave_count[kThreads / 64];
   uint32_t digit, total, listed;
 };
 
 // Work-group (r, p) of a grid (rows, parts): reads part p of row r once and
 // lists its candidates - keys at or above the row's threshold digit - when
-// the row's candidates fit kListCap: each wave stages its own in LDS in
-// column order (positions from ballots, no atomics); one atomic on the row's
+// the row's candidates fit kListCap: each wave stages its own (score bits and
+// column code) in LDS in column order (positions from ballots, no atomics;
+// the radix keys are formed in the copy); one atomic on the row's
 // fill then places the part's candidates in the row's list, where the waves
 // copy them in whole lines. Part 0 also stores the row's threshold record.
 __global__ __launch_bounds__(kThreads, 1) void topk_digit_select(const float* __restrict__ scores,
@@ -1065,12 +1066,21 @@ __global__ __launch_bounds__(kThreads, 1) void topk_digit_select(const float* __
   const bool nonnegative = d0 >= 1024;
   const int32_t floor_bits = (int32_t)((d0 - 1024) << 21);
   const uint32_t not_col0 = ~(uint32_t)col0;
-  uint64_t* staged = ss.staged[wave];
+  uint32_t(*staged)[kWaveCap + 1] = ss.staged[wave];
+  const uint32_t col_base = not_col0 - 4u * (uint32_t)dt;  // not_col0 - column(e) = col_base - offset(e)
   uint32_t off = 0;  // wave-uniform
-  auto stage = [&](int e, uint32_t key, bool hit) {
+  // Staged entries hold the raw score bits; the copy below turns them into
+  // radix keys (a fraction of the elements reach it).
+  auto stage = [&](int e, bool hit) {
     const uint64_t m = __builtin_amdgcn_ballot_w64(hit);
-    const uint32_t pos = off + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
-    if (hit && pos < (uint32_t)kWaveCap) staged[pos] = ((uint64_t)key << 32) | (uint64_t)(not_col0 - column(e));
+    // Slot kWaveCap takes every entry past the wave's capacity (a part with
+    // such a wave is not listed).
+    const uint32_t pos = min(__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, off)),
+                             (uint32_t)kWaveCap);
+    if (hit) {
+      staged[0][pos] = bits[e];
+      staged[1][pos] = col_base - (4u * (uint32_t)(e >> 2) * kSelectDataThreads + (uint32_t)(e & 3));
+    }
     off += (uint32_t)__builtin_popcountll(m);
   };
   if (wave != 0) {  // wave 0 holds no keys
@@ -1079,12 +1089,11 @@ __global__ __launch_bounds__(kThreads, 1) void topk_digit_select(const float* __
       // part's end can never pass it.
 #pragma unroll
       for (int e = 0; e < 4 * kSelectVec; ++e)
-        stage(e, bits[e] | 0x80000000u, (int32_t)bits[e] >= floor_bits);
+        stage(e, (int32_t)bits[e] >= floor_bits);
     } else {
 #pragma unroll
       for (int e = 0; e < 4 * kSelectVec; ++e) {
-        const uint32_t key = radix_key(__uint_as_float(bits[e]));
-        stage(e, key, key >= floor_key && column(e) < n);
+        stage(e, radix_key(__uint_as_float(bits[e])) >= floor_key && column(e) < n);
       }
     }
   }
@@ -1107,7 +1116,9 @@ __global__ __launch_bounds__(kThreads, 1) void topk_digit_select(const float* __
   // count - must not place the list anywhere but inside it.)
   if (overflow || base > (uint32_t)kListCap || total > (uint32_t)kListCap - base) return;
   uint64_t* list = ws.lists + r * kListCap + base + before;
-  for (uint32_t i = lane; i < off; i += 64) list[i] = staged[i];
+  for (uint32_t i = lane; i < off; i += 64) {
+    list[i] = ((uint64_t)radix_key(__uint_as_float(staged[0][i])) << 32) | (uint64_t)staged[1][i];
+  }
 }
 
 // LDS of topk_digit_finish: its one-pass counting sort, or (fallback) the
