@@ -190,6 +190,35 @@ def test_digits_topk_bucket_beyond_the_lds_list(gpu):
     assert not counts.any()
 
 
+def test_digits_topk_wave_staging_overflow(gpu):
+    """Candidates concentrated in the columns one wave of the select launch
+    reads (2,304 of them, past the 1,024 a wave stages) while the row's
+    candidates still fit its list: the part is not listed and the finish
+    selects the row from its scores. At 65,664 columns the select launch has
+    two parts of 32,832 columns; wave 1 of a part reads its columns
+    3840 g + [0, 256), g = 0..8."""
+    rows, columns, k = 3, 65664, 2048
+    generator = torch.Generator(device="cuda").manual_seed(79)
+    scores = torch.randn(rows, columns, device=gpu, generator=generator)
+    local = torch.arange(columns, device=gpu) % 32832
+    wave1 = (local % 3840) < 256
+    assert int(wave1.sum()) == 2 * 2304
+    scores[0, wave1] = 5.0 + torch.arange(2 * 2304, device=gpu, dtype=torch.float32) * 1e-6
+    scores[1, wave1] = 5.0  # ties: the SMALL order decides
+    values, ids = _one_part_topk(scores, columns, k)
+    workspace, counts = _workspace(rows, columns, gpu)
+    expected = torch.from_numpy(otopk.digit_counts(scores.cpu().numpy()).astype(np.int32)).to(gpu)
+    for _ in range(2):
+        counts.copy_(expected)
+        got_values, got_ids = _digits_topk(scores, columns, k, workspace)
+        assert torch.equal(got_values.view(torch.int32), values.view(torch.int32))
+        assert torch.equal(got_ids, ids)
+        assert not counts.any()
+    ref_values, ref_ids = otopk.exact_topk(scores.cpu().numpy(), k)
+    np.testing.assert_array_equal(got_ids.cpu().numpy(), ref_ids)
+    np.testing.assert_array_equal(got_values.cpu().numpy().view(np.uint32), ref_values.view(np.uint32))
+
+
 @pytest.mark.parametrize(
     "rows,columns,query_start,topk,ragged",
     [(128, 65664, 65536, 2048, False), (5, 4099, 4094, 2048, False), (3, 1000, 997, 2048, False),
