@@ -205,6 +205,9 @@ def test_digits_topk_wave_staging_overflow(gpu):
     assert int(wave1.sum()) == 2 * 2304
     scores[0, wave1] = 5.0 + torch.arange(2 * 2304, device=gpu, dtype=torch.float32) * 1e-6
     scores[1, wave1] = 5.0  # ties: the SMALL order decides
+    # A negative threshold (the staging's general radix-key compare).
+    scores[2] = -scores[2].abs() - 2.0
+    scores[2, wave1] = -0.5 - torch.arange(2 * 2304, device=gpu, dtype=torch.float32) * 1e-6
     values, ids = _one_part_topk(scores, columns, k)
     workspace, counts = _workspace(rows, columns, gpu)
     expected = torch.from_numpy(otopk.digit_counts(scores.cpu().numpy()).astype(np.int32)).to(gpu)
