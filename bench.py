@@ -45,6 +45,8 @@ def parse_args():
     p.add_argument("--cpu-rows", type=int, default=128,
                    help="query rows of the CPU baseline sample (scaled to all rows)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-config4", action="store_true",
+                   help="skip the compact config-4 layer time of the default line")
     p.add_argument("--only", choices=["layer", "logits", "topk", "mla", "producer"], default=None,
                    help="time only one stage (for profiler runs)")
     p.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -85,12 +87,24 @@ def event_time_us(torch, fn, iters):
     return start.elapsed_time(stop) * 1e3 / iters
 
 
-def indexer_stage_calls(layer, tokens, topk, q8, folded, q_fold):
-    """The two launches of the layer's indexer step (``indexer.logits_topk``)
-    as separate calls: logits with their radix-digit counts, then the top-k
-    that starts from the counts. Returns (logits_fn, topk_fn, ids)."""
+def select_workspace(rows, tokens, device):
     import ctypes
 
+    import torch
+
+    from cxldsagr_amd import _native
+
+    needed = ctypes.c_int64()
+    _native.call("dsa_indexer_select_workspace_bytes", rows, tokens, 0, ctypes.byref(needed))
+    return torch.empty(needed.value, dtype=torch.uint8, device=device)
+
+
+def indexer_stage_calls(layer, tokens, topk, q8, folded, q_fold, workspace):
+    """The launches of the layer's indexer step (``indexer.select_topk``) as
+    separate calls: the per-row floors (in the layer prologue when it runs
+    fused, else their own launch), the logits kernel writing only the
+    candidates at or above them, and the top-k of the candidates. Returns
+    (floors_fn, logits_fn, topk_fn, ids)."""
     import torch
 
     from cxldsagr_amd import _native, indexer
@@ -98,57 +112,96 @@ def indexer_stage_calls(layer, tokens, topk, q8, folded, q_fold):
     device = q8.device
     rows, width = len(q8), indexer.padded_columns(tokens)
     scores = torch.empty(rows, width, device=device)
-    ids = torch.empty(rows, min(topk, tokens), dtype=torch.int32, device=device)
-    values = torch.empty(rows, min(topk, tokens), device=device)
-    needed = ctypes.c_int64()
-    _native.call("dsa_indexer_topk_workspace_bytes", rows, tokens, ctypes.byref(needed))
-    workspace = torch.zeros(needed.value, dtype=torch.uint8, device=device)
+    count = min(topk, tokens)
+    ids = torch.empty(rows, count, dtype=torch.int32, device=device)
+    values = torch.empty(rows, count, device=device)
     keys, kscale = layer.index_keys[:tokens], layer.index_scales[:tokens]
     history = tokens - rows
+    head = (_native.ptr(q8), _native.ptr(keys), _native.ptr(folded), _native.ptr(kscale), None,
+            None, history, rows, tokens)
+
+    def floors_fn():
+        _native.call("dsa_indexer_floors_fp8", *head, topk, _native.ptr(workspace),
+                     _native.stream_of(device))
 
     def logits_fn():
-        _native.call("dsa_indexer_logits_fp8_counted", _native.ptr(q8), _native.ptr(keys),
-                     _native.ptr(folded), _native.ptr(kscale), None, None, history, rows, tokens,
-                     width, _native.ptr(q_fold), _native.ptr(scores), _native.ptr(workspace),
+        _native.call("dsa_indexer_logits_fp8_emit", *head, width, _native.ptr(q_fold),
+                     _native.ptr(scores), 0, _native.ptr(workspace), workspace.numel(),
                      _native.stream_of(device))
 
     def topk_fn():
-        _native.call("dsa_topk_radix_digits", _native.ptr(scores), rows, tokens, width, topk,
-                     _native.ptr(values), _native.ptr(ids), ids.shape[1], _native.ptr(workspace),
+        _native.call("dsa_indexer_emit_topk", *head, _native.ptr(q_fold), _native.ptr(scores), topk,
+                     _native.ptr(values), _native.ptr(ids), count, 0, _native.ptr(workspace),
                      workspace.numel(), _native.stream_of(device))
 
-    return logits_fn, topk_fn, ids
+    return floors_fn, logits_fn, topk_fn, ids
+
+
+STAGES = ("prologue", "floors", "logits", "topk", "sparse_mla")
 
 
 def in_layer_stage_us(torch, layer, history, tokens, topk, iters, args):
     """Average duration of each stage of the layer step, from HIP events recorded
     between its launches on the current stream (the same launches, in the same
-    order, as DSALayer.forward with the fused prologue)."""
+    order, as DSALayer.forward; with the fused prologue the floors are part of
+    the prologue launch and the floors stage is empty). Also returns the
+    candidate keys the indexer step listed and the key splits that spilled."""
     index_q, index_k, weights, mla_q, kv = args
-    if not layer._fused_prologue_applies(index_q, index_k, weights, kv):
-        raise RuntimeError("bench expects the fused layer prologue")
-    names = ("prologue", "logits", "topk", "sparse_mla")
+    fused = layer._fused_prologue_applies(index_q, index_k, weights, kv)
     stream = torch.cuda.current_stream()
-    marks = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+    marks = [[torch.cuda.Event(enable_timing=True) for _ in range(len(STAGES) + 1)]
              for _ in range(iters)]
+    rows = len(index_q)
+    workspace = select_workspace(rows, tokens, layer.device)
+    floors = workspace[:4 * rows].view(torch.int32)
+
+    def prologue():
+        if fused:
+            return layer._prologue(index_q, index_k, weights, kv, history, floors)
+        from cxldsagr_amd import indexer
+
+        indexer.quantize_into(index_k, layer.index_keys[history:tokens],
+                              layer.index_scales[history:tokens])
+        q8, _, folded = indexer.quantize_index_folded(index_q, weights)
+        layer._append_kv(kv, history)
+        return q8, folded, None
+
     layer.written = history
-    q8, folded, q_fold = layer._prologue(index_q, index_k, weights, kv, history)
-    logits_fn, topk_fn, ids = indexer_stage_calls(layer, tokens, topk, q8, folded, q_fold)
+    q8, folded, q_fold = prologue()
+    floors_fn, logits_fn, topk_fn, ids = indexer_stage_calls(
+        layer, tokens, topk, q8, folded, q_fold, workspace)
     torch.cuda.synchronize()
     for ev in marks:
         layer.written = history
         ev[0].record(stream)
-        layer._prologue(index_q, index_k, weights, kv, history)
+        prologue()
         ev[1].record(stream)
-        logits_fn()
+        if not fused:
+            floors_fn()
         ev[2].record(stream)
-        topk_fn()
+        logits_fn()
         ev[3].record(stream)
-        layer._attend(mla_q, ids, tokens)
+        topk_fn()
         ev[4].record(stream)
+        layer._attend(mla_q, ids, tokens)
+        ev[5].record(stream)
     torch.cuda.synchronize()
-    return {name: sum(ev[i].elapsed_time(ev[i + 1]) for ev in marks) * 1e3 / iters
-            for i, name in enumerate(names)}
+    # Candidates listed per row (records [rows][splits][2] after the floors).
+    records_at = (4 * rows + 255) // 256 * 256
+    width = (tokens + 255) // 256 * 256
+    cus = torch.cuda.get_device_properties(layer.device).multi_processor_count
+    qgroups = (rows + 15) // 16
+    splits = max(1, (cus + qgroups - 1) // qgroups)
+    per = ((width + splits - 1) // splits + 127) // 128 * 128
+    splits = (width + per - 1) // per
+    splits = (splits + 7) // 8 * 8 if splits >= 8 else splits
+    rec = workspace[records_at:records_at + rows * splits * 8].view(torch.int32).view(rows, splits, 2)
+    live = [sp for sp in range(splits) if sp * per < tokens]
+    candidates = int(rec[:, live, 0].sum().item())
+    spilled = int((rec[:, live, 1] != 0x7FFFFFFF).sum().item())
+    times = {name: sum(ev[i].elapsed_time(ev[i + 1]) for ev in marks) * 1e3 / iters
+             for i, name in enumerate(STAGES)}
+    return times, candidates, spilled
 
 
 def cpu_baseline(inputs, rows_sample, topk):
@@ -271,12 +324,15 @@ def main():
                                   kv=kv_new, kv_cache=layer.kv_cache, page_table=layer.page_table,
                                   token_offset=history)
 
-    # Isolated stages: the counted top-k consumes its counts, so the indexer
-    # step is timed as the pair; the unfused logits and top-k beside it.
+    # Isolated stages: the layer's indexer step (floors, candidate logits,
+    # top-k of the candidates) as one call; the earlier fused step that writes
+    # every score and counts its digits, and the unfused logits and top-k,
+    # beside it.
     stages = {
         "index_producer": producer_stage,
         "quantize_q": lambda: indexer.quantize_index_folded(index_q, weights),
-        "logits_topk": lambda: indexer.logits_topk(q8, keys, w_eff, kscale, history, topk),
+        "select_topk": lambda: indexer.select_topk(q8, keys, w_eff, kscale, history, topk),
+        "logits_topk_counted": lambda: indexer.logits_topk(q8, keys, w_eff, kscale, history, topk),
         "logits_unfused": lambda: indexer.logits(q8, keys, w_eff, kscale, history,
                                                  _pad_to_stride=True),
         "topk_unfused": lambda: indexer.exact_topk(scores, topk),
@@ -292,7 +348,7 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     if args.only is not None:
-        fn = step if args.only == "layer" else stages[{"mla": "sparse_mla", "topk": "logits_topk", "logits": "logits_unfused", "producer": "index_producer"}.get(args.only, args.only)]
+        fn = step if args.only == "layer" else stages[{"mla": "sparse_mla", "topk": "select_topk", "logits": "logits_unfused", "producer": "index_producer"}.get(args.only, args.only)]
         for _ in range(args.warmup):
             fn()
         us = event_time_us(torch, fn, args.steps)
@@ -309,8 +365,9 @@ def main():
     projected_layer_us = event_time_us(torch, projected_step, args.steps)
     step()  # leave the layer as the plain step left it
     torch.cuda.synchronize()
-    in_layer = in_layer_stage_us(torch, layer, history, tokens, topk, args.steps,
-                                 (index_q, index_k_new, weights, mla_q, kv_new))
+    in_layer, candidates, spilled = in_layer_stage_us(
+        torch, layer, history, tokens, topk, args.steps,
+        (index_q, index_k_new, weights, mla_q, kv_new))
     # Kernel figures are the launches inside the layer step (the clock of the
     # timed region); the isolated stage loops are reported beside them.
     kernel_us = dict(isolated_us)
@@ -319,7 +376,9 @@ def main():
     logits_flop = 2 * 64 * 128 * pairs
     mla_flop = 2 * queries * topk * 128 * (576 + 512)
     gather_bytes = queries * topk * 656
-    topk_bytes = queries * scores.stride(0) * 4 + queries * topk * 8
+    # The top-k of the candidates reads the listed composite keys (8 B each)
+    # and writes 8 B per selected (value, id).
+    topk_bytes = candidates * 8 + queries * topk * 8
     producer_bytes = ((queries * 64 + queries) * (256 + 128 + 4 + 256) + queries * 64 * 8
                       + queries * 4 * 128 * 4 + queries * (1152 + 656))
     kernels = {
@@ -328,9 +387,13 @@ def main():
             "TFLOPs": round(logits_flop / kernel_us["logits"] / 1e6, 1),
             "frac_fp8_peak": round(logits_flop / kernel_us["logits"] / 1e6 / PEAKS["fp8_TFLOPs"], 4),
         },
+        # The per-row floors run inside the prologue launch in the layer step.
+        "floors": {"us": round(kernel_us["floors"], 2), "in_prologue": True},
         "topk": {
             "us": round(kernel_us["topk"], 2),
             "GBps": round(topk_bytes / kernel_us["topk"] / 1e3, 1),
+            "candidates": candidates,
+            "spilled_splits": spilled,
         },
         "sparse_mla": {
             "us": round(kernel_us["sparse_mla"], 2),
@@ -350,6 +413,11 @@ def main():
             "bytes": producer_bytes,
         },
         "isolated_us": {name: round(us, 2) for name, us in isolated_us.items()},
+        # The stage times come from HIP events recorded between the layer's
+        # launches (one marker per stage boundary, each adding ~2-3 us), so
+        # they sum above `value`, the plain step.
+        "stage_sum_us": round(sum(kernel_us[name] for name in STAGES), 2),
+        "stage_note": "in-layer stage times carry one event marker each; their sum exceeds value",
     }
     dominant = max(("logits", "topk", "sparse_mla"), key=lambda k: kernel_us[k])
     traffic = None
@@ -366,7 +434,7 @@ def main():
                     "peak": PEAKS["bf16_TFLOPs"], "unit": "TFLOP/s"}
     else:
         achieved = topk_bytes / kernel_us["topk"] / 1e3
-        roofline = {"kernel": "dsa_topk_radix_digits", "bound": "hbm", "achieved": achieved,
+        roofline = {"kernel": "dsa_indexer_emit_topk", "bound": "hbm", "achieved": achieved,
                     "peak": PEAKS["hbm_GBps"], "unit": "GB/s"}
     roofline["achieved"] = round(roofline["achieved"], 1)
     roofline["frac"] = round(achieved / roofline["peak"], 4)
@@ -399,6 +467,13 @@ def main():
         # place of the prologue); not the headline value.
         "layer_from_gemm_outputs_us": round(projected_layer_us, 2),
     }
+    del layer, scores
+    torch.cuda.empty_cache()
+    if not args.no_config4:
+        # BASELINE config 4's layer (131072 + 512, fp8 paged KV), measured the
+        # same way; the full config-4 report is `bench.py --config 4`.
+        result["config4_fp8_paged_us"] = config4_layer(torch, args, ("fp8_paged",))[
+            "formats"]["fp8_paged"]["layer_us"]
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(inputs, args.cpu_rows, topk)
     print(json.dumps(result))
@@ -408,12 +483,35 @@ def stage_times(torch, fns, steps):
     return {name: round(event_time_us(torch, fn, steps), 2) for name, fn in fns.items()}
 
 
-def bench_config4(args):
-    """Long-context stress (BASELINE config 4): 131072 history + 512 queries, 10 % heavy
-    hitters in 8 spans, the layer over the fp8 paged cache and over bf16 records."""
-    import torch
+def mla_reference_f32(torch, mla_q, kv, ids, rows, scale, value_dim=512):
+    """Plain fp32 torch sparse MLA of the given query rows over the original
+    bf16 KV records (the values the model meant): softmax over the selected
+    records (padding ids skipped), then P @ V. On the GPU, per row."""
+    out = []
+    kv32 = kv.float()
+    for r in rows:
+        sel = ids[r].long()
+        sel = sel[(sel >= 0) & (sel < kv.shape[0])]
+        records = kv32.index_select(0, sel)
+        logits = torch.matmul(mla_q[r].float(), records.t().contiguous()) * scale
+        p = torch.softmax(logits, dim=-1)
+        out.append(torch.matmul(p, records[:, :value_dim].contiguous()))
+    return torch.stack(out)
 
-    from cxldsagr_amd import indexer
+
+def accuracy(torch, got, want):
+    """Cosine, max-abs and relative RMS of got against want (fp32)."""
+    g, w = got.float().flatten(), want.float().flatten()
+    cos = torch.nn.functional.cosine_similarity(g, w, dim=0).item()
+    return {"cosine": round(cos, 7), "max_abs": round((g - w).abs().max().item(), 5),
+            "rel_rms": round(((g - w).norm() / w.norm()).item(), 6)}
+
+
+def config4_layer(torch, args, formats=("fp8_paged", "bf16")):
+    """Long-context stress (BASELINE config 4): 131072 history + 512 queries, 10 % heavy
+    hitters in 8 spans; the layer per KV format, its in-layer stage times (the launches
+    the layer runs) and its outputs at 16 spread query rows against an fp32 attention
+    over the original bf16 KV."""
     from cxldsagr_amd.layer import DSALayer
     from cxldsagr_amd.workloads import make_layer_inputs
 
@@ -422,13 +520,17 @@ def bench_config4(args):
     tokens = history + queries
     inputs = make_layer_inputs(history, queries, seed=args.seed, heavy_fraction=0.10, spans=8)
     result = {"config": 4, "history": history, "queries": queries, "topk": topk, "formats": {}}
-    for kv_format in ("fp8_paged", "bf16"):
+    sample_rows = [round(i * (queries - 1) / 15) for i in range(16)]
+    kv_all = inputs.kv.to(device)
+    mla_q = inputs.mla_q.to(device)
+    outputs, reference = {}, None
+    for kv_format in formats:
         layer = DSALayer(tokens, device=device, kv_format=kv_format,
                          page_table=inputs.page_table if kv_format == "fp8_paged" else None)
-        layer.write_history(inputs.index_k[:history].to(device), inputs.kv[:history].to(device))
+        layer.write_history(inputs.index_k[:history].to(device), kv_all[:history])
         index_q, weights = inputs.index_q.to(device), inputs.weights.to(device)
         index_k_new = inputs.index_k[history:].to(device).contiguous()
-        mla_q, kv_new = inputs.mla_q.to(device), inputs.kv[history:].to(device).contiguous()
+        kv_new = kv_all[history:].contiguous()
 
         def step():
             layer.written = history
@@ -439,30 +541,42 @@ def bench_config4(args):
         for _ in range(args.warmup):
             step()
         layer_us = event_time_us(torch, step, args.steps)
-        q8, _, w_eff = indexer.quantize_index_folded(index_q, weights)
-        keys, kscale = layer.index_keys[:tokens], layer.index_scales[:tokens]
-        scores = indexer.logits(q8, keys, w_eff, kscale, history, _pad_to_stride=True)
-        ids = selection.token_ids
-        fns = {
-            "logits": lambda: indexer.logits(q8, keys, w_eff, kscale, history, _pad_to_stride=True),
-            "topk": lambda: indexer.exact_topk(scores, topk),
-            "sparse_mla": lambda: layer.consume(mla_q, selection, kv_new, history),
-        }
-        times = stage_times(torch, fns, args.steps)
+        times, candidates, spilled = in_layer_stage_us(
+            torch, layer, history, tokens, topk, args.steps,
+            (index_q, index_k_new, weights, mla_q, kv_new))
         pairs = queries * history + queries * (queries + 1) // 2
         logits_flop = 2 * 64 * 128 * pairs
         mla_flop = 2 * queries * topk * 128 * (576 + 512)
         record = 656 if kv_format == "fp8_paged" else 1152
+        ids = selection.token_ids
+        if reference is None:
+            reference = mla_reference_f32(torch, mla_q, kv_all, ids, sample_rows, layer.scale)
+        outputs[kv_format] = (out[sample_rows].float(), ids)
         result["formats"][kv_format] = {
             "layer_us": round(layer_us, 2),
-            "stage_us": times,
+            "stage_us": {name: round(us, 2) for name, us in times.items()},
+            "stage_note": "in-layer stage times carry one event marker each",
+            "candidates": candidates,
+            "spilled_splits": spilled,
             "logits_frac_fp8_peak": round(logits_flop / times["logits"] / 1e6 / PEAKS["fp8_TFLOPs"], 4),
             "mla_frac_bf16_peak": round(mla_flop / times["sparse_mla"] / 1e6 / PEAKS["bf16_TFLOPs"], 4),
             "gather_GBps": round(queries * topk * record / times["sparse_mla"] / 1e3, 1),
+            "vs_fp32_over_bf16_kv": accuracy(torch, out[sample_rows], reference),
         }
-        del layer, scores, out
+        del layer, out
         torch.cuda.empty_cache()
-    print(json.dumps(result))
+    if len(outputs) == 2:
+        (a, ids_a), (b, ids_b) = outputs["fp8_paged"], outputs["bf16"]
+        result["fp8_vs_bf16"] = accuracy(torch, a, b)
+        result["fp8_vs_bf16"]["same_selection"] = bool(torch.equal(ids_a, ids_b))
+    result["accuracy_rows"] = sample_rows
+    return result
+
+
+def bench_config4(args):
+    import torch
+
+    print(json.dumps(config4_layer(torch, args)))
 
 
 def pcie_reference(pool, records=262144, reps=5, seed=11):

@@ -40,9 +40,21 @@ SIGNATURES = {
     "dsa_indexer_topk_workspace_bytes": [_i64, _i64, ctypes.POINTER(ctypes.c_int64)],
     "dsa_indexer_topk_fp8": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _ptr,
                              _ptr, _i64, _ptr, _ptr, _i64, _ptr, _i64, _ptr],
+    "dsa_indexer_select_workspace_bytes": [_i64, _i64, _i64, ctypes.POINTER(ctypes.c_int64)],
+    "dsa_indexer_floors_fp8": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _ptr,
+                               _ptr],
+    "dsa_indexer_logits_fp8_emit": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64,
+                                    _ptr, _ptr, _i64, _ptr, _i64, _ptr],
+    "dsa_indexer_emit_topk": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _ptr, _ptr,
+                              _i64, _ptr, _ptr, _i64, _i64, _ptr, _i64, _ptr],
+    "dsa_indexer_select_fp8": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _ptr, _ptr,
+                               _i64, _ptr, _ptr, _i64, _ptr, _i64, _ptr],
     "dsa_kv_pack_fp8": [_ptr, _i64, _i64, _ptr, _i64, _ptr, _ptr, _ptr],
     "dsa_layer_prologue_fp8": [_ptr, _i64, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _ptr, _ptr,
                                _ptr, _i64, _i64, _ptr, _i64, _ptr, _ptr, _ptr],
+    "dsa_layer_prologue_floors_fp8": [_ptr, _i64, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _ptr,
+                                      _ptr, _ptr, _i64, _i64, _ptr, _i64, _ptr, _ptr, _ptr, _ptr,
+                                      _i64, _i64, _ptr, _ptr],
     "dsa_index_producer_fp8": [_ptr, _i64, _ptr, _f32, _f32, _ptr, _ptr, _ptr, _f32, _ptr, _i64,
                                _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _ptr, _i64,
                                _ptr, _ptr, _ptr],
@@ -59,6 +71,7 @@ SIGNATURES = {
     "dsa_pool_recall_pipelined": [_ptr, _i64, _ptr, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr,
                                   _i64, _i64, _ptr, _ptr, _ptr, _i64, _i64, _ptr, _i64, _i64,
                                   _int, _ptr, _ptr, _ptr, _i64, _i64, _ptr, _ptr],
+    "dsa_pool_release_rows": [_ptr, _i64, _i64, _ptr, _ptr, _ptr, _i64, _ptr, _ptr],
 }
 
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}

@@ -46,6 +46,9 @@ FLAGS = [
 SOURCE_FLAGS = {
     "sparse_mla.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "logits.hip": ["-fno-honor-nans", "-mllvm", "-amdgpu-mfma-vgpr-form"],
+    # topk: the exact row recompute of the candidate top-k runs the logits
+    # arithmetic (logits_core.h) and must compile it as logits.hip does.
+    "topk.hip": ["-fno-honor-nans", "-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

@@ -42,6 +42,16 @@ void clear_error();
 
 int device_cu_count();
 
+// The exact top-k of the fused indexer step from the candidate lists that the
+// logits kernel's candidate mode leaves (topk.hip; launched by logits.hip).
+int topk_from_candidates(const uint8_t* q, const uint8_t* k, const float* weights,
+                         const float* kscale, const int32_t* starts, const int32_t* ends,
+                         int64_t query_start, const float* q_fold, float* scores, int64_t rows,
+                         int64_t columns, int64_t ld, int64_t topk, float* values,
+                         int32_t* indices, int64_t out_ld, const uint32_t* floors,
+                         const uint32_t* records, const uint64_t* lists, int64_t splits,
+                         int64_t per, int64_t cap, hipStream_t stream);
+
 // ------------------------------------------------------------ numerics --
 // fl32(1/448): the reciprocal the reference GPU path multiplies by.
 constexpr float kReciprocal448 = 1.0f / 448.0f;

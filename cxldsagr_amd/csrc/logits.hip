@@ -18,7 +18,9 @@
 //   four e4m3 digits (q' to ~2^-17 of its largest element). The four lane
 //   rows are then combined with a reduce-scatter on the gfx950 row-swap
 //   permutes (v_permlane32_swap, v_permlane16_swap) so lane l ends with key
-//   l of a 64-key pass: one coalesced 256-byte row store.
+//   l of a 64-key pass: one coalesced 256-byte row store. The arithmetic
+//   lives in logits_core.h, shared with the exact row recompute of the
+//   candidate top-k.
 // * The epilogue of one (query, 16-key) unit runs while the four MFMAs of the
 //   next unit execute (explicitly interleaved).
 // * Work-group: 8 waves (two per SIMD) x 2 queries = 16 queries; the key
@@ -36,23 +38,21 @@
 //   pending it no longer says which loads are done. Wave 0 issues every DMA
 //   (and waits on vmcnt for them) but stores nothing; its rows go through LDS
 //   to waves 1-7, which store their own rows and wave 0's in turn.
-#include <utility>
-
-#include "dsa_common.h"
+//
+// Three output modes of the one kernel: plain scores; scores plus their
+// radix-digit counts (the level-0 histogram of the top-k); or candidates
+// only (the fused indexer top-k): every score at or above its row's floor
+// is written as a composite top-k key into the row's list for the split, and
+// the score matrix is not written (see logits_fp8_mfma's kModeEmit notes).
+#include "logits_core.h"
 #include "../../include/dsa_gfx950.h"
 
 namespace dsa {
 namespace {
 
-typedef int v8i __attribute__((ext_vector_type(8)));
-typedef float v2f __attribute__((ext_vector_type(2)));
-typedef float v4f __attribute__((ext_vector_type(4)));
-typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+using namespace logits_core;
 
-constexpr int kHeads = 64;
-constexpr int kDim = 128;
 constexpr int kWaves = 8;
-constexpr int kQueriesPerWave = 2;
 constexpr int kQueriesPerBlock = kWaves * kQueriesPerWave;
 constexpr int kStageKeys = 128;                    // keys per DMA stage and barrier
 constexpr int kHalfKeys = 64;                      // keys per compute pass (lane = key)
@@ -62,7 +62,6 @@ constexpr int kKBytes = kStageKeys * kDim;         // 16 KB of keys per stage
 constexpr int kKLoads = kKBytes / (64 * 16);       // DMA instructions for the keys (wave 0)
 constexpr int kSLoads = kStageKeys / 64;           // DMA instructions for the key scales
 constexpr int kStageBytes = kKBytes + kStageKeys * 4;  // + the stage's key scales
-constexpr int kDigits = 4;                         // e4m3 digits of the folded query
 // Radix-digit counts for the top-k (optional output): per query row, the
 // number of its scores in [0, columns) by the top 11 bits of their radix key
 // (the top-k's level-0 digit). A work-group counts its rows in LDS as two
@@ -74,6 +73,20 @@ constexpr int kDigitBins = 2048;
 constexpr int kDigitShift = 21;
 constexpr int64_t kMaxSplitKeys = 65535 / kStageKeys * kStageKeys;
 constexpr uint32_t kNegInfDigit = 0x007FFFFFu >> kDigitShift;  // radix key of -inf, top 11 bits
+
+enum Mode : int { kModePlain = 0, kModeCount = 1, kModeEmit = 2 };
+
+// Candidate output of kModeEmit. Per (row, split): a list of `cap` composite
+// keys (radix(v) << 32 | ~column) and a record {listed, spill}: the keys
+// listed, and the first column from which the split's scores of that row
+// were stored in full into the score matrix instead (INT32_MAX: none).
+struct EmitArgs {
+  const uint32_t* floors;  // [rows] radix-key floor per row; 0: store the row in full
+  uint64_t* lists;         // [rows][splits][cap]
+  uint32_t* records;       // [rows][splits][2]
+  int32_t cap;
+  int32_t splits;
+};
 
 // The count word and half of a score's digit, d = radix(v) >> 21: for v >= 0
 // (sign clear) d = 1024 + bits 21-30 of v, for v < 0 d = 1023 - bits 21-30,
@@ -88,11 +101,27 @@ __device__ __forceinline__ uint32_t digit_half_shift(float v) {
   return (~__float_as_uint(v) >> 27) & 16u;  // 16 for the upper half
 }
 
-
-// f(integral_constant<int, I>) for every I of the sequence, in order.
-template <typename F, int... I>
-__device__ __forceinline__ void for_each_index(F&& f, std::integer_sequence<int, I...>) {
-  (f(std::integral_constant<int, I>{}), ...);
+// kModeEmit store of one row's 64 scores of a pass (lane = column key0 +
+// lane; wave-uniform state): scores at or above the floor go to the list
+// (positions from the ballot, no atomics); once fewer than 64 slots are
+// left, or from `spill` on, the scores are stored in full instead.
+__device__ __forceinline__ void emit_pass(float v, int32_t key0, int lane, uint32_t floor,
+                                          int32_t& listed, int32_t& spill, int32_t cap,
+                                          float* __restrict__ out_row,
+                                          uint64_t* __restrict__ list) {
+  if (key0 < spill && listed + kHalfKeys > cap) spill = key0;
+  if (key0 >= spill) {
+    out_row[key0 + lane] = v;
+    return;
+  }
+  const uint32_t key = radix_of(v);
+  const bool hit = key >= floor;
+  const uint64_t m = __builtin_amdgcn_ballot_w64(hit);
+  if (hit) {
+    const uint32_t pos = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+    list[listed + pos] = ((uint64_t)key << 32) | (uint64_t)(~(uint32_t)(key0 + lane));
+  }
+  listed += __builtin_popcountll(m);
 }
 
 __device__ __forceinline__ v4u lds_v4u(uint32_t addr) {
@@ -119,39 +148,30 @@ __device__ __forceinline__ void dma4_s(const void* base, uint32_t off, uint32_t 
                ::"s"(lds_base), "v"(off), "s"(base) : "memory", "m0");
 }
 
-// Sum of x over lanes l and l ^ 32 (first operand) and of y likewise, with
-// the results exchanged so that lanes 0-31 get x's sum and lanes 32-63 y's.
-__device__ __forceinline__ float fold32(float x, float y) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-// The same for lanes l and l ^ 16: rows 0 and 2 get x's sums, rows 1 and 3 y's.
-__device__ __forceinline__ float fold16(float x, float y) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(y), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-// part[u] holds the row-partial sums for key 16u + l % 16; returns the total
-// for key l of the stage.
-__device__ __forceinline__ float reduce_scatter4(const float part[4]) {
-  const float a0 = fold32(part[0], part[2]);  // rows 0-1: key group 0, rows 2-3: group 2
-  const float a1 = fold32(part[1], part[3]);  // rows 0-1: group 1, rows 2-3: group 3
-  return fold16(a0, a1);                      // row g: key group g
-}
-
-template <bool kCount>
+// kModeEmit: rows whose floor is 0 are stored in full (as kModePlain, with
+// the -inf tail); the others list only their scores at or above the floor,
+// per split into a list of `cap` keys, and switch to full stores (from a
+// 64-key pass on, recorded in the split's record) when fewer than 64 slots
+// are left. No digit counts, and no score of a listing row is stored before
+// its spill point.
+template <int kMode>
 __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
     const uint8_t* __restrict__ q, const uint8_t* __restrict__ k, const float* __restrict__ w,
     const float* __restrict__ kscale, const int32_t* __restrict__ starts,
     const int32_t* __restrict__ ends, int64_t query_start, int64_t rows, int64_t columns,
     int64_t ldo, int64_t keys_per_split, const float* __restrict__ q_fold, float* __restrict__ out,
-    uint32_t* __restrict__ digit_counts) {
+    uint32_t* __restrict__ digit_counts, EmitArgs emit) {
+  constexpr bool kCount = kMode == kModeCount;
+  constexpr bool kEmit = kMode == kModeEmit;
   __shared__ __align__(16) uint8_t ring[kRing][kStageBytes];
   // Packed 16-bit digit counts of the block's rows: digit d of row i is half
   // d >> 10 of word i * kDigitBins / 2 + (d & 1023).
   constexpr int kBinWords = kQueriesPerBlock * kDigitBins / 2;
   constexpr int kBinVecs = kBinWords / (4 * kThreads);  // 16-byte LDS accesses per thread
   __shared__ __align__(16) uint32_t bins[kCount ? kBinWords : 4];
+  // kModeEmit: wave 0's rows' {listed, spill}, kept by the waves that store
+  // those rows in turn.
+  __shared__ int32_t w0_state[kQueriesPerWave][2];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -236,15 +256,9 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
   int32_t qs[kQueriesPerWave], qe[kQueriesPerWave];
   const int64_t qw = q0 + wave * kQueriesPerWave;
 
-  // Linear half of the head sum: sum_h (w_h / 2) s_h = k . q' with
-  // q' = sum_h (w_h / 2) q_h, formed here in fp32 (lane 32j + c: query j,
-  // dims 4c .. 4c + 3) and written as kDigits e4m3 digits, digit d at scale
-  // 2^(E_j - 4d) (|q'| < 2^(E_j + 8)): each digit holds the residual of the
-  // ones before it to within half an e4m3 ulp, so the four carry q' to about
-  // 2^-17 of its largest element. In the MFMA operand, row 4d + j is digit d
-  // of query j (rows 4d + 2 and 4d + 3 are zero); its C row then sits in lane
-  // group d, register j, so the reduction over lane groups that sums head
-  // partials also sums the digits.
+  // Linear half of the head sum (query_digits): q' from four partial sums
+  // over heads 16g .. 16g + 15 - from the layer prologue (q_fold,
+  // [rows][4][128]) or formed here the same way (fold_partials).
   //
   // Load order: the inputs of q' and the head weights first, then the query
   // operands (the bulk of the bytes), so that forming q' waits only for its
@@ -252,15 +266,10 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
   __shared__ __align__(16) uint8_t digits[kWaves][kQueriesPerWave][kDigits][kDim];
   v8i qd;
   float fl[kQueriesPerWave];
-  static_assert(kQueriesPerWave == 2, "the fold maps 32 lanes x 4 dims to a query");
   const int fj = lane >> 5;
   const int fc = lane & 31;
   const bool flive = qw + fj < rows;
   const int64_t fqc = flive ? qw + fj : 0;
-  // q' in four partial sums over heads 16g .. 16g + 15 (each one fmaf chain
-  // from 0 in increasing head order), then 0.5 (((p0 + p1) + p2) + p3): the
-  // same bits whether the partials come from the layer prologue (q_fold,
-  // [rows][4][128]) or are formed here.
   float pg[4][4];
   uint32_t codes[kHeads];
   v4f w4;
@@ -296,92 +305,73 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
     qs[j] = live ? (starts ? starts[qc] : 0) : 0;
     qe[j] = live ? (int32_t)e : 0;
   }
+  // kModeEmit: the floors of this wave's rows and of wave 0's (stored by
+  // the other waves), and the list state of this wave's rows.
+  uint32_t floor_own[kQueriesPerWave] = {}, floor_w0[kQueriesPerWave] = {};
+  int32_t listed[kQueriesPerWave] = {}, spill[kQueriesPerWave] = {};
+  if constexpr (kEmit) {
+#pragma unroll
+    for (int j = 0; j < kQueriesPerWave; ++j) {
+      floor_own[j] = qw + j < rows ? emit.floors[qw + j] : 0u;
+      floor_w0[j] = q0 + j < rows ? emit.floors[q0 + j] : 0u;
+    }
+  }
 #pragma unroll
   for (int j = 0; j < kQueriesPerWave; ++j) {
     const int64_t qc = qw + j < rows ? qw + j : 0;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const v4u* src = reinterpret_cast<const v4u*>(q + ((qc * kHeads + 16 * t + col) * kDim + 32 * group));
-      const v4u lo = src[0], hi = src[1];
-      qa[j][t] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    for (int t = 0; t < 4; ++t) qa[j][t] = query_operand(q, qc, t, col, group);
+  }
+  if (!q_fold) fold_partials(codes, w4, flive, pg);
+  query_digits(pg, digits[wave], lane, qd, fl);
+  if constexpr (kEmit) {
+#pragma unroll
+    for (int j = 0; j < kQueriesPerWave; ++j) {
+      floor_own[j] = __builtin_amdgcn_readfirstlane(floor_own[j]);
+      floor_w0[j] = __builtin_amdgcn_readfirstlane(floor_w0[j]);
+      // A row without a floor is stored in full from its first column.
+      spill[j] = floor_own[j] == 0u ? 0 : 0x7FFFFFFF;
+    }
+    // Ordered before the first store of wave 0's rows by the first barrier.
+    if (wave == 1 && lane < kQueriesPerWave) {
+      w0_state[lane][0] = 0;
+      w0_state[lane][1] = floor_w0[lane] == 0u ? 0 : 0x7FFFFFFF;
     }
   }
-  {
-    const int j = fj;
-    const int c = fc;
-    if (!q_fold) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) pg[g][i] = 0.0f;
-      // Each head's weight broadcast along the 16-lane row by DPP
-      // (row_newbcast).
-      auto add_head = [&](auto head) {
-        constexpr int h = decltype(head)::value;
-        const float wb = __int_as_float(
-            __builtin_amdgcn_update_dpp(0, __float_as_int(w4[h & 3]), 0x150 + (h >> 2), 0xF, 0xF, false));
-        const float wh = flive ? wb : 0.0f;
-        const v2f x0 = __builtin_amdgcn_cvt_pk_f32_fp8(codes[h], false);
-        const v2f x1 = __builtin_amdgcn_cvt_pk_f32_fp8(codes[h], true);
-        float* p = pg[h >> 4];
-        p[0] = fmaf(wh, x0[0], p[0]);
-        p[1] = fmaf(wh, x0[1], p[1]);
-        p[2] = fmaf(wh, x1[0], p[2]);
-        p[3] = fmaf(wh, x1[1], p[3]);
-      };
-      for_each_index(add_head, std::make_integer_sequence<int, kHeads>{});
-    }
-    float qp[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) qp[i] = 0.5f * (((pg[0][i] + pg[1][i]) + pg[2][i]) + pg[3][i]);
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) amax = fmaxf(amax, fabsf(qp[i]));
-#pragma unroll
-    for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
-    int ex = 0;
-    (void)frexpf(amax, &ex);  // amax < 2^ex (ex = 0 for amax = 0)
-    const int e0 = ex - 8;
-#pragma unroll
-    for (int d = 0; d < kDigits; ++d) {
-      const int e = e0 - 4 * d;
-      uint32_t code = 0;
-      code = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(qp[0], -e), ldexpf(qp[1], -e), code, false);
-      code = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(qp[2], -e), ldexpf(qp[3], -e), code, true);
-      *reinterpret_cast<uint32_t*>(&digits[wave][j][d][4 * c]) = code;
-      const v2f y0 = __builtin_amdgcn_cvt_pk_f32_fp8(code, false);
-      const v2f y1 = __builtin_amdgcn_cvt_pk_f32_fp8(code, true);
-      qp[0] -= ldexpf(y0[0], e);
-      qp[1] -= ldexpf(y0[1], e);
-      qp[2] -= ldexpf(y1[0], e);
-      qp[3] -= ldexpf(y1[1], e);
-    }
-    // A operand: lane l holds row l % 16 = 4d + j', dims 32 (l / 16) .. + 31;
-    // rows j' >= 2 (no query) are zero.
-    const int jr = lane & 3, dr = (lane & 15) >> 2, blk = lane >> 4;
-    const bool jlive = jr < kQueriesPerWave;
-    const int jc = jlive ? jr : 0;
-    v4u lo = *reinterpret_cast<const v4u*>(&digits[wave][jc][dr][32 * blk]);
-    v4u hi = *reinterpret_cast<const v4u*>(&digits[wave][jc][dr][32 * blk + 16]);
-    if (!jlive) lo = hi = v4u{0u, 0u, 0u, 0u};
-    qd = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-    // C rows of lane group g = digit g: register r (query r) is scaled by
-    // 2^(E_r - 4g).
-#pragma unroll
-    for (int r = 0; r < kQueriesPerWave; ++r)
-      fl[r] = ldexpf(1.0f, __builtin_amdgcn_readlane(e0, 32 * r) - 4 * group);
-  }
+  auto list_of = [&](int64_t row) {
+    return emit.lists + (row * emit.splits + blockIdx.x) * (int64_t)emit.cap;
+  };
 
   // Wave 0's finished rows, [stage parity][query][key].
   __shared__ __align__(16) float staged[2][kQueriesPerWave][kStageKeys];
   auto store_staged = [&](int st) {
-#pragma unroll
-    for (int hf = 0; hf < kStageKeys / kHalfKeys; ++hf) {
-      const int64_t key = kb + (int64_t)st * kStageKeys + kHalfKeys * hf + lane;
+    if constexpr (kEmit) {
 #pragma unroll
       for (int j = 0; j < kQueriesPerWave; ++j) {
         const int64_t qi = q0 + j;  // wave 0's queries
-        if (qi < rows && key < ke) out[qi * ldo + key] = staged[st & 1][j][kHalfKeys * hf + lane];
+        if (qi >= rows) continue;
+        int32_t n = __builtin_amdgcn_readfirstlane(w0_state[j][0]);
+        int32_t sp = __builtin_amdgcn_readfirstlane(w0_state[j][1]);
+#pragma unroll
+        for (int hf = 0; hf < kStageKeys / kHalfKeys; ++hf) {
+          const int32_t key0 = (int32_t)(kb + (int64_t)st * kStageKeys + kHalfKeys * hf);
+          emit_pass(staged[st & 1][j][kHalfKeys * hf + lane], key0, lane, floor_w0[j], n, sp,
+                    emit.cap, out + qi * ldo, list_of(qi));
+        }
+        if (lane == 0) {
+          w0_state[j][0] = n;
+          w0_state[j][1] = sp;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int hf = 0; hf < kStageKeys / kHalfKeys; ++hf) {
+        const int64_t key = kb + (int64_t)st * kStageKeys + kHalfKeys * hf + lane;
+#pragma unroll
+        for (int j = 0; j < kQueriesPerWave; ++j) {
+          const int64_t qi = q0 + j;  // wave 0's queries
+          if (qi < rows && key < ke) out[qi * ldo + key] = staged[st & 1][j][kHalfKeys * hf + lane];
+        }
       }
     }
   };
@@ -447,17 +437,10 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
       };
       auto epilogue = [&](int i) {
         const int u = i / kQueriesPerWave, j = i % kQueriesPerWave;
-        // relu(s) w = (|s| + s) w / 2: the |s| half here, one FMA per head
-        // (wt holds w / 2) in one chain over the head tiles in order; the s
-        // half is the linear MFMA's share of this lane. (One chain: a wave's
+        // relu(s) w = (|s| + s) w / 2 (head_sum). One chain: a wave's
         // dependent FMAs issue back to back, and partial chains would cost
-        // three adds per unit.)
-        float p = fabsf(acc[i & 1][0][0]) * wt[j][0];
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-          for (int r = (t == 0 ? 1 : 0); r < 4; ++r) p = fmaf(fabsf(acc[i & 1][t][r]), wt[j][4 * t + r], p);
-        p = fmaf(acc_lin[u & 1][j], fl[j], p);
+        // three adds per unit.
+        float p = head_sum(acc[i & 1], acc_lin[u & 1][j], wt[j], fl[j]);
         // Pins the epilogue here: otherwise instruction selection sinks it below
         // every MFMA of the stage and all 64 results stay live.
         asm volatile("" : "+v"(p));
@@ -515,6 +498,12 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
         }
         if (wave == 0) {
           staged[s & 1][j][kHalfKeys * hf + lane] = v;
+        } else if constexpr (kEmit) {
+          // (Stages never reach past the split: its length is a multiple of
+          // the stage, and ldo of 256.)
+          if (qw + j < rows)
+            emit_pass(v, (int32_t)key0, lane, floor_own[j], listed[j], spill[j], emit.cap,
+                      out + (qw + j) * ldo, list_of(qw + j));
         } else if (qw + j < rows && (full || key < ke)) {
           out[(qw + j) * ldo + key] = v;
         }
@@ -530,13 +519,35 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
   // Drain the DMA issued past the last stage before exit.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  // Columns of this split at or beyond every causal end: -inf.
+  // Columns of this split at or beyond every causal end: -inf (kModeEmit:
+  // only rows stored in full).
   const int64_t tail = kb + (int64_t)stages * kStageKeys;
   if (tail < ke) {
     for (int i = wave; i < kQueriesPerBlock; i += kWaves) {
       const int64_t qi = q0 + i;
       if (qi >= rows) continue;
+      if constexpr (kEmit) {
+        if (emit.floors[qi] != 0u) continue;
+      }
       for (int64_t key = tail + lane; key < ke; key += 64) out[qi * ldo + key] = neg_inf;
+    }
+  }
+  if constexpr (kEmit) {
+    // Records: waves 1-7 their own rows; wave 0's rows by the wave that
+    // stored its last stage (wave 1 without stages).
+    const int w0_writer = stages > 0 ? 1 + (stages - 1) % (kWaves - 1) : 1;
+    if (wave != 0 && lane < kQueriesPerWave) {
+      const int64_t row = qw + lane;
+      if (row < rows) {
+        uint32_t* rec = emit.records + (row * emit.splits + blockIdx.x) * 2;
+        rec[0] = (uint32_t)(lane == 0 ? listed[0] : listed[1]);
+        rec[1] = (uint32_t)(lane == 0 ? spill[0] : spill[1]);
+      }
+    }
+    if (wave == w0_writer && lane < kQueriesPerWave && q0 + lane < rows) {
+      uint32_t* rec = emit.records + ((q0 + lane) * emit.splits + blockIdx.x) * 2;
+      rec[0] = (uint32_t)w0_state[lane][0];
+      rec[1] = (uint32_t)w0_state[lane][1];
     }
   }
   if constexpr (kCount) {
@@ -565,23 +576,135 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
   }
 }
 
+// ---- per-row floors of the candidate top-k (floor_rank, floor_of_samples in
+// logits_core.h): one work-group per row scores the row's sample columns
+// from the quantised queries and folded weights the logits kernel takes.
+constexpr int kFloorThreads = 512;
+constexpr int kFloorWaves = kFloorThreads / 64;
+constexpr int kFloorBatch = 8;  // 16-sample groups per wave whose loads are in flight together
+
+__global__ __launch_bounds__(kFloorThreads) void index_floors(
+    const uint8_t* __restrict__ q, const uint8_t* __restrict__ k, const float* __restrict__ w,
+    const float* __restrict__ kscale, const int32_t* __restrict__ starts,
+    const int32_t* __restrict__ ends, int64_t query_start, int64_t columns, int count,
+    uint32_t* __restrict__ floors) {
+  __shared__ uint32_t keys[kFloorMaxSamples];
+  __shared__ uint32_t hist[2048];
+  __shared__ uint32_t wave_sums[kFloorWaves];
+  __shared__ uint32_t result[2];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int group = lane >> 4;
+  const int col = lane & 15;
+  const int64_t s = starts ? (int64_t)starts[row] : 0;
+  int64_t e = ends ? (int64_t)ends[row] : query_start + row + 1;
+  if (e > columns) e = columns;
+  const int64_t visible = e > s ? e - s : 0;
+  if (visible < kFloorMinVisible) {
+    if (tid == 0) floors[row] = 0u;
+    return;
+  }
+  const int64_t n = floor_samples(visible, kFloorMaxSamples);
+  const int64_t stride = visible / n;  // >= 2
+  const uint32_t rank = floor_rank(n, count, visible);
+  if (rank > (uint32_t)n) {
+    if (tid == 0) floors[row] = 0u;
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) hist[4 * tid + j] = 0;
+  if (tid < 2) result[tid] = 0;
+  // Sample m is column s + m stride + stride / 2. Wave w scores the 16-sample
+  // groups w, w + waves, ... in batches of kFloorBatch whose key loads are
+  // issued together: four MFMAs (16 heads each) per group, then
+  // sum_h w_h max(s_h, 0) per lane and over the four lane rows.
+  const int groups = (int)(n / 16);
+  auto sample_key = [&](int g) { return s + (int64_t)(16 * g + col) * stride + stride / 2; };
+  v8i qa[4];
+  float wv[16];
+  for (int g0 = wave; g0 < groups; g0 += kFloorBatch * kFloorWaves) {
+    v8i b[kFloorBatch];
+    float ks[kFloorBatch];
+#pragma unroll
+    for (int i = 0; i < kFloorBatch; ++i) {
+      const int g = g0 + i * kFloorWaves;
+      const int64_t key = sample_key(g < groups ? g : 0);
+      b[i] = key_operand(k, key, group);
+      ks[i] = kscale[key];
+    }
+    if (g0 == wave) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        qa[t] = query_operand(q, row, t, col, group);
+        const v4f x = *reinterpret_cast<const v4f*>(w + row * kHeads + 16 * t + 4 * group);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) wv[4 * t + r] = x[r];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kFloorBatch; ++i) {
+      const int g = g0 + i * kFloorWaves;
+      float p = 0.0f;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const v4f acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+            qa[t], b[i], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) p = fmaf(wv[4 * t + r], fmaxf(acc[r], 0.0f), p);
+      }
+      p += __shfl_xor(p, 16);
+      p += __shfl_xor(p, 32);
+      if (group == 0 && g < groups) keys[16 * g + col] = radix_of(p * ks[i]);
+    }
+  }
+  __syncthreads();
+  const uint32_t floor = floor_of_samples<kFloorThreads>(keys, (int)n, rank, hist, wave_sums, result);
+  if (tid == 0) floors[row] = floor;
+}
+
 }  // namespace
 }  // namespace dsa
 
 namespace dsa {
 namespace {
 
-int logits_launch(const void* q, const void* k, const float* weights, const float* kscale,
-                  const int32_t* starts, const int32_t* ends, int64_t query_start, int64_t rows,
-                  int64_t columns, int64_t ldo, const float* q_fold, float* out,
-                  uint32_t* digit_counts, hipStream_t stream) {
+// Key range per work-group: the grid is about one work-group per CU.
+struct SplitPlan {
+  int64_t qgroups, splits, per;
+};
+
+SplitPlan split_plan(int64_t rows, int64_t ldo, bool counted) {
+  SplitPlan p;
+  p.qgroups = (rows + kQueriesPerBlock - 1) / kQueriesPerBlock;
+  const int64_t cus = device_cu_count();
+  int64_t splits = (cus + p.qgroups - 1) / p.qgroups;
+  if (splits < 1) splits = 1;
+  int64_t per = (ldo + splits - 1) / splits;
+  per = (per + kStageKeys - 1) / kStageKeys * kStageKeys;
+  if (counted && per > kMaxSplitKeys) per = kMaxSplitKeys;  // 16-bit LDS counters
+  splits = (ldo + per - 1) / per;
+  // Work-groups are dealt to the eight XCDs round-robin by linear id
+  // (x + splits * y): with a multiple of 8 splits every query group of one
+  // key range runs on the same XCD and the eight share its keys through that
+  // XCD's L2. The added splits start past the last column and exit at once.
+  if (splits >= 8) splits = (splits + 7) / 8 * 8;
+  p.splits = splits;
+  p.per = per;
+  return p;
+}
+
+int check_logits_args(const void* q, const void* k, const float* weights, const float* kscale,
+                      const int32_t* starts, const int32_t* ends, int64_t query_start,
+                      int64_t rows, int64_t columns, int64_t ldo, const float* q_fold) {
   DSA_CHECK_ARG(rows >= 0 && columns >= 1, "logits requires nonempty K");
   DSA_CHECK_ARG(ldo >= columns, "output row stride must cover every column");
   DSA_CHECK_ARG(query_start >= 0 && query_start + rows <= columns,
                 "query_start must place all query rows inside the visible KV sequence");
   DSA_CHECK_ARG((starts == nullptr) == (ends == nullptr), "starts and ends go together");
   if (rows == 0) return kOk;
-  DSA_CHECK_ARG(q && k && weights && kscale && out, "null pointer");
+  DSA_CHECK_ARG(q && k && weights && kscale, "null pointer");
   DSA_CHECK_ARG(reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(weights) % 16 == 0 &&
@@ -589,28 +712,56 @@ int logits_launch(const void* q, const void* k, const float* weights, const floa
                     reinterpret_cast<uintptr_t>(q_fold) % 16 == 0,
                 "q, k, weights and q_fold must be 16-byte aligned");
   DSA_CHECK_ARG(columns * kDim < 0xFFFFFFFFll, "K must be addressable with 32-bit offsets");
-  const int64_t qgroups = (rows + kQueriesPerBlock - 1) / kQueriesPerBlock;
-  const int64_t cus = device_cu_count();
-  int64_t splits = (cus + qgroups - 1) / qgroups;
-  if (splits < 1) splits = 1;
-  int64_t per = (ldo + splits - 1) / splits;
-  per = (per + kStageKeys - 1) / kStageKeys * kStageKeys;
-  if (digit_counts && per > kMaxSplitKeys) per = kMaxSplitKeys;  // 16-bit LDS counters
-  splits = (ldo + per - 1) / per;
-  // Work-groups are dealt to the eight XCDs round-robin by linear id
-  // (x + splits * y): with a multiple of 8 splits every query group of one
-  // key range runs on the same XCD and the eight share its keys through that
-  // XCD's L2. The added splits start past the last column and exit at once.
-  if (splits >= 8) splits = (splits + 7) / 8 * 8;
-  DSA_CHECK_ARG(qgroups < 65536, "too many query rows for one launch");
   DSA_CHECK_ARG(ldo < 0x7FFFFFFF - 64, "the logits row stride must fit int32");
-  hipLaunchKernelGGL(digit_counts ? logits_fp8_mfma<true> : logits_fp8_mfma<false>,
-                     dim3((unsigned)splits, (unsigned)qgroups), dim3(kThreads), 0, stream,
+  DSA_CHECK_ARG((rows + kQueriesPerBlock - 1) / kQueriesPerBlock < 65536,
+                "too many query rows for one launch");
+  return kOk;
+}
+
+int logits_launch(const void* q, const void* k, const float* weights, const float* kscale,
+                  const int32_t* starts, const int32_t* ends, int64_t query_start, int64_t rows,
+                  int64_t columns, int64_t ldo, const float* q_fold, float* out,
+                  uint32_t* digit_counts, hipStream_t stream) {
+  const int status = check_logits_args(q, k, weights, kscale, starts, ends, query_start, rows,
+                                       columns, ldo, q_fold);
+  if (status != kOk || rows == 0) return status;
+  DSA_CHECK_ARG(out != nullptr, "null pointer");
+  const SplitPlan p = split_plan(rows, ldo, digit_counts != nullptr);
+  hipLaunchKernelGGL(digit_counts ? logits_fp8_mfma<kModeCount> : logits_fp8_mfma<kModePlain>,
+                     dim3((unsigned)p.splits, (unsigned)p.qgroups), dim3(kThreads), 0, stream,
                      static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(k), weights,
-                     kscale, starts, ends, query_start, rows, columns, ldo, per, q_fold, out,
-                     digit_counts);
+                     kscale, starts, ends, query_start, rows, columns, ldo, p.per, q_fold, out,
+                     digit_counts, EmitArgs{});
   DSA_CHECK_LAUNCH("indexer logits");
   return kOk;
+}
+
+// Workspace of the candidate top-k (256-byte aligned parts): floors u32
+// [rows], records u32 [rows][splits][2], lists u64 [rows][splits][cap].
+struct EmitLayout {
+  SplitPlan plan;
+  int64_t cap;
+  int64_t records_offset, lists_offset, bytes;
+};
+
+constexpr int64_t kMaxEmitSplits = 512;
+
+int64_t round256(int64_t x) { return (x + 255) & ~(int64_t)255; }
+
+EmitLayout emit_layout(int64_t rows, int64_t columns, int64_t list_cap) {
+  EmitLayout l;
+  const int64_t ldo = (columns + 255) / 256 * 256;
+  l.plan = split_plan(rows, ldo, false);
+  // Default: an eighth of the split (~2x the expected candidates of a split
+  // at a uniform spread).
+  int64_t cap = list_cap > 0 ? list_cap : l.plan.per / 8;
+  cap = (cap + 63) / 64 * 64;
+  if (cap < 64) cap = 64;
+  l.cap = cap;
+  l.records_offset = round256(rows * 4);
+  l.lists_offset = l.records_offset + round256(rows * l.plan.splits * 8);
+  l.bytes = l.lists_offset + rows * l.plan.splits * cap * 8;
+  return l;
 }
 
 }  // namespace
@@ -677,5 +828,118 @@ extern "C" int dsa_indexer_topk_fp8(const void* q, const void* k, const float* w
                                    ldo, q_fold, scores, static_cast<uint32_t*>(workspace), stream);
   if (status != kOk) return status;
   return dsa_topk_radix_digits(scores, rows, columns, ldo, topk, values, indices, out_ld, workspace,
+                               workspace_bytes, stream);
+}
+
+// ---- the fused indexer top-k that writes only candidates.
+
+extern "C" int dsa_indexer_select_workspace_bytes(int64_t rows, int64_t columns, int64_t list_cap,
+                                                  int64_t* bytes) {
+  using namespace dsa;
+  DSA_CHECK_ARG(rows >= 0 && rows < 0x7FFFFFFF && columns >= 1 && columns < 0x7FFFFFFF - 256 &&
+                    list_cap >= 0 && bytes != nullptr,
+                "invalid indexer select workspace query");
+  *bytes = emit_layout(rows, columns, list_cap).bytes;
+  return kOk;
+}
+
+extern "C" int dsa_indexer_floors_fp8(const void* q, const void* k, const float* weights,
+                                      const float* kscale, const int32_t* starts,
+                                      const int32_t* ends, int64_t query_start, int64_t rows,
+                                      int64_t columns, int64_t topk, uint32_t* floors,
+                                      hipStream_t stream) {
+  using namespace dsa;
+  DSA_CHECK_ARG(topk >= 1 && topk <= 2048, "k must be an integer in [1, 2048]");
+  const int status = check_logits_args(q, k, weights, kscale, starts, ends, query_start, rows,
+                                       columns, columns, nullptr);
+  if (status != kOk || rows == 0) return status;
+  DSA_CHECK_ARG(floors != nullptr && reinterpret_cast<uintptr_t>(floors) % 4 == 0, "null pointer");
+  DSA_CHECK_ARG(rows < 0x7FFFFFFF, "too many rows");
+  const int count = (int)(topk < columns ? topk : columns);
+  hipLaunchKernelGGL(index_floors, dim3((unsigned)rows), dim3(kFloorThreads), 0, stream,
+                     static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(k), weights,
+                     kscale, starts, ends, query_start, columns, count, floors);
+  DSA_CHECK_LAUNCH("indexer floors");
+  return kOk;
+}
+
+extern "C" int dsa_indexer_logits_fp8_emit(const void* q, const void* k, const float* weights,
+                                           const float* kscale, const int32_t* starts,
+                                           const int32_t* ends, int64_t query_start, int64_t rows,
+                                           int64_t columns, int64_t ldo, const float* q_fold,
+                                           float* scores, int64_t list_cap, void* workspace,
+                                           int64_t workspace_bytes, hipStream_t stream) {
+  using namespace dsa;
+  const int status = check_logits_args(q, k, weights, kscale, starts, ends, query_start, rows,
+                                       columns, ldo, q_fold);
+  if (status != kOk || rows == 0) return status;
+  DSA_CHECK_ARG(ldo == (columns + 255) / 256 * 256, "the score stride must be columns rounded up to 256");
+  DSA_CHECK_ARG(scores != nullptr, "null pointer");
+  const EmitLayout l = emit_layout(rows, columns, list_cap);
+  DSA_CHECK_ARG(l.plan.splits <= kMaxEmitSplits, "too many key splits");
+  DSA_CHECK_ARG(workspace != nullptr && reinterpret_cast<uintptr_t>(workspace) % 256 == 0 &&
+                    workspace_bytes >= l.bytes,
+                "indexer select workspace too small or misaligned");
+  uint8_t* base = static_cast<uint8_t*>(workspace);
+  EmitArgs emit{reinterpret_cast<const uint32_t*>(base),
+                reinterpret_cast<uint64_t*>(base + l.lists_offset),
+                reinterpret_cast<uint32_t*>(base + l.records_offset), (int32_t)l.cap,
+                (int32_t)l.plan.splits};
+  hipLaunchKernelGGL(logits_fp8_mfma<kModeEmit>, dim3((unsigned)l.plan.splits, (unsigned)l.plan.qgroups),
+                     dim3(kThreads), 0, stream, static_cast<const uint8_t*>(q),
+                     static_cast<const uint8_t*>(k), weights, kscale, starts, ends, query_start,
+                     rows, columns, ldo, l.plan.per, q_fold, scores, nullptr, emit);
+  DSA_CHECK_LAUNCH("indexer logits (candidates)");
+  return kOk;
+}
+
+extern "C" int dsa_indexer_emit_topk(const void* q, const void* k, const float* weights,
+                                     const float* kscale, const int32_t* starts,
+                                     const int32_t* ends, int64_t query_start, int64_t rows,
+                                     int64_t columns, const float* q_fold, float* scores,
+                                     int64_t topk, float* values, int32_t* indices,
+                                     int64_t out_ld, int64_t list_cap, const void* workspace,
+                                     int64_t workspace_bytes, hipStream_t stream) {
+  using namespace dsa;
+  DSA_CHECK_ARG(topk >= 1 && topk <= 2048, "k must be an integer in [1, 2048]");
+  const int status = check_logits_args(q, k, weights, kscale, starts, ends, query_start, rows,
+                                       columns, columns, q_fold);
+  if (status != kOk || rows == 0) return status;
+  DSA_CHECK_ARG(out_ld >= (topk < columns ? topk : columns), "output row stride too small");
+  DSA_CHECK_ARG(values && indices && scores, "null pointer");
+  const EmitLayout l = emit_layout(rows, columns, list_cap);
+  DSA_CHECK_ARG(l.plan.splits <= kMaxEmitSplits, "too many key splits");
+  DSA_CHECK_ARG(workspace != nullptr && reinterpret_cast<uintptr_t>(workspace) % 256 == 0 &&
+                    workspace_bytes >= l.bytes,
+                "indexer select workspace too small or misaligned");
+  const uint8_t* base = static_cast<const uint8_t*>(workspace);
+  return topk_from_candidates(
+      static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(k), weights, kscale, starts,
+      ends, query_start, q_fold, scores, rows, columns, (columns + 255) / 256 * 256, topk, values,
+      indices, out_ld, reinterpret_cast<const uint32_t*>(base),
+      reinterpret_cast<const uint32_t*>(base + l.records_offset),
+      reinterpret_cast<const uint64_t*>(base + l.lists_offset), l.plan.splits, l.plan.per, l.cap,
+      stream);
+}
+
+// Floors, candidate logits and the top-k from the candidates, in one call.
+extern "C" int dsa_indexer_select_fp8(const void* q, const void* k, const float* weights,
+                                      const float* kscale, const int32_t* starts,
+                                      const int32_t* ends, int64_t query_start, int64_t rows,
+                                      int64_t columns, const float* q_fold, float* scores,
+                                      int64_t topk, float* values, int32_t* indices,
+                                      int64_t out_ld, void* workspace, int64_t workspace_bytes,
+                                      hipStream_t stream) {
+  using namespace dsa;
+  int status = dsa_indexer_floors_fp8(q, k, weights, kscale, starts, ends, query_start, rows,
+                                      columns, topk, static_cast<uint32_t*>(workspace), stream);
+  if (status != kOk || rows == 0) return status;
+  const int64_t ldo = (columns + 255) / 256 * 256;
+  status = dsa_indexer_logits_fp8_emit(q, k, weights, kscale, starts, ends, query_start, rows,
+                                       columns, ldo, q_fold, scores, 0, workspace, workspace_bytes,
+                                       stream);
+  if (status != kOk) return status;
+  return dsa_indexer_emit_topk(q, k, weights, kscale, starts, ends, query_start, rows, columns,
+                               q_fold, scores, topk, values, indices, out_ld, 0, workspace,
                                workspace_bytes, stream);
 }

@@ -11,6 +11,7 @@
 // 16 lanes per row, 8 bf16 (one 16-byte load) per lane. Other shapes and
 // dtypes use one wave per row.
 #include "dsa_common.h"
+#include "logits_core.h"
 #include "../../include/dsa_gfx950.h"
 
 namespace dsa {
@@ -296,11 +297,166 @@ __global__ __launch_bounds__(256) void kv_pack_fp8(const uint16_t* __restrict__ 
   pack_tokens(blockIdx.x, kv, tokens, token_offset, page_table, pages, cache, status);
 }
 
-// The three small stages of a layer step in one launch: blocks [0, nq) quantise
+// Floors of the candidate top-k (logits_core.h: floor_rank,
+// floor_of_samples) for the layer step, one 256-thread block per query row
+// i: the row's 64 index-Q head rows quantised here (the A1 scale; the e4m3
+// codes by the hardware conversion - the floor is an estimate, and the
+// exact codes are the Q blocks'), scored at n sample columns of the resident
+// history [0, history) - the new keys are being written by this launch -
+// with four MFMAs per 16 samples (each wave a quarter of the samples, all
+// 64 heads; the MFMAs of one group are issued before the previous group's
+// head sum). The sample loads are issued first.
+constexpr int kPrologueFloorSamples = 2048;
+constexpr int kPrologueFloorBatch = 16;  // 16-sample groups per wave in flight together
+
+struct FloorArgs {
+  const uint8_t* keys;      // resident index-K codes [history + ...][128]
+  const float* key_scales;  // [history + ...]
+  int64_t history;          // sample columns [0, history); row i sees history + i + 1
+  int count;                // min(topk, columns)
+  uint32_t* floors;         // [rows]
+};
+
+// Max over the four consecutive lanes of a quad (DPP quad permutes).
+__device__ __forceinline__ uint32_t quad_max(uint32_t v) {
+  uint32_t o = __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);  // lane ^ 1
+  v = v > o ? v : o;
+  o = __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);           // lane ^ 2
+  return v > o ? v : o;
+}
+
+__device__ void prologue_floor(int64_t i, const uint16_t* __restrict__ q,
+                               const float* __restrict__ weights, const FloorArgs fa) {
+  using namespace logits_core;
+  __shared__ __align__(16) uint32_t codes[kHeads][36];  // 144-byte rows: fewer bank conflicts
+  __shared__ float folded[kHeads];
+  __shared__ uint32_t keys[kPrologueFloorSamples];
+  __shared__ uint32_t hist[2048];
+  __shared__ uint32_t wave_sums[4];
+  __shared__ uint32_t result[2];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int group = lane >> 4;
+  const int col = lane & 15;
+  const int32_t history = (int32_t)fa.history;  // < 2^25 (the launcher checks)
+  if (history < kFloorMinVisible) {
+    if (tid == 0) fa.floors[i] = 0u;
+    return;
+  }
+  const int n = (int)floor_samples(history, kPrologueFloorSamples);
+  const int stride = history / n;  // >= 2
+  const uint32_t rank = floor_rank(n, fa.count, (int64_t)history + i + 1);
+  if (rank > (uint32_t)n) {
+    if (tid == 0) fa.floors[i] = 0u;
+    return;
+  }
+  const int groups = n / 16;
+  // Sample m is column m stride + stride / 2; wave w scores groups w, w + 4, ...
+  v8i b[kPrologueFloorBatch];
+  float ks[kPrologueFloorBatch];
+  auto load_batch = [&](int g0) {
+#pragma unroll
+    for (int j = 0; j < kPrologueFloorBatch; ++j) {
+      const int g = g0 + 4 * j;
+      const uint32_t key = (uint32_t)((g < groups ? 16 * g + col : col) * stride + stride / 2);
+      const v4u* src = reinterpret_cast<const v4u*>(fa.keys + key * (uint32_t)kDim + 32u * group);
+      const v4u lo = src[0], hi = src[1];
+      b[j] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+      ks[j] = fa.key_scales[key];
+    }
+  };
+  load_batch(wave);
+  // Quantise the row's heads: thread t takes head t / 4, dims 32 (t % 4) ..
+  // + 31 (the row amax over its four threads).
+  {
+    const int h = tid >> 2, part = tid & 3;
+    const uint4* src = reinterpret_cast<const uint4*>(q + ((i * kHeads + h) * kDim + 32 * part));
+    float v[32];
+    uint32_t m = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint4 raw = src[c];
+      const uint32_t words[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[8 * c + 2 * j] = bf16_to_f32(words[j] & 0xFFFFu);
+        v[8 * c + 2 * j + 1] = bf16_to_f32(words[j] >> 16);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      const uint32_t a = __float_as_uint(v[j]) & 0x7FFFFFFFu;
+      m = m > a ? m : a;
+    }
+    m = quad_max(m);
+    const float scale = scale_from_amax_bits(m, true);
+    const float inverse = 1.0f / scale;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      float y[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) y[j] = fminf(fmaxf(v[4 * c + j] * inverse, -448.0f), 448.0f);
+      uint32_t word = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
+      word = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], word, true);
+      codes[h][8 * part + c] = word;
+    }
+    if (part == 0) folded[h] = weights[i * kHeads + h] * scale;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) hist[8 * tid + j] = 0;
+  if (tid < 2) result[tid] = 0;
+  __syncthreads();
+  v8i qa[4];
+  float wv[16];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const v4u lo = *reinterpret_cast<const v4u*>(&codes[16 * t + col][8 * group]);
+    const v4u hi = *reinterpret_cast<const v4u*>(&codes[16 * t + col][8 * group + 4]);
+    qa[t] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) wv[4 * t + r] = folded[16 * t + 4 * group + r];
+  }
+  // sum_h w_h max(s_h, 0) of one group: the lane's 16 heads, then the four
+  // lane rows (row-swap permutes).
+  auto head_sums = [&](const v4f (&acc)[4], int g, float kscale_key) {
+    float p = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) p = fmaf(wv[4 * t + r], fmaxf(acc[t][r], 0.0f), p);
+    p = fold32(p, p);
+    p = fold16(p, p);
+    if (group == 0 && g < groups) keys[16 * g + col] = radix_of(p * kscale_key);
+  };
+  for (int g0 = wave; g0 < groups; g0 += 4 * kPrologueFloorBatch) {
+    if (g0 != wave) load_batch(g0);
+    v4f prev[4];
+#pragma unroll
+    for (int j = 0; j < kPrologueFloorBatch; ++j) {
+      v4f acc[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        acc[t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+            qa[t], b[j], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0, 0, 0, 0);
+      if (j > 0) head_sums(prev, g0 + 4 * (j - 1), ks[j - 1]);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) prev[t] = acc[t];
+    }
+    head_sums(prev, g0 + 4 * (kPrologueFloorBatch - 1), ks[kPrologueFloorBatch - 1]);
+  }
+  __syncthreads();
+  const uint32_t floor = floor_of_samples<256>(keys, n, rank, hist, wave_sums, result);
+  if (tid == 0) fa.floors[i] = floor;
+}
+
+// The small stages of a layer step in one launch: blocks [0, nq) quantise
 // the indexer Q rows and fold their scales into the head weights, blocks
-// [nq, nq + nk) quantise the new index-K rows into the resident cache, and the
-// rest pack the new KV tokens into the fp8 paged cache. All three are
-// independent of each other.
+// [nq, nq + nk) quantise the new index-K rows into the resident cache,
+// blocks [nq + nk, nq + nk + nt) pack the new KV tokens into the fp8 paged
+// cache, and nf more blocks (when floors are asked for; placed first)
+// compute the candidate top-k's per-row floors. All are independent of
+// each other.
 __global__ __launch_bounds__(256) void layer_prologue(
     const uint16_t* __restrict__ q, int64_t q_rows, const float* __restrict__ weights,
     uint8_t* __restrict__ q_codes, float* __restrict__ q_scales, float* __restrict__ w_folded,
@@ -308,8 +464,15 @@ __global__ __launch_bounds__(256) void layer_prologue(
     uint8_t* __restrict__ k_codes,
     float* __restrict__ k_scales, const uint16_t* __restrict__ kv, int64_t tokens,
     int64_t token_offset, const int32_t* __restrict__ page_table, int64_t pages,
-    uint8_t* __restrict__ cache, int32_t* __restrict__ status, int64_t nq, int64_t nk) {
-  const int64_t b = blockIdx.x;
+    uint8_t* __restrict__ cache, int32_t* __restrict__ status, int64_t nq, int64_t nk,
+    int64_t nf, FloorArgs fa) {
+  // The floor blocks (the longest) come first in the grid, so that they
+  // start at once and the short blocks fill the CUs around them.
+  if ((int64_t)blockIdx.x < nf) {
+    prologue_floor(blockIdx.x, q, weights, fa);
+    return;
+  }
+  const int64_t b = blockIdx.x - nf;
   if (b < nq) {
     const QuantLane mine = quantize_rows_d128(b, q, q_rows, 128, q_codes, q_scales, 1, weights, w_folded);
     if (q_fold) fold_partial(b, mine, q_fold);
@@ -348,6 +511,19 @@ extern "C" int dsa_layer_prologue_fp8(const void* q, int64_t q_rows, const float
                                       int64_t token_offset, const int32_t* page_table,
                                       int64_t pages, void* cache, int32_t* status,
                                       hipStream_t stream) {
+  return dsa_layer_prologue_floors_fp8(q, q_rows, weights, q_codes, q_scales, w_folded, q_fold, k,
+                                       k_rows, k_codes, k_scales, kv, tokens, token_offset,
+                                       page_table, pages, cache, status, nullptr, nullptr, 0, 0,
+                                       nullptr, stream);
+}
+
+extern "C" int dsa_layer_prologue_floors_fp8(
+    const void* q, int64_t q_rows, const float* weights, void* q_codes, float* q_scales,
+    float* w_folded, float* q_fold, const void* k, int64_t k_rows, void* k_codes,
+    float* k_scales, const void* kv, int64_t tokens, int64_t token_offset,
+    const int32_t* page_table, int64_t pages, void* cache, int32_t* status,
+    const void* key_cache, const float* key_cache_scales, int64_t history, int64_t topk,
+    uint32_t* floors, hipStream_t stream) {
   using namespace dsa;
   DSA_CHECK_ARG(q_rows >= 0 && k_rows >= 0 && tokens >= 0 && token_offset >= 0 && pages >= 0,
                 "invalid prologue shape");
@@ -367,14 +543,29 @@ extern "C" int dsa_layer_prologue_fp8(const void* q, int64_t q_rows, const float
   const int64_t nq = (q_rows * 16 + 255) / 256;
   const int64_t nk = (k_rows * 16 + 255) / 256;
   const int64_t nt = (tokens + 3) / 4;
-  if (nq + nk + nt == 0) return kOk;
-  DSA_CHECK_ARG(nq + nk + nt < 0x7FFFFFFF, "prologue too large for one launch");
-  hipLaunchKernelGGL(layer_prologue, dim3((unsigned)(nq + nk + nt)), dim3(256), 0, stream,
+  // Floor blocks: one per query row (q_rows / 64 queries).
+  int64_t nf = 0;
+  if (floors != nullptr) {
+    DSA_CHECK_ARG(q_rows % 64 == 0 && key_cache && key_cache_scales && history >= 0 &&
+                      topk >= 1 && topk <= 2048 &&
+                      reinterpret_cast<uintptr_t>(key_cache) % 16 == 0 &&
+                      reinterpret_cast<uintptr_t>(floors) % 4 == 0,
+                  "floors need whole queries, the resident key cache (16-byte aligned) and "
+                  "k in [1, 2048]");
+    DSA_CHECK_ARG(history < ((int64_t)1 << 25), "the key cache must be addressable with 32-bit offsets");
+    nf = q_rows / 64;
+  }
+  if (nq + nk + nt + nf == 0) return kOk;
+  DSA_CHECK_ARG(nq + nk + nt + nf < 0x7FFFFFFF, "prologue too large for one launch");
+  const int64_t columns = history + q_rows / 64;
+  const FloorArgs fa{static_cast<const uint8_t*>(key_cache), key_cache_scales, history,
+                     (int)(topk < columns ? topk : columns), floors};
+  hipLaunchKernelGGL(layer_prologue, dim3((unsigned)(nq + nk + nt + nf)), dim3(256), 0, stream,
                      static_cast<const uint16_t*>(q), q_rows, weights,
                      static_cast<uint8_t*>(q_codes), q_scales, w_folded, q_rows ? q_fold : nullptr,
                      static_cast<const uint16_t*>(k), k_rows, static_cast<uint8_t*>(k_codes),
                      k_scales, static_cast<const uint16_t*>(kv), tokens, token_offset, page_table,
-                     pages, static_cast<uint8_t*>(cache), status, nq, nk);
+                     pages, static_cast<uint8_t*>(cache), status, nq, nk, nf, fa);
   DSA_CHECK_LAUNCH("layer prologue");
   return kOk;
 }

@@ -35,6 +35,7 @@
 #include <mutex>
 
 #include "dsa_common.h"
+#include "logits_core.h"
 #include "../../include/dsa_gfx950.h"
 
 namespace dsa {
@@ -980,6 +981,19 @@ __device__ __forceinline__ uint32_t wave_prefix(uint32_t n, uint32_t* total) {
   return pre;
 }
 
+// Exclusive prefix over the wave of any per-lane counts, and the total.
+__device__ __forceinline__ uint32_t wave_prefix_any(uint32_t n, uint32_t* total) {
+  const int lane = threadIdx.x & 63;
+  uint32_t incl = n;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t o = __shfl_up(incl, d);
+    if (lane >= d) incl += o;
+  }
+  *total = __shfl(incl, 63);
+  return incl - n;
+}
+
 typedef uint32_t v4u32 __attribute__((ext_vector_type(4)));
 
 struct SelectShared {
@@ -1136,6 +1150,113 @@ union FinishShared {
   FinishSort fs;
 };
 
+// One counting sort of the n candidate keys (unique composite keys whose
+// radix keys lie in [lo, hi]) held kSortPerThread per thread (slot j of a
+// thread holds a key when bit j of `valid` is set): kSortBins linear
+// buckets of the radix keys,
+// ranks inside a bucket by comparison, the first `count` through LDS to
+// emit(i, key). Buckets that start at or past `count` hold no output key and
+// are neither ranked nor limited in size. fs.cursor and fs.crowded must be
+// zero on entry. Returns false, with nothing emitted, when a bucket that
+// starts below `count` holds more than kSortBucketMax keys.
+template <typename Emit>
+__device__ __forceinline__ bool counting_sort_mask(FinishSort& fs, const uint64_t (&key)[kSortPerThread],
+                                                   uint32_t valid, uint32_t n, uint32_t lo,
+                                                   uint32_t hi, int count, Emit&& emit) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  // Linear buckets over the radix keys [lo, hi], descending order =
+  // descending bucket, then descending key.
+  const uint32_t span = hi - lo + 1u;  // 0 stands for 2^32
+  const int bits = 32 - __builtin_clz((span - 1) | 1u);
+  const int shift = bits > 12 ? bits - 12 : 0;
+  // (Clamped: keys outside the range only come with counts that disagree
+  // with the scores, and must not index outside the buckets.)
+  auto bucket_of = [lo, shift](uint64_t k) {
+    return min(((uint32_t)(k >> 32) - lo) >> shift, (uint32_t)kSortBins - 1);
+  };
+#pragma unroll
+  for (int j = 0; j < kSortPerThread; ++j)
+    if ((valid >> j) & 1u) atomicAdd(&fs.cursor[bucket_of(key[j])], 1u);
+  __syncthreads();
+  // Thread t owns buckets 4t .. 4t + 3; start = keys in higher buckets.
+  uint32_t c4[4], own = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    c4[j] = fs.cursor[4 * tid + j];
+    own += c4[j];
+  }
+  uint32_t incl = own;  // keys in buckets of this and higher threads of the wave
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t o = __shfl_down(incl, d);
+    if (lane + d < 64) incl += o;
+  }
+  if (lane == 0) fs.wave_sums[wave] = incl;
+  __syncthreads();
+  uint32_t higher = incl - own;
+  for (int w = wave + 1; w < kThreads / 64; ++w) higher += fs.wave_sums[w];
+#pragma unroll
+  for (int j = 3; j >= 0; --j) {
+    fs.start[4 * tid + j] = higher;
+    fs.cursor[4 * tid + j] = higher;
+    if (c4[j] > kSortBucketMax && higher < (uint32_t)count) fs.crowded = 1;
+    higher += c4[j];
+  }
+  __syncthreads();
+  if (!fs.crowded) {
+#pragma unroll
+    for (int j = 0; j < kSortPerThread; ++j)
+      if ((valid >> j) & 1u) fs.sorted[atomicAdd(&fs.cursor[bucket_of(key[j])], 1u)] = key[j];
+    __syncthreads();
+    // Rank inside the bucket; bucket b spans [start[b], start[b - 1]). A
+    // bucket that starts at or past `count` holds no output key: its keys
+    // (most of the threshold digit's, typically) are not ranked.
+    for (uint32_t i = tid; i < n; i += kThreads) {
+      const uint64_t k = fs.sorted[i];
+      const uint32_t b = bucket_of(k);
+      const uint32_t b0 = fs.start[b], b1 = b ? fs.start[b - 1] : n;
+      if (b0 >= (uint32_t)count) continue;
+      uint32_t rank = b0, j = b0;
+      for (; j + 4 <= b1; j += 4) {
+        const uint64_t x0 = fs.sorted[j], x1 = fs.sorted[j + 1];
+        const uint64_t x2 = fs.sorted[j + 2], x3 = fs.sorted[j + 3];
+        rank += (x0 > k ? 1u : 0u) + (x1 > k ? 1u : 0u) + (x2 > k ? 1u : 0u) + (x3 > k ? 1u : 0u);
+      }
+      for (; j < b1; ++j) rank += fs.sorted[j] > k ? 1u : 0u;
+      if (rank < (uint32_t)count) fs.out[rank] = k;
+    }
+    __syncthreads();
+    for (int i = tid; i < count; i += kThreads) emit(i, fs.out[i]);
+    return true;
+  }
+  return false;
+}
+
+// The same with the keys at positions t + j kThreads < n.
+__device__ __forceinline__ uint32_t prefix_slots(uint32_t n) {
+  uint32_t valid = 0;
+#pragma unroll
+  for (int j = 0; j < kSortPerThread; ++j)
+    valid |= (int)threadIdx.x + j * kThreads < (int)n ? 1u << j : 0u;
+  return valid;
+}
+template <typename Emit>
+__device__ __forceinline__ bool counting_sort_range(FinishSort& fs, const uint64_t (&key)[kSortPerThread],
+                                                    uint32_t n, uint32_t lo, uint32_t hi, int count,
+                                                    Emit&& emit) {
+  return counting_sort_mask(fs, key, prefix_slots(n), n, lo, hi, count, emit);
+}
+
+// The same over every key at or above digit d0, top the highest digit.
+template <typename Emit>
+__device__ __forceinline__ bool counting_sort_keys(FinishSort& fs, const uint64_t (&key)[kSortPerThread],
+                                                   uint32_t n, uint32_t d0, uint32_t top, int count,
+                                                   Emit&& emit) {
+  return counting_sort_range(fs, key, n, d0 << 21, ((top + 1) << 21) - 1u, count, emit);
+}
+
 // One work-group per row, after topk_digit_select. Zeroes the row's counts
 // and fill, then sorts the listed candidates (every key at or above the
 // threshold digit, held kSortPerThread per thread) by one counting sort over
@@ -1213,72 +1334,7 @@ __global__ __launch_bounds__(kThreads, 1) void topk_digit_finish(const float* __
 #pragma unroll
       for (int j = kSortEager; j < kSortPerThread; ++j) key[j] = list[tid + j * kThreads];
     }
-    // Linear buckets over the radix keys [d0 << 21, (top + 1) << 21),
-    // descending order = descending bucket, then descending key.
-    const uint32_t lo = d0 << 21;
-    const uint32_t span = ((top + 1) << 21) - lo;  // top >= d0; 0 stands for 2^32
-    const int bits = 32 - __builtin_clz((span - 1) | 1u);
-    const int shift = bits > 12 ? bits - 12 : 0;
-    // (Clamped: keys outside the range only come with counts that disagree
-    // with the scores, and must not index outside the buckets.)
-    auto bucket_of = [lo, shift](uint64_t k) {
-      return min(((uint32_t)(k >> 32) - lo) >> shift, (uint32_t)kSortBins - 1);
-    };
-#pragma unroll
-    for (int j = 0; j < kSortPerThread; ++j)
-      if (tid + j * kThreads < (int)n) atomicAdd(&fs.cursor[bucket_of(key[j])], 1u);
-    __syncthreads();
-    // Thread t owns buckets 4t .. 4t + 3; start = keys in higher buckets.
-    uint32_t c4[4], own = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      c4[j] = fs.cursor[4 * tid + j];
-      own += c4[j];
-      if (c4[j] > kSortBucketMax) fs.crowded = 1;
-    }
-    uint32_t incl = own;  // keys in buckets of this and higher threads of the wave
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const uint32_t o = __shfl_down(incl, d);
-      if (lane + d < 64) incl += o;
-    }
-    if (lane == 0) fs.wave_sums[wave] = incl;
-    __syncthreads();
-    uint32_t higher = incl - own;
-    for (int w = wave + 1; w < kThreads / 64; ++w) higher += fs.wave_sums[w];
-#pragma unroll
-    for (int j = 3; j >= 0; --j) {
-      fs.start[4 * tid + j] = higher;
-      fs.cursor[4 * tid + j] = higher;
-      higher += c4[j];
-    }
-    __syncthreads();
-    if (!fs.crowded) {
-#pragma unroll
-      for (int j = 0; j < kSortPerThread; ++j)
-        if (tid + j * kThreads < (int)n) fs.sorted[atomicAdd(&fs.cursor[bucket_of(key[j])], 1u)] = key[j];
-      __syncthreads();
-      // Rank inside the bucket; bucket b spans [start[b], start[b - 1]). A
-      // bucket that starts at or past `count` holds no output key: its keys
-      // (most of the threshold digit's, typically) are not ranked.
-      for (uint32_t i = tid; i < n; i += kThreads) {
-        const uint64_t k = fs.sorted[i];
-        const uint32_t b = bucket_of(k);
-        const uint32_t b0 = fs.start[b], b1 = b ? fs.start[b - 1] : n;
-        if (b0 >= (uint32_t)count) continue;
-        uint32_t rank = b0, j = b0;
-        for (; j + 4 <= b1; j += 4) {
-          const uint64_t x0 = fs.sorted[j], x1 = fs.sorted[j + 1];
-          const uint64_t x2 = fs.sorted[j + 2], x3 = fs.sorted[j + 3];
-          rank += (x0 > k ? 1u : 0u) + (x1 > k ? 1u : 0u) + (x2 > k ? 1u : 0u) + (x3 > k ? 1u : 0u);
-        }
-        for (; j < b1; ++j) rank += fs.sorted[j] > k ? 1u : 0u;
-        if (rank < (uint32_t)count) fs.out[rank] = k;
-      }
-      __syncthreads();
-      for (int i = tid; i < count; i += kThreads) emit(i, fs.out[i]);
-      return;
-    }
+    if (counting_sort_keys(fs, key, n, d0, top, count, emit)) return;
     __syncthreads();  // before the fallback reuses the LDS
   }
   // Fallback: split the threshold digit's keys to exactly `count` keys, then sort.
@@ -1311,6 +1367,268 @@ __global__ __launch_bounds__(kThreads, 1) void topk_digit_finish(const float* __
   __syncthreads();
   sort_selected(sh, count);
   for (int i = tid; i < count; i += kThreads) emit(i, sh.sel[i]);
+}
+
+// ---- exact top-k from the candidates of the fused indexer step.
+//
+// The logits kernel's candidate mode (logits.hip) leaves, per row r with a
+// floor F > 0: for each key split, a list of the composite keys of the
+// split's scores at or above F, and from the split's spill column on (when
+// its list would overflow) the split's scores stored in full in the score
+// row. A row with F = 0 was stored in full. The candidates - listed keys and
+// spilled scores at or above F - hold every score of the row at or above F,
+// so when there are at least `count` of them they hold the row's top
+// `count` (and the top-k of the candidates is the row's). Otherwise (F was
+// above the row's count-th largest score), or when they do not fit the
+// work-group, the row's scores are recomputed here with the logits kernel's
+// arithmetic (logits_core.h) and selected from in full.
+struct CandidateLists {
+  const uint32_t* floors;   // [rows] the row's floor (a radix key), 0 when stored in full
+  const uint32_t* records;  // [rows][splits][2]: keys listed, first spilled column
+  const uint64_t* lists;    // [rows][splits][cap] composite keys
+  int64_t splits, per, cap;
+};
+struct LogitsInputs {
+  const uint8_t* q;
+  const uint8_t* k;
+  const float* w;
+  const float* kscale;
+  const int32_t* starts;
+  const int32_t* ends;
+  int64_t query_start;
+  const float* q_fold;
+};
+constexpr int kMaxCandidateSplits = 512;
+
+__global__ __launch_bounds__(kThreads, 1) void topk_candidates(float* __restrict__ scores,
+                                                              int64_t cols, int64_t ld,
+                                                              int total_count,
+                                                              float* __restrict__ values,
+                                                              int32_t* __restrict__ ids,
+                                                              int64_t out_ld, CandidateLists cl,
+                                                              LogitsInputs li) {
+  __shared__ FinishShared lds;
+  __shared__ uint32_t info[8];  // fill, largest radix key, misfit, digit, above, bucket
+  FinishSort& fs = lds.fs;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t r = blockIdx.x;
+  const int count = total_count < cols ? total_count : (int)cols;
+  const uint32_t floor = cl.floors[r];
+  if (floor == 0) {
+    select_row<kResidentVecSmall>(lds.sh, scores, cols, ld, total_count, values, ids, out_ld,
+                                  nullptr, r, 0, 1);
+    return;
+  }
+  const int64_t vis_lo = li.starts ? (int64_t)li.starts[r] : 0;
+  int64_t vis_hi = li.ends ? (int64_t)li.ends[r] : li.query_start + r + 1;
+  if (vis_hi > cols) vis_hi = cols;
+  float* row = scores + r * ld;
+  float* vout = values + r * out_ld;
+  int32_t* iout = ids + r * out_ld;
+  auto emit = [&](int i, uint64_t k) {
+    const uint32_t b = key_bits((uint32_t)(k >> 32));
+    vout[i] = __uint_as_float(b);
+    const bool finite = (b & 0x7F800000u) != 0x7F800000u;
+    iout[i] = finite ? (int32_t)(~(uint32_t)k) : -1;
+  };
+  for (int i = tid; i < kSortBins; i += kThreads) fs.cursor[i] = 0;
+  if (tid < 3) info[tid] = 0;  // listed keys, largest radix key, any split not taken in registers
+  if (tid == 0) fs.crowded = 0;
+
+  // Fast path: the candidates go straight into the sort's registers. Thread
+  // t serves key split t / T (T = kThreads / splits threads per split) and
+  // holds entries u, u + T, ... (u = t % T) of its list, when no split
+  // spilled and every list fits its threads' kSortPerThread slots.
+  constexpr int kWaves = kThreads / 64;
+  const int splits = (int)cl.splits;
+  const int per_split = kThreads / splits;  // >= 2 (splits <= 512)
+  const int sp = tid / per_split, u = tid % per_split;
+  uint32_t n_sp = 0;
+  int32_t spill_sp = 0x7FFFFFFF;
+  if (sp < splits && (int64_t)sp * cl.per < cols) {
+    const uint32_t* rec = cl.records + (r * cl.splits + sp) * 2;
+    n_sp = rec[0];
+    spill_sp = (int32_t)rec[1];
+  }
+  const bool fits = spill_sp == 0x7FFFFFFF && n_sp <= (uint32_t)(per_split * kSortPerThread);
+  uint64_t key[kSortPerThread];
+  uint32_t valid = 0, top_key = 0;
+  {
+    const uint64_t* src = cl.lists + (r * cl.splits + sp) * cl.cap;
+#pragma unroll
+    for (int j = 0; j < kSortPerThread; ++j) {
+      const uint32_t e = (uint32_t)(u + per_split * j);
+      const bool live = fits && e < n_sp;
+      key[j] = live ? src[e] : 0ull;
+      valid |= live ? 1u << j : 0u;
+      top_key = max(top_key, (uint32_t)(key[j] >> 32));
+    }
+  }
+  __syncthreads();  // the LDS state above is set
+  {
+    uint32_t total = 0;
+    (void)wave_prefix_any(u == 0 ? n_sp : 0u, &total);
+    const bool misfit = __builtin_amdgcn_ballot_w64(!fits) != 0;
+    top_key = max(top_key, lane_xor<1>(top_key));
+    top_key = max(top_key, lane_xor<2>(top_key));
+    top_key = max(top_key, lane_xor<4>(top_key));
+    top_key = max(top_key, lane_xor<8>(top_key));
+    top_key = max(top_key, lane_xor<16>(top_key));
+    top_key = max(top_key, lane_xor<32>(top_key));
+    if (lane == 0) {
+      if (total) atomicAdd(&info[0], total);
+      atomicMax(&info[1], top_key);
+      if (misfit) atomicOr(&info[2], 1u);
+    }
+  }
+  __syncthreads();
+  uint32_t n_cand = info[0];
+  if (info[2]) {
+    // Candidates into the LDS buffer in no order (the sort does not need
+    // one): wave w takes the key splits w, w + 16, ... - lane j holds split
+    // w + 16 j's record - and one LDS atomic places all their listed keys;
+    // the lists are copied in chunks of 64 keys, eight chunks of loads in
+    // flight at a time. Spilled scores at or above the floor follow.
+    if (tid == 0) info[0] = 0;
+    __syncthreads();
+    const int my_split = wave + kWaves * lane;
+    uint32_t n_l = 0;
+    int32_t spill_l = 0x7FFFFFFF;
+    if (my_split < splits && (int64_t)my_split * cl.per < cols) {
+      const uint32_t* rec = cl.records + (r * cl.splits + my_split) * 2;
+      n_l = rec[0];
+      spill_l = (int32_t)rec[1];
+    }
+    uint32_t n_wave = 0;
+    const uint32_t n_pre = wave_prefix_any(n_l, &n_wave);
+    uint32_t chunks_wave = 0;
+    const uint32_t chunks_l = (n_l + 63) / 64;
+    const uint32_t chunk_pre = wave_prefix_any(chunks_l, &chunks_wave);
+    uint32_t wave_base = 0;
+    if (lane == 0 && n_wave) wave_base = atomicAdd(&info[0], n_wave);
+    wave_base = __builtin_amdgcn_readfirstlane(wave_base);
+    const int wave_splits = (splits - wave + kWaves - 1) / kWaves;  // lanes holding a split
+    uint32_t top = 0;
+    constexpr int kChunks = 8;
+    for (uint32_t c0 = 0; c0 < chunks_wave; c0 += kChunks) {
+      uint64_t v[kChunks];
+      uint32_t dst[kChunks];
+      bool ok[kChunks];
+#pragma unroll
+      for (int q = 0; q < kChunks; ++q) {
+        const uint32_t c = c0 + q;
+        // The lane whose split holds chunk c (wave-uniform search).
+        int j = 0;
+        for (int t = 1; t < wave_splits && t < 64; ++t)
+          if (__builtin_amdgcn_readlane(chunk_pre, t) <= c) j = t;
+        const uint32_t n_j = __builtin_amdgcn_readlane(n_l, j);
+        const uint32_t i = 64 * (c - __builtin_amdgcn_readlane(chunk_pre, j)) + lane;
+        ok[q] = c < chunks_wave && i < n_j;
+        const uint64_t* src = cl.lists + (r * cl.splits + wave + kWaves * j) * cl.cap;
+        v[q] = ok[q] ? src[i] : 0ull;
+        dst[q] = wave_base + __builtin_amdgcn_readlane(n_pre, j) + i;
+      }
+#pragma unroll
+      for (int q = 0; q < kChunks; ++q)
+        if (ok[q] && dst[q] < (uint32_t)kSortCap) fs.sorted[dst[q]] = v[q];
+    }
+    for (int j = 0; j < wave_splits && j < 64; ++j) {
+      const int32_t spill = __builtin_amdgcn_readlane(spill_l, j);
+      if (spill == 0x7FFFFFFF) continue;
+      const int64_t kb = (int64_t)(wave + kWaves * j) * cl.per;
+      int64_t lo = spill, hi = kb + cl.per;
+      if (lo < vis_lo) lo = vis_lo;
+      if (hi > vis_hi) hi = vis_hi;
+      for (int64_t c0 = lo; c0 < hi; c0 += 64) {
+        const int64_t c = c0 + lane;
+        const float v = c < hi ? row[c] : 0.0f;
+        const uint32_t k = radix_key(v);
+        const bool hit = c < hi && k >= floor;
+        const uint32_t slot = wave_slot(&info[0], hit);
+        if (hit && slot < (uint32_t)kSortCap) fs.sorted[slot] = composite(v, c);
+        if (hit) top = max(top, k);
+      }
+    }
+    top = max(top, lane_xor<1>(top));
+    top = max(top, lane_xor<2>(top));
+    top = max(top, lane_xor<4>(top));
+    top = max(top, lane_xor<8>(top));
+    top = max(top, lane_xor<16>(top));
+    top = max(top, lane_xor<32>(top));
+    if (lane == 0) atomicMax(&info[1], top);
+    __syncthreads();
+    n_cand = info[0];
+    valid = n_cand <= (uint32_t)kSortCap ? prefix_slots(n_cand) : 0u;
+#pragma unroll
+    for (int j = 0; j < kSortPerThread; ++j)
+      key[j] = (valid >> j) & 1u ? fs.sorted[tid + j * kThreads] : 0ull;
+    __syncthreads();  // the sort scatters into the buffer
+  }
+  // Fewer than `count` candidates: the floor was above the count-th
+  // largest score, and scores below it are missing.
+  if (n_cand <= (uint32_t)kSortCap && n_cand >= (uint32_t)count) {
+    if (counting_sort_mask(fs, key, valid, n_cand, floor, info[1], count, emit)) return;
+    // A crowded bucket: the threshold digit from the candidates' digit
+    // histogram, then its keys split to exactly count - above (select_row's
+    // refinement).
+    __syncthreads();
+    for (int i = tid; i < kBins; i += kThreads) fs.start[i] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kSortPerThread; ++j)
+      if ((valid >> j) & 1u) atomicAdd(&fs.start[key[j] >> 53], 1u);
+    __syncthreads();
+    if (wave == 0) {
+      const Threshold t = row_threshold(fs.start, (uint32_t)count);
+      if (lane == 0) {
+        info[3] = t.digit;
+        info[4] = t.above;
+        info[5] = t.bucket;
+      }
+    }
+    __syncthreads();
+    const uint32_t d0 = info[3], above = info[4], bucket = info[5];
+    if (bucket <= (uint32_t)kRefineCap) {
+      Shared& sh = lds.sh;
+      if (tid == 0) {
+        sh.n_sel = 0;
+        sh.n_buf = 0;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < kSortPerThread; ++j) {
+        const bool live = (valid >> j) & 1u;
+        const uint32_t digit = (uint32_t)(key[j] >> kShift[0]);
+        const bool is_above = live && digit > d0;
+        const bool in_bucket = live && digit == d0;
+        const uint32_t slot_above = wave_slot(&sh.n_sel, is_above);
+        const uint32_t slot_bucket = wave_slot(&sh.n_buf, in_bucket);
+        if (is_above && slot_above < (uint32_t)kMaxK) sh.sel[slot_above] = key[j];
+        if (in_bucket && slot_bucket < (uint32_t)kRefineCap) sh.buf[slot_bucket] = key[j];
+      }
+      __syncthreads();
+      const uint32_t remaining = (uint32_t)count - above;
+      refine_buffer(sh, (uint64_t)d0 << kShift[0], kShift[0], remaining, bucket == remaining, bucket);
+      __syncthreads();
+      sort_selected(sh, count);
+      for (int i = tid; i < count; i += kThreads) emit(i, sh.sel[i]);
+      return;
+    }
+    // A threshold digit of more than kRefineCap keys: from the full row.
+  }
+  // The row's exact scores (every column), then the selection over them.
+  __syncthreads();
+  uint8_t(*digits)[logits_core::kDigits][logits_core::kDim] =
+      reinterpret_cast<uint8_t(*)[logits_core::kDigits][logits_core::kDim]>(
+          reinterpret_cast<uint8_t*>(&lds) +
+          wave * logits_core::kQueriesPerWave * logits_core::kDigits * logits_core::kDim);
+  logits_core::row_scores(li.q, li.k, li.w, li.kscale, li.q_fold, r, (int32_t)vis_lo,
+                          (int32_t)vis_hi, cols, row, digits, wave, kThreads / 64);
+  __syncthreads();
+  select_row<kResidentVecSmall>(lds.sh, scores, cols, ld, total_count, values, ids, out_ld,
+                                nullptr, r, 0, 1);
 }
 }  // namespace
 }  // namespace dsa
@@ -1378,6 +1696,28 @@ extern "C" int dsa_topk_radix_digits(const float* scores, int64_t rows, int64_t 
   DSA_CHECK_LAUNCH("exact top-k");
   return kOk;
 }
+
+namespace dsa {
+
+int topk_from_candidates(const uint8_t* q, const uint8_t* k, const float* weights,
+                         const float* kscale, const int32_t* starts, const int32_t* ends,
+                         int64_t query_start, const float* q_fold, float* scores, int64_t rows,
+                         int64_t columns, int64_t ld, int64_t topk, float* values,
+                         int32_t* indices, int64_t out_ld, const uint32_t* floors,
+                         const uint32_t* records, const uint64_t* lists, int64_t splits,
+                         int64_t per, int64_t cap, hipStream_t stream) {
+  DSA_CHECK_ARG(splits >= 1 && splits <= kMaxCandidateSplits, "too many key splits");
+  DSA_CHECK_ARG(columns < (int64_t)0x7FFFFFFF && rows < 0x7FFFFFFF, "too many rows or columns");
+  const int64_t count = topk < columns ? topk : columns;
+  hipLaunchKernelGGL(topk_candidates, dim3((unsigned)rows), dim3(kThreads), 0, stream, scores,
+                     columns, ld, (int)count, values, indices, out_ld,
+                     CandidateLists{floors, records, lists, splits, per, cap},
+                     LogitsInputs{q, k, weights, kscale, starts, ends, query_start, q_fold});
+  DSA_CHECK_LAUNCH("indexer top-k from candidates");
+  return kOk;
+}
+
+}  // namespace dsa
 
 namespace dsa {
 namespace {

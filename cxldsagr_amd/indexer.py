@@ -212,11 +212,89 @@ def logits_topk(q, k, weights, kscale, query_start, topk, *, _bounds=None, _q_fo
     return scores, values, indices
 
 
-def _logits_launch_args(q, k, weights, kscale, query_start, bounds, q_fold):
+def select_topk(q, k, weights, kscale, query_start, topk, *, _bounds=None, _q_fold=None,
+                _list_cap=0, _floors=None, _floors_ready=False):
+    """The indexer step's top-k without the score matrix: ``(values, indices)``
+    equal, bit for bit, to ``exact_topk(logits(q, k, weights, kscale,
+    query_start), topk)`` for every input.
+
+    Three launches (``dsa_indexer_select_fp8``): per-row floors estimated from
+    ~1/64 of each row's scores; the logits kernel writing only the composite
+    top-k keys of the scores at or above the floor (per key split, ~4K per
+    row at 64K keys, instead of every score); the exact top-k of those
+    candidates, which recomputes a row in full when it holds fewer than
+    ``min(topk, N)`` of them. This replaces the reference's ``logits`` then
+    ``exact_topk`` (``models/deepseek_v32/attention.py:338-363``); the
+    per-query score buckets of its fused ECHO kernel play the same role
+    (``indexer/csrc/echo_logits.cuh:497-561``).
+
+    ``_floors_ready``: the floors are already in this stream's workspace
+    (``select_floors_buffer``; the layer prologue writes them), so the
+    floors launch is skipped. ``_list_cap`` (candidate slots per row and key
+    split, 0 = default) and ``_floors`` (uint32 ``[Q]`` radix keys replacing
+    the estimated floors) are test hooks: small lists force spills, high
+    floors force the recompute.
+    """
+    if type(topk) is not int or not 1 <= topk <= 2048:
+        raise ValueError("k must be an integer in [1, 2048]")
+    args, q_fold, _, _operands = _logits_launch_args(q, k, weights, kscale, query_start, _bounds,
+                                                     _q_fold, allocate_output=False)
+    rows, columns, device = len(q), len(k), q.device
+    count = min(topk, columns)
+    values = torch.empty((rows, count), dtype=torch.float32, device=device)
+    indices = torch.empty((rows, count), dtype=torch.int32, device=device)
+    head = args[:9]  # q, k, weights, kscale, starts, ends, query_start, rows, columns
+    with torch.cuda.device(device):
+        stream = _native.stream_of(device)
+        workspace, scores = _select_buffers(device, stream, rows, columns, _list_cap)
+        if _floors is None and _list_cap == 0 and not _floors_ready:
+            _native.call("dsa_indexer_select_fp8", *head, _native.ptr(q_fold), _native.ptr(scores),
+                         topk, _native.ptr(values), _native.ptr(indices), count,
+                         _native.ptr(workspace), workspace.numel(), stream)
+            return values, indices
+        floors = workspace[:4 * rows].view(torch.int32)
+        if not _floors_ready:
+            _native.call("dsa_indexer_floors_fp8", *head, topk, _native.ptr(floors), stream)
+        if _floors is not None:
+            _check_tensor(_floors, (rows,), torch.int32, device, "_floors")
+            floors.copy_(_floors)
+        _native.call("dsa_indexer_logits_fp8_emit", *head, scores.shape[1], _native.ptr(q_fold),
+                     _native.ptr(scores), _list_cap, _native.ptr(workspace), workspace.numel(),
+                     stream)
+        _native.call("dsa_indexer_emit_topk", *head, _native.ptr(q_fold), _native.ptr(scores), topk,
+                     _native.ptr(values), _native.ptr(indices), count, _list_cap,
+                     _native.ptr(workspace), workspace.numel(), stream)
+    return values, indices
+
+
+def select_floors_buffer(device, rows, columns):
+    """The floors (int32 ``[rows]``) of the current stream's ``select_topk``
+    workspace for ``rows`` x ``columns``: a producer that computes the floors
+    itself (``dsa_layer_prologue_floors_fp8``) writes them here, then calls
+    ``select_topk(..., _floors_ready=True)``."""
+    with torch.cuda.device(device):
+        workspace, _ = _select_buffers(device, _native.stream_of(device), rows, columns, 0)
+    return workspace[:4 * rows].view(torch.int32)
+
+
+def select_floors(q, k, weights, kscale, query_start, topk, *, _bounds=None):
+    """The per-row floors ``select_topk`` estimates (uint32 radix keys as
+    int32 ``[Q]``; 0 for rows selected from their full scores)."""
+    args, _, _, _operands = _logits_launch_args(q, k, weights, kscale, query_start, _bounds, None,
+                                                allocate_output=False)
+    floors = torch.empty(len(q), dtype=torch.int32, device=q.device)
+    with torch.cuda.device(q.device):
+        _native.call("dsa_indexer_floors_fp8", *args[:9], topk, _native.ptr(floors),
+                     _native.stream_of(q.device))
+    return floors
+
+
+def _logits_launch_args(q, k, weights, kscale, query_start, bounds, q_fold, allocate_output=True):
     """Validation of ``echo.py:299-330`` and the kernel arguments up to ``ldo``;
     returns ``(args, q_fold, output, operands)`` with the padded output
-    allocated; ``operands`` holds the (possibly realigned) inputs the pointers
-    in ``args`` refer to, to be kept alive until the launch."""
+    allocated (None with ``allocate_output=False``); ``operands`` holds the
+    (possibly realigned) inputs the pointers in ``args`` refer to, to be kept
+    alive until the launch."""
     if q.ndim != 3 or q.shape[1:] != (64, 128) or not q.is_cuda or len(q) < 1:
         raise ValueError("ECHO requires nonempty CUDA Q[query,64,128]")
     if k.ndim != 2 or k.shape[1] != 128 or len(k) < 1:
@@ -244,7 +322,8 @@ def _logits_launch_args(q, k, weights, kscale, query_start, bounds, q_fold):
     # The kernel reads q, k and weights in 16-byte units.
     q, k, weights = (t if t.data_ptr() % 16 == 0 else t.clone() for t in (q, k, weights))
     width = padded_columns(columns)
-    output = torch.empty((rows, width), dtype=torch.float32, device=device)
+    output = (torch.empty((rows, width), dtype=torch.float32, device=device)
+              if allocate_output else None)
     args = [_native.ptr(q), _native.ptr(k), _native.ptr(weights), _native.ptr(kscale),
             _native.ptr(starts), _native.ptr(ends), query_start, rows, columns, width]
     return args, q_fold, output, (q, k, weights)
@@ -325,6 +404,28 @@ def _digit_workspace(device, stream, rows, columns):
         workspace.zero_()
     _DIGIT_WORKSPACES[key] = (workspace, rows)
     return workspace
+
+
+# Per (device, stream) workspace and score scratch of ``select_topk``: the
+# workspace needs no initialisation; the scratch holds rows stored in full and
+# spilled columns.
+_SELECT_BUFFERS = {}
+
+
+def _select_buffers(device, stream, rows, columns, list_cap):
+    key = (device.index, stream.value)
+    workspace, scores = _SELECT_BUFFERS.get(key, (None, None))
+    needed = ctypes.c_int64()
+    _native.call("dsa_indexer_select_workspace_bytes", rows, columns, list_cap,
+                 ctypes.byref(needed))
+    if workspace is None or workspace.numel() < needed.value:
+        # 256-byte alignment: the caching allocator's blocks are 512-aligned.
+        workspace = torch.empty(needed.value, dtype=torch.uint8, device=device)
+    width = padded_columns(columns)
+    if scores is None or scores.numel() < rows * width:
+        scores = torch.empty(rows * width, dtype=torch.float32, device=device)
+    _SELECT_BUFFERS[key] = (workspace, scores)
+    return workspace, scores[:rows * width].view(rows, width)
 
 
 def _topk_workspace(device, stream, rows):

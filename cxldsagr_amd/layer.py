@@ -7,10 +7,11 @@ Follows the stage order of the reference's ``EchoAttentionRunner._forward``
    in the same kernel (``models/deepseek_v32/projections.py:241-244``; A2);
 2. quantise the new tokens' index K straight into the resident index cache
    (``attention.py:323-326``; A3);
-3. fp8 logits with the causal ``-inf`` tail over the aligned score storage
-   (``attention.py:338-353``; A4), counting each row's scores by radix digit;
-4. exact top-k from those counts (``attention.py:358-370``; A6), fused with
-   step 3 through ``indexer.logits_topk``;
+3. fp8 logits with the causal ``-inf`` tail (``attention.py:338-353``; A4),
+   written only as top-k candidates: the scores at or above a per-row floor
+   estimated from a sample of the row;
+4. exact top-k of those candidates (``attention.py:358-370``; A6), fused
+   with step 3 through ``indexer.select_topk`` (no score matrix);
 5. append the new tokens' KV records (quantise-on-append into the fp8 paged
    cache, or a bf16 copy) (``attention.py:400-401``);
 6. sparse MLA over the selection (``attention.py:201-235``; A7).
@@ -108,8 +109,8 @@ class DSALayer:
         q8, _, weights = indexer.quantize_index_folded(index_q, weights)
         indexer.quantize_into(index_k, self.index_keys[position:end],
                               self.index_scales[position:end])
-        _, _, ids = indexer.logits_topk(q8, self.index_keys[:end], weights,
-                                        self.index_scales[:end], position, self.topk)
+        _, ids = indexer.select_topk(q8, self.index_keys[:end], weights,
+                                     self.index_scales[:end], position, self.topk)
         return TokenSelection(ids)
 
     def consume(self, q, selection, kv, position):
@@ -128,12 +129,15 @@ class DSALayer:
                 and kv.dtype == torch.bfloat16 and tuple(kv.shape) == (rows, attention.QK_DIM)
                 and all(t.device == self.device for t in (index_q, index_k, weights, kv)))
 
-    def _prologue(self, index_q, index_k, weights, kv, position):
+    def _prologue(self, index_q, index_k, weights, kv, position, floors=None):
         """Q quantisation + weight fold, new index K into the cache and the new
         KV records into the fp8 paged cache, in one launch
         (``dsa_layer_prologue_fp8``; the same bits as the three separate
         operators). Also returns the partial folded queries ``[rows, 4, 128]``
-        that let the logits kernel skip forming them (same logits bits)."""
+        that let the logits kernel skip forming them (same logits bits). With
+        ``floors`` (int32 ``[rows]``), the same launch also estimates the
+        candidate top-k's per-row floors into it
+        (``dsa_layer_prologue_floors_fp8``)."""
         rows = len(index_q)
         end = position + rows
         index_q, index_k, weights, kv = (t.contiguous() for t in (index_q, index_k, weights, kv))
@@ -144,14 +148,15 @@ class DSALayer:
         q_fold = torch.empty((rows, 4, 128), dtype=torch.float32, device=self.device)
         with torch.cuda.device(self.device):
             _native.call(
-                "dsa_layer_prologue_fp8",
+                "dsa_layer_prologue_floors_fp8",
                 _native.ptr(index_q), rows * 64, _native.ptr(weights), _native.ptr(q8),
                 _native.ptr(q_scales), _native.ptr(folded), _native.ptr(q_fold),
                 _native.ptr(index_k), rows, _native.ptr(self.index_keys[position:end]),
                 _native.ptr(self.index_scales[position:end]),
                 _native.ptr(kv), rows, position, _native.ptr(self.page_table),
                 self.kv_cache.shape[0], _native.ptr(self.kv_cache), None,
-                _native.stream_of(self.device),
+                _native.ptr(self.index_keys), _native.ptr(self.index_scales), position, self.topk,
+                _native.ptr(floors), _native.stream_of(self.device),
             )
         return q8, folded, q_fold
 
@@ -172,17 +177,18 @@ class DSALayer:
         end = position + rows
         if end > self.capacity or len(q) != rows or len(kv) != rows or len(index_k) != rows:
             raise ValueError("query batch exceeds the layer capacity or inputs disagree in length")
-        q_fold = None
+        q_fold = floors = None
         if self._fused_prologue_applies(index_q, index_k, weights, kv):
-            q8, folded, q_fold = self._prologue(index_q, index_k, weights, kv, position)
+            floors = indexer.select_floors_buffer(self.device, rows, end)
+            q8, folded, q_fold = self._prologue(index_q, index_k, weights, kv, position, floors)
         else:
             indexer.quantize_into(index_k, self.index_keys[position:end],
                                   self.index_scales[position:end])
             q8, _, folded = indexer.quantize_index_folded(index_q, weights)
             self._append_kv(kv, position)
-        _, _, ids = indexer.logits_topk(q8, self.index_keys[:end], folded,
-                                        self.index_scales[:end], position, self.topk,
-                                        _q_fold=q_fold)
+        _, ids = indexer.select_topk(q8, self.index_keys[:end], folded,
+                                     self.index_scales[:end], position, self.topk,
+                                     _q_fold=q_fold, _floors_ready=floors is not None)
         selection = TokenSelection(ids)
         out = self._attend(q, ids, end)
         self.written = end
@@ -211,9 +217,9 @@ class DSALayer:
             token_offset=position)
         if not paged:
             self._append_kv(kv, position)
-        _, _, ids = indexer.logits_topk(q8, self.index_keys[:end], folded,
-                                        self.index_scales[:end], position, self.topk,
-                                        _q_fold=q_fold)
+        _, ids = indexer.select_topk(q8, self.index_keys[:end], folded,
+                                     self.index_scales[:end], position, self.topk,
+                                     _q_fold=q_fold)
         out = self._attend(q, ids, end)
         self.written = end
         return out, TokenSelection(ids)
@@ -297,8 +303,8 @@ class OffloadDSALayer:
             raise ValueError("query batch exceeds the layer capacity or inputs disagree in length")
         q8, _, folded = indexer.quantize_index_folded(index_q, weights)
         indexer.quantize_into(index_k, self.index_keys[position:end], self.index_scales[position:end])
-        _, _, ids = indexer.logits_topk(q8, self.index_keys[:end], folded,
-                                        self.index_scales[:end], position, self.topk)
+        _, ids = indexer.select_topk(q8, self.index_keys[:end], folded,
+                                     self.index_scales[:end], position, self.topk)
         return ids
 
     def consume(self, q, ids, *, written, transient_start=None):

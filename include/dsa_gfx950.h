@@ -204,6 +204,68 @@ int dsa_indexer_topk_fp8(const void* q, const void* k, const float* weights, con
                          int64_t out_ld, void* workspace, int64_t workspace_bytes,
                          hipStream_t stream);
 
+/*
+ * A4 + A6 fused without the score matrix (the SURVEY (f)1 indexer step that
+ * writes only top-k candidates): the same values and indices as
+ * dsa_indexer_logits_fp8 followed by dsa_topk_radix over its [rows, columns]
+ * scores, bit for bit, for every input. Replaces the reference's logits()
+ * followed by exact_topk() in the indexer step
+ * (models/deepseek_v32/attention.py:338-363, echo.py:299-410,
+ * selection.py:62-113); the reference's ECHO kernel likewise buckets each
+ * query's scores against a per-query offset estimated ahead of the call
+ * (indexer/csrc/echo_logits.cuh:497-561, indexer/prefetch_hint.py:38-85).
+ *
+ * Three launches, also available one by one:
+ *  - dsa_indexer_floors_fp8: per row a floor (an fp32 radix key) estimated
+ *    from the row's scores at about 1/64 of its visible columns, so that the
+ *    row almost surely holds at least min(topk, columns) scores at or above
+ *    it; 0 for rows of fewer than 8192 visible columns;
+ *  - dsa_indexer_logits_fp8_emit: the logits kernel writes, per row and key
+ *    split, only the composite keys (radix(v) << 32 | ~column) of the scores
+ *    at or above the row's floor into the workspace lists; a split whose list
+ *    fills up stores the rest of its scores into `scores` instead, and rows
+ *    with floor 0 are stored there in full;
+ *  - dsa_indexer_emit_topk: per row, the exact top-k of the candidates when
+ *    there are at least min(topk, columns) of them (they then hold the row's
+ *    top); otherwise the row's scores are recomputed into `scores` with the
+ *    logits kernel's arithmetic and selected from (exact, slow, rare).
+ * `scores` is f32 [rows, ldo] with ldo = columns rounded up to 256: scratch
+ * that holds only stored rows and spilled columns afterwards. q_fold as for
+ * dsa_indexer_logits_fp8_folded (may be NULL). list_cap = 0 picks the list
+ * length per (row, split) (an eighth of the split); a smaller one makes
+ * splits spill earlier (for tests). The workspace (256-byte aligned, size
+ * from dsa_indexer_select_workspace_bytes with the same rows, columns and
+ * list_cap on the same device) holds floors u32 [rows], records and lists;
+ * it needs no initialisation, and calls that overlap on different streams
+ * need distinct workspaces and score buffers. A caller may overwrite the
+ * floors between the first two launches (a floor too high for a row only
+ * sends that row to the recompute).
+ */
+int dsa_indexer_select_workspace_bytes(int64_t rows, int64_t columns, int64_t list_cap,
+                                       int64_t* bytes);
+int dsa_indexer_floors_fp8(const void* q, const void* k, const float* weights, const float* kscale,
+                           const int32_t* starts, const int32_t* ends, int64_t query_start,
+                           int64_t rows, int64_t columns, int64_t topk, uint32_t* floors,
+                           hipStream_t stream);
+int dsa_indexer_logits_fp8_emit(const void* q, const void* k, const float* weights,
+                                const float* kscale, const int32_t* starts, const int32_t* ends,
+                                int64_t query_start, int64_t rows, int64_t columns, int64_t ldo,
+                                const float* q_fold, float* scores, int64_t list_cap,
+                                void* workspace, int64_t workspace_bytes, hipStream_t stream);
+int dsa_indexer_emit_topk(const void* q, const void* k, const float* weights, const float* kscale,
+                          const int32_t* starts, const int32_t* ends, int64_t query_start,
+                          int64_t rows, int64_t columns, const float* q_fold, float* scores,
+                          int64_t topk, float* values, int32_t* indices, int64_t out_ld,
+                          int64_t list_cap, const void* workspace, int64_t workspace_bytes,
+                          hipStream_t stream);
+/* The three launches above in order, with list_cap = 0 (floors at the start
+ * of the workspace). */
+int dsa_indexer_select_fp8(const void* q, const void* k, const float* weights, const float* kscale,
+                           const int32_t* starts, const int32_t* ends, int64_t query_start,
+                           int64_t rows, int64_t columns, const float* q_fold, float* scores,
+                           int64_t topk, float* values, int32_t* indices, int64_t out_ld,
+                           void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
 
 /*
  * A8 producer - pack bf16 [tokens, 576] (512 latent + 64 RoPE) into the
@@ -238,6 +300,27 @@ int dsa_layer_prologue_fp8(const void* q, int64_t q_rows, const float* weights, 
                            int64_t k_rows, void* k_codes, float* k_scales, const void* kv,
                            int64_t tokens, int64_t token_offset, const int32_t* page_table,
                            int64_t pages, void* cache, int32_t* status, hipStream_t stream);
+
+/*
+ * dsa_layer_prologue_fp8 that also writes the per-row floors of the
+ * candidate top-k (as dsa_indexer_floors_fp8 estimates them) into `floors`
+ * (uint32 [q_rows / 64]), for a layer step whose queries are the causal rows
+ * history .. history + q_rows / 64 - 1 over the resident index keys
+ * key_cache e4m3 [history + ..., 128] / key_cache_scales f32: each row's
+ * floor is sampled from columns [0, history) (the new keys are written by
+ * the same launch). Pass the select workspace's floors (its first bytes) and
+ * then call dsa_indexer_logits_fp8_emit and dsa_indexer_emit_topk. No
+ * reference counterpart (the reference has no floors); the same quantised
+ * outputs as dsa_layer_prologue_fp8.
+ */
+int dsa_layer_prologue_floors_fp8(const void* q, int64_t q_rows, const float* weights,
+                                  void* q_codes, float* q_scales, float* w_folded, float* q_fold,
+                                  const void* k, int64_t k_rows, void* k_codes, float* k_scales,
+                                  const void* kv, int64_t tokens, int64_t token_offset,
+                                  const int32_t* page_table, int64_t pages, void* cache,
+                                  int32_t* status, const void* key_cache,
+                                  const float* key_cache_scales, int64_t history, int64_t topk,
+                                  uint32_t* floors, hipStream_t stream);
 
 /*
  * Indexer input producers: the indexer half of the projection step after
@@ -383,6 +466,18 @@ int dsa_pool_recall_pipelined(const int32_t* indices, int64_t n, const int32_t* 
                               int32_t* status, int32_t* physical, int64_t keep_floor,
                               int64_t candidate_offset, hipStream_t stream,
                               hipStream_t gather_stream);
+
+/*
+ * A10 release of a session's host rows from one layer's pool maps
+ * (cache/sparse_token_pool.py:697-710, release_ids): for every host row of
+ * the session's pages (page_table int32 [pages], 64 rows per page) that is
+ * resident, its slot is freed (d2h = MISSING, priority = -1) and h2d of the
+ * row becomes MISSING. A page outside [0, host_rows / 64) or an h2d entry
+ * outside [1, slots] ORs 1 into *status (may be NULL) and is skipped.
+ */
+int dsa_pool_release_rows(const int32_t* page_table, int64_t pages, int64_t host_rows,
+                          int32_t* h2d, int64_t* d2h, int64_t* priority, int64_t slots,
+                          int32_t* status, hipStream_t stream);
 
 #ifdef __cplusplus
 }
