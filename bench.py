@@ -153,7 +153,7 @@ def in_layer_stage_us(torch, layer, history, tokens, topk, iters, args):
              for _ in range(iters)]
     rows = len(index_q)
     workspace = select_workspace(rows, tokens, layer.device)
-    floors = workspace[:4 * rows].view(torch.int32)
+    floors = workspace[:8 * rows].view(torch.int32).view(rows, 2)
 
     def prologue():
         if fused:
@@ -187,7 +187,7 @@ def in_layer_stage_us(torch, layer, history, tokens, topk, iters, args):
         ev[5].record(stream)
     torch.cuda.synchronize()
     # Candidates listed per row (records [rows][splits][2] after the floors).
-    records_at = (4 * rows + 255) // 256 * 256
+    records_at = (8 * rows + 255) // 256 * 256
     width = (tokens + 255) // 256 * 256
     cus = torch.cuda.get_device_properties(layer.device).multi_processor_count
     qgroups = (rows + 15) // 16

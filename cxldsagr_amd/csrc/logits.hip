@@ -81,7 +81,7 @@ enum Mode : int { kModePlain = 0, kModeCount = 1, kModeEmit = 2 };
 // listed, and the first column from which the split's scores of that row
 // were stored in full into the score matrix instead (INT32_MAX: none).
 struct EmitArgs {
-  const uint32_t* floors;  // [rows] radix-key floor per row; 0: store the row in full
+  const uint32_t* floors;  // [rows][2] radix-key floors per row (row_floor); 0: store the row in full
   uint64_t* lists;         // [rows][splits][cap]
   uint32_t* records;       // [rows][splits][2]
   int32_t cap;
@@ -312,8 +312,8 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
   if constexpr (kEmit) {
 #pragma unroll
     for (int j = 0; j < kQueriesPerWave; ++j) {
-      floor_own[j] = qw + j < rows ? emit.floors[qw + j] : 0u;
-      floor_w0[j] = q0 + j < rows ? emit.floors[q0 + j] : 0u;
+      floor_own[j] = qw + j < rows ? row_floor(emit.floors, qw + j) : 0u;
+      floor_w0[j] = q0 + j < rows ? row_floor(emit.floors, q0 + j) : 0u;
     }
   }
 #pragma unroll
@@ -527,7 +527,7 @@ __global__ __launch_bounds__(kThreads, 1) void logits_fp8_mfma(
       const int64_t qi = q0 + i;
       if (qi >= rows) continue;
       if constexpr (kEmit) {
-        if (emit.floors[qi] != 0u) continue;
+        if (row_floor(emit.floors, qi) != 0u) continue;
       }
       for (int64_t key = tail + lane; key < ke; key += 64) out[qi * ldo + key] = neg_inf;
     }
@@ -591,7 +591,7 @@ __global__ __launch_bounds__(kFloorThreads) void index_floors(
   __shared__ uint32_t keys[kFloorMaxSamples];
   __shared__ uint32_t hist[2048];
   __shared__ uint32_t wave_sums[kFloorWaves];
-  __shared__ uint32_t result[2];
+  __shared__ uint32_t result[4];
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -603,19 +603,19 @@ __global__ __launch_bounds__(kFloorThreads) void index_floors(
   if (e > columns) e = columns;
   const int64_t visible = e > s ? e - s : 0;
   if (visible < kFloorMinVisible) {
-    if (tid == 0) floors[row] = 0u;
+    if (tid < 2) floors[2 * row + tid] = 0u;
     return;
   }
   const int64_t n = floor_samples(visible, kFloorMaxSamples);
   const int64_t stride = visible / n;  // >= 2
   const uint32_t rank = floor_rank(n, count, visible);
   if (rank > (uint32_t)n) {
-    if (tid == 0) floors[row] = 0u;
+    if (tid < 2) floors[2 * row + tid] = 0u;
     return;
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) hist[4 * tid + j] = 0;
-  if (tid < 2) result[tid] = 0;
+  if (tid < 4) result[tid] = 0;
   // Sample m is column s + m stride + stride / 2. Wave w scores the 16-sample
   // groups w, w + waves, ... in batches of kFloorBatch whose key loads are
   // issued together: four MFMAs (16 heads each) per group, then
@@ -661,7 +661,7 @@ __global__ __launch_bounds__(kFloorThreads) void index_floors(
   }
   __syncthreads();
   const uint32_t floor = floor_of_samples<kFloorThreads>(keys, (int)n, rank, hist, wave_sums, result);
-  if (tid == 0) floors[row] = floor;
+  if (tid < 2) floors[2 * row + tid] = floor;  // one estimate, kept twice
 }
 
 }  // namespace
@@ -737,7 +737,7 @@ int logits_launch(const void* q, const void* k, const float* weights, const floa
 }
 
 // Workspace of the candidate top-k (256-byte aligned parts): floors u32
-// [rows], records u32 [rows][splits][2], lists u64 [rows][splits][cap].
+// [rows][2], records u32 [rows][splits][2], lists u64 [rows][splits][cap].
 struct EmitLayout {
   SplitPlan plan;
   int64_t cap;
@@ -758,7 +758,7 @@ EmitLayout emit_layout(int64_t rows, int64_t columns, int64_t list_cap) {
   cap = (cap + 63) / 64 * 64;
   if (cap < 64) cap = 64;
   l.cap = cap;
-  l.records_offset = round256(rows * 4);
+  l.records_offset = round256(rows * 8);
   l.lists_offset = l.records_offset + round256(rows * l.plan.splits * 8);
   l.bytes = l.lists_offset + rows * l.plan.splits * cap * 8;
   return l;

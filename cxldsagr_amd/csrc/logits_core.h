@@ -211,15 +211,41 @@ __device__ __forceinline__ int64_t floor_samples(int64_t span, int64_t max_sampl
   return n < kFloorMinSamples ? kFloorMinSamples : n > max_samples ? max_samples : n;
 }
 
-__device__ __forceinline__ uint32_t floor_rank(int64_t n, int count, int64_t visible) {
+__device__ __forceinline__ uint32_t floor_rank(int64_t n, int count, int64_t visible,
+                                               float sigmas = 6.0f) {
   const float expected = (float)n * (float)count / (float)visible;
-  return (uint32_t)ceilf(expected + 6.0f * sqrtf(expected)) + 2u;
+  return (uint32_t)ceilf(expected + sigmas * sqrtf(expected)) + 2u;
+}
+
+// A row's floor is kept as two estimates, floors[2 row] and floors[2 row + 1]
+// (from disjoint halves of its sample, or the same value twice), and is
+// their minimum: it is too high only when both are. 0 = no floor (the row is
+// selected from its full scores).
+__device__ __forceinline__ uint32_t row_floor(const uint32_t* __restrict__ floors, int64_t row) {
+  const uint32_t a = floors[2 * row], b = floors[2 * row + 1];
+  return a < b ? a : b;
 }
 
 // Radix select in LDS by a work-group of kBlock threads: the digit d (of
 // `width` bits at `shift`) of the `rank`-th largest of the n keys whose bits
 // above shift + width equal `prefix` (hist has 2048 entries, zero on entry
 // and on exit). Returns the digit and reduces `rank` to the rank inside it.
+// Inclusive suffix sum over the wave (lane l: the sum over lanes >= l) with
+// VALU lane moves: DPP row shifts inside each 16-lane row, then the totals of
+// the higher rows.
+__device__ __forceinline__ uint32_t wave_suffix_sum(uint32_t v) {
+  const int lane = threadIdx.x & 63;
+  // row_shl:k (0x100 + k): lane l reads lane l + k of its row, 0 past the row.
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x101, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x102, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x104, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x108, 0xF, 0xF, false);
+  const uint32_t r1 = __builtin_amdgcn_readlane(v, 16), r2 = __builtin_amdgcn_readlane(v, 32),
+                 r3 = __builtin_amdgcn_readlane(v, 48);
+  const int row = lane >> 4;
+  return v + (row < 1 ? r1 : 0u) + (row < 2 ? r2 : 0u) + (row < 3 ? r3 : 0u);
+}
+
 template <int kBlock>
 __device__ uint32_t floor_digit(const uint32_t* __restrict__ keys, int n, uint32_t prefix,
                                 int shift, int width, uint32_t* __restrict__ hist,
@@ -245,12 +271,7 @@ __device__ uint32_t floor_digit(const uint32_t* __restrict__ keys, int n, uint32
     c[j] = hist[kPer * tid + j];
     own += c[j];
   }
-  uint32_t incl = own;  // bins of this thread and the higher threads of its wave
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const uint32_t o = __shfl_down(incl, d);
-    if (lane + d < 64) incl += o;
-  }
+  const uint32_t incl = wave_suffix_sum(own);  // this thread's and the higher threads' bins
   if (lane == 0) wave_sums[wave] = incl;
   __syncthreads();
   uint32_t above = incl - own;
@@ -271,7 +292,8 @@ __device__ uint32_t floor_digit(const uint32_t* __restrict__ keys, int n, uint32
 }
 
 // The floor from n sample radix keys in LDS (hist zero on entry and exit):
-// the rank-th largest key to two 11-bit digits; 0 at or below -inf.
+// the rank-th largest key to two 11-bit digits (below it by less than 2^10
+// in radix order); 0 at or below the radix key of -inf.
 template <int kBlock>
 __device__ __forceinline__ uint32_t floor_of_samples(const uint32_t* __restrict__ keys, int n,
                                                      uint32_t rank, uint32_t* __restrict__ hist,

@@ -297,24 +297,29 @@ __global__ __launch_bounds__(256) void kv_pack_fp8(const uint16_t* __restrict__ 
   pack_tokens(blockIdx.x, kv, tokens, token_offset, page_table, pages, cache, status);
 }
 
-// Floors of the candidate top-k (logits_core.h: floor_rank,
-// floor_of_samples) for the layer step, one 256-thread block per query row
-// i: the row's 64 index-Q head rows quantised here (the A1 scale; the e4m3
-// codes by the hardware conversion - the floor is an estimate, and the
-// exact codes are the Q blocks'), scored at n sample columns of the resident
-// history [0, history) - the new keys are being written by this launch -
-// with four MFMAs per 16 samples (each wave a quarter of the samples, all
-// 64 heads; the MFMAs of one group are issued before the previous group's
-// head sum). The sample loads are issued first.
-constexpr int kPrologueFloorSamples = 2048;
-constexpr int kPrologueFloorBatch = 16;  // 16-sample groups per wave in flight together
+// Floors of the candidate top-k (logits_core.h: floor_rank, row_floor,
+// floor_of_samples) for the layer step: two 256-thread blocks per query row
+// i, block h scoring the interleaved half h of the row's sample columns
+// (2m + h for m < n/2) of the resident history [0, history) - the new keys
+// are being written by this launch - and writing its own estimate to
+// floors[2i + h]; the row's floor is the smaller of the two, which is too
+// high only when both are, so each half takes a 3.5 sigma margin. Each block
+// quantises the row's 64 index-Q head rows (the A1 scale; the e4m3 codes by
+// the hardware conversion - the floor is an estimate, and the exact codes
+// are the Q blocks') and scores its samples with four MFMAs per 16 (each
+// wave a quarter of them, all 64 heads; the MFMAs of one group are issued
+// before the previous group's head sum). The query loads are issued first,
+// then the sample loads.
+constexpr int kPrologueFloorSamples = 2048;  // per row (both halves)
+constexpr int kPrologueFloorBatch = 8;  // 16-sample groups per wave in flight together
+constexpr float kPrologueFloorSigmas = 3.5f;
 
 struct FloorArgs {
   const uint8_t* keys;      // resident index-K codes [history + ...][128]
   const float* key_scales;  // [history + ...]
   int64_t history;          // sample columns [0, history); row i sees history + i + 1
   int count;                // min(topk, columns)
-  uint32_t* floors;         // [rows]
+  uint32_t* floors;         // [rows][2]
 };
 
 // Max over the four consecutive lanes of a quad (DPP quad permutes).
@@ -325,7 +330,7 @@ __device__ __forceinline__ uint32_t quad_max(uint32_t v) {
   return v > o ? v : o;
 }
 
-__device__ void prologue_floor(int64_t i, const uint16_t* __restrict__ q,
+__device__ void prologue_floor(int64_t i, int half, const uint16_t* __restrict__ q,
                                const float* __restrict__ weights, const FloorArgs fa) {
   using namespace logits_core;
   __shared__ __align__(16) uint32_t codes[kHeads][36];  // 144-byte rows: fewer bank conflicts
@@ -333,50 +338,59 @@ __device__ void prologue_floor(int64_t i, const uint16_t* __restrict__ q,
   __shared__ uint32_t keys[kPrologueFloorSamples];
   __shared__ uint32_t hist[2048];
   __shared__ uint32_t wave_sums[4];
-  __shared__ uint32_t result[2];
+  __shared__ uint32_t result[4];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int group = lane >> 4;
   const int col = lane & 15;
   const int32_t history = (int32_t)fa.history;  // < 2^25 (the launcher checks)
+  uint32_t* out = fa.floors + 2 * i + half;
   if (history < kFloorMinVisible) {
-    if (tid == 0) fa.floors[i] = 0u;
+    if (tid == 0) *out = 0u;
     return;
   }
-  const int n = (int)floor_samples(history, kPrologueFloorSamples);
-  const int stride = history / n;  // >= 2
-  const uint32_t rank = floor_rank(n, fa.count, (int64_t)history + i + 1);
+  const int n = (int)floor_samples(history, kPrologueFloorSamples) / 2;  // this half's
+  const int stride = history / (2 * n);  // >= 2
+  const uint32_t rank = floor_rank(n, fa.count, (int64_t)history + i + 1, kPrologueFloorSigmas);
   if (rank > (uint32_t)n) {
-    if (tid == 0) fa.floors[i] = 0u;
+    if (tid == 0) *out = 0u;
     return;
   }
   const int groups = n / 16;
-  // Sample m is column m stride + stride / 2; wave w scores groups w, w + 4, ...
+  // Sample m of this half is column (2m + half) stride + stride / 2; wave w
+  // scores groups w, w + 4, ...
   v8i b[kPrologueFloorBatch];
   float ks[kPrologueFloorBatch];
   auto load_batch = [&](int g0) {
 #pragma unroll
     for (int j = 0; j < kPrologueFloorBatch; ++j) {
       const int g = g0 + 4 * j;
-      const uint32_t key = (uint32_t)((g < groups ? 16 * g + col : col) * stride + stride / 2);
+      const uint32_t key = (uint32_t)((2 * (g < groups ? 16 * g + col : col) + half) * stride + stride / 2);
       const v4u* src = reinterpret_cast<const v4u*>(fa.keys + key * (uint32_t)kDim + 32u * group);
       const v4u lo = src[0], hi = src[1];
       b[j] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
       ks[j] = fa.key_scales[key];
     }
   };
+  // The query loads first (the quantisation waits for them alone), then the
+  // sample loads (the MFMAs wait for them after the quantisation).
+  uint4 qraw[4];
+  {
+    const uint4* src = reinterpret_cast<const uint4*>(q + ((i * kHeads + (tid >> 2)) * kDim + 32 * (tid & 3)));
+#pragma unroll
+    for (int c = 0; c < 4; ++c) qraw[c] = src[c];
+  }
   load_batch(wave);
   // Quantise the row's heads: thread t takes head t / 4, dims 32 (t % 4) ..
   // + 31 (the row amax over its four threads).
   {
     const int h = tid >> 2, part = tid & 3;
-    const uint4* src = reinterpret_cast<const uint4*>(q + ((i * kHeads + h) * kDim + 32 * part));
     float v[32];
     uint32_t m = 0;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const uint4 raw = src[c];
+      const uint4 raw = qraw[c];
       const uint32_t words[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -405,7 +419,7 @@ __device__ void prologue_floor(int64_t i, const uint16_t* __restrict__ q,
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) hist[8 * tid + j] = 0;
-  if (tid < 2) result[tid] = 0;
+  if (tid < 4) result[tid] = 0;
   __syncthreads();
   v8i qa[4];
   float wv[16];
@@ -447,7 +461,7 @@ __device__ void prologue_floor(int64_t i, const uint16_t* __restrict__ q,
   }
   __syncthreads();
   const uint32_t floor = floor_of_samples<256>(keys, n, rank, hist, wave_sums, result);
-  if (tid == 0) fa.floors[i] = floor;
+  if (tid == 0) *out = floor;
 }
 
 // The small stages of a layer step in one launch: blocks [0, nq) quantise
@@ -455,7 +469,7 @@ __device__ void prologue_floor(int64_t i, const uint16_t* __restrict__ q,
 // [nq, nq + nk) quantise the new index-K rows into the resident cache,
 // blocks [nq + nk, nq + nk + nt) pack the new KV tokens into the fp8 paged
 // cache, and nf more blocks (when floors are asked for; placed first)
-// compute the candidate top-k's per-row floors. All are independent of
+// compute the candidate top-k's per-row floors, two blocks per row. All are independent of
 // each other.
 __global__ __launch_bounds__(256) void layer_prologue(
     const uint16_t* __restrict__ q, int64_t q_rows, const float* __restrict__ weights,
@@ -469,7 +483,7 @@ __global__ __launch_bounds__(256) void layer_prologue(
   // The floor blocks (the longest) come first in the grid, so that they
   // start at once and the short blocks fill the CUs around them.
   if ((int64_t)blockIdx.x < nf) {
-    prologue_floor(blockIdx.x, q, weights, fa);
+    prologue_floor(blockIdx.x >> 1, (int)(blockIdx.x & 1), q, weights, fa);
     return;
   }
   const int64_t b = blockIdx.x - nf;
@@ -553,7 +567,7 @@ extern "C" int dsa_layer_prologue_floors_fp8(
                   "floors need whole queries, the resident key cache (16-byte aligned) and "
                   "k in [1, 2048]");
     DSA_CHECK_ARG(history < ((int64_t)1 << 25), "the key cache must be addressable with 32-bit offsets");
-    nf = q_rows / 64;
+    nf = 2 * (q_rows / 64);  // two per query row
   }
   if (nq + nk + nt + nf == 0) return kOk;
   DSA_CHECK_ARG(nq + nk + nt + nf < 0x7FFFFFFF, "prologue too large for one launch");

@@ -1144,6 +1144,8 @@ struct FinishSort {
   uint32_t cursor[kSortBins];  // bucket counts, then scatter cursors
   uint32_t wave_sums[kThreads / 64];
   uint32_t crowded;
+  uint32_t bound;     // the bucket holding sorted position count - 1
+  uint32_t live_end;  // the end of that bucket: keys past it are not sorted
 };
 union FinishShared {
   Shared sh;
@@ -1202,22 +1204,29 @@ __device__ __forceinline__ bool counting_sort_mask(FinishSort& fs, const uint64_
     fs.start[4 * tid + j] = higher;
     fs.cursor[4 * tid + j] = higher;
     if (c4[j] > kSortBucketMax && higher < (uint32_t)count) fs.crowded = 1;
+    if (higher < (uint32_t)count && higher + c4[j] >= (uint32_t)count) {
+      fs.bound = 4 * tid + j;
+      fs.live_end = higher + c4[j];
+    }
     higher += c4[j];
   }
   __syncthreads();
   if (!fs.crowded) {
+    // Buckets below the one holding position count - 1 start at or past
+    // `count` and hold no output key: their keys are neither placed nor
+    // ranked.
+    const uint32_t bound = fs.bound, live_end = fs.live_end;
 #pragma unroll
-    for (int j = 0; j < kSortPerThread; ++j)
-      if ((valid >> j) & 1u) fs.sorted[atomicAdd(&fs.cursor[bucket_of(key[j])], 1u)] = key[j];
+    for (int j = 0; j < kSortPerThread; ++j) {
+      const uint32_t b = bucket_of(key[j]);
+      if (((valid >> j) & 1u) && b >= bound) fs.sorted[atomicAdd(&fs.cursor[b], 1u)] = key[j];
+    }
     __syncthreads();
-    // Rank inside the bucket; bucket b spans [start[b], start[b - 1]). A
-    // bucket that starts at or past `count` holds no output key: its keys
-    // (most of the threshold digit's, typically) are not ranked.
-    for (uint32_t i = tid; i < n; i += kThreads) {
+    // Rank inside the bucket; bucket b spans [start[b], start[b - 1]).
+    for (uint32_t i = tid; i < live_end; i += kThreads) {
       const uint64_t k = fs.sorted[i];
       const uint32_t b = bucket_of(k);
       const uint32_t b0 = fs.start[b], b1 = b ? fs.start[b - 1] : n;
-      if (b0 >= (uint32_t)count) continue;
       uint32_t rank = b0, j = b0;
       for (; j + 4 <= b1; j += 4) {
         const uint64_t x0 = fs.sorted[j], x1 = fs.sorted[j + 1];
@@ -1383,7 +1392,7 @@ __global__ __launch_bounds__(kThreads, 1) void topk_digit_finish(const float* __
 // work-group, the row's scores are recomputed here with the logits kernel's
 // arithmetic (logits_core.h) and selected from in full.
 struct CandidateLists {
-  const uint32_t* floors;   // [rows] the row's floor (a radix key), 0 when stored in full
+  const uint32_t* floors;   // [rows][2] the row's floor (row_floor), 0 when stored in full
   const uint32_t* records;  // [rows][splits][2]: keys listed, first spilled column
   const uint64_t* lists;    // [rows][splits][cap] composite keys
   int64_t splits, per, cap;
@@ -1415,7 +1424,7 @@ __global__ __launch_bounds__(kThreads, 1) void topk_candidates(float* __restrict
   const int wave = tid >> 6;
   const int64_t r = blockIdx.x;
   const int count = total_count < cols ? total_count : (int)cols;
-  const uint32_t floor = cl.floors[r];
+  const uint32_t floor = logits_core::row_floor(cl.floors, r);
   if (floor == 0) {
     select_row<kResidentVecSmall>(lds.sh, scores, cols, ld, total_count, values, ids, out_ld,
                                   nullptr, r, 0, 1);

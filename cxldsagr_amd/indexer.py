@@ -232,8 +232,8 @@ def select_topk(q, k, weights, kscale, query_start, topk, *, _bounds=None, _q_fo
     (``select_floors_buffer``; the layer prologue writes them), so the
     floors launch is skipped. ``_list_cap`` (candidate slots per row and key
     split, 0 = default) and ``_floors`` (uint32 ``[Q]`` radix keys replacing
-    the estimated floors) are test hooks: small lists force spills, high
-    floors force the recompute.
+    the estimated floors, as int32) are test hooks: small lists force
+    spills, high floors force the recompute.
     """
     if type(topk) is not int or not 1 <= topk <= 2048:
         raise ValueError("k must be an integer in [1, 2048]")
@@ -252,12 +252,12 @@ def select_topk(q, k, weights, kscale, query_start, topk, *, _bounds=None, _q_fo
                          topk, _native.ptr(values), _native.ptr(indices), count,
                          _native.ptr(workspace), workspace.numel(), stream)
             return values, indices
-        floors = workspace[:4 * rows].view(torch.int32)
+        floors = workspace[:8 * rows].view(torch.int32).view(rows, 2)
         if not _floors_ready:
             _native.call("dsa_indexer_floors_fp8", *head, topk, _native.ptr(floors), stream)
         if _floors is not None:
             _check_tensor(_floors, (rows,), torch.int32, device, "_floors")
-            floors.copy_(_floors)
+            floors.copy_(_floors[:, None].expand(rows, 2))
         _native.call("dsa_indexer_logits_fp8_emit", *head, scores.shape[1], _native.ptr(q_fold),
                      _native.ptr(scores), _list_cap, _native.ptr(workspace), workspace.numel(),
                      stream)
@@ -268,13 +268,14 @@ def select_topk(q, k, weights, kscale, query_start, topk, *, _bounds=None, _q_fo
 
 
 def select_floors_buffer(device, rows, columns):
-    """The floors (int32 ``[rows]``) of the current stream's ``select_topk``
+    """The floors (int32 ``[rows, 2]``: two estimates per row, the row's floor
+    being the smaller as uint32) of the current stream's ``select_topk``
     workspace for ``rows`` x ``columns``: a producer that computes the floors
     itself (``dsa_layer_prologue_floors_fp8``) writes them here, then calls
     ``select_topk(..., _floors_ready=True)``."""
     with torch.cuda.device(device):
         workspace, _ = _select_buffers(device, _native.stream_of(device), rows, columns, 0)
-    return workspace[:4 * rows].view(torch.int32)
+    return workspace[:8 * rows].view(torch.int32).view(rows, 2)
 
 
 def select_floors(q, k, weights, kscale, query_start, topk, *, _bounds=None):
@@ -282,11 +283,11 @@ def select_floors(q, k, weights, kscale, query_start, topk, *, _bounds=None):
     int32 ``[Q]``; 0 for rows selected from their full scores)."""
     args, _, _, _operands = _logits_launch_args(q, k, weights, kscale, query_start, _bounds, None,
                                                 allocate_output=False)
-    floors = torch.empty(len(q), dtype=torch.int32, device=q.device)
+    floors = torch.empty((len(q), 2), dtype=torch.int32, device=q.device)
     with torch.cuda.device(q.device):
         _native.call("dsa_indexer_floors_fp8", *args[:9], topk, _native.ptr(floors),
                      _native.stream_of(q.device))
-    return floors
+    return floors[:, 0].contiguous()
 
 
 def _logits_launch_args(q, k, weights, kscale, query_start, bounds, q_fold, allocate_output=True):

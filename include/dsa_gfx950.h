@@ -219,7 +219,8 @@ int dsa_indexer_topk_fp8(const void* q, const void* k, const float* weights, con
  *  - dsa_indexer_floors_fp8: per row a floor (an fp32 radix key) estimated
  *    from the row's scores at about 1/64 of its visible columns, so that the
  *    row almost surely holds at least min(topk, columns) scores at or above
- *    it; 0 for rows of fewer than 8192 visible columns;
+ *    it; 0 for rows of fewer than 8192 visible columns; written to
+ *    floors[2 row] and floors[2 row + 1] (uint32 [rows][2]);
  *  - dsa_indexer_logits_fp8_emit: the logits kernel writes, per row and key
  *    split, only the composite keys (radix(v) << 32 | ~column) of the scores
  *    at or above the row's floor into the workspace lists; a split whose list
@@ -235,7 +236,9 @@ int dsa_indexer_topk_fp8(const void* q, const void* k, const float* weights, con
  * length per (row, split) (an eighth of the split); a smaller one makes
  * splits spill earlier (for tests). The workspace (256-byte aligned, size
  * from dsa_indexer_select_workspace_bytes with the same rows, columns and
- * list_cap on the same device) holds floors u32 [rows], records and lists;
+ * list_cap on the same device) holds floors u32 [rows][2] (a row's floor is
+ * the smaller of its two entries; dsa_indexer_floors_fp8 writes one
+ * estimate twice), records and lists;
  * it needs no initialisation, and calls that overlap on different streams
  * need distinct workspaces and score buffers. A caller may overwrite the
  * floors between the first two launches (a floor too high for a row only
@@ -303,8 +306,9 @@ int dsa_layer_prologue_fp8(const void* q, int64_t q_rows, const float* weights, 
 
 /*
  * dsa_layer_prologue_fp8 that also writes the per-row floors of the
- * candidate top-k (as dsa_indexer_floors_fp8 estimates them) into `floors`
- * (uint32 [q_rows / 64]), for a layer step whose queries are the causal rows
+ * candidate top-k into `floors` (uint32 [q_rows / 64][2]: two estimates per
+ * row from the two halves of its sample, the row's floor being the smaller),
+ * for a layer step whose queries are the causal rows
  * history .. history + q_rows / 64 - 1 over the resident index keys
  * key_cache e4m3 [history + ..., 128] / key_cache_scales f32: each row's
  * floor is sampled from columns [0, history) (the new keys are written by

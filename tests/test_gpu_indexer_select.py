@@ -107,7 +107,8 @@ def test_select_config1_lists_only_candidates(gpu):
     torch.cuda.synchronize()
     _same(got, (values, ids))
     workspace, _ = indexer._SELECT_BUFFERS[(gpu.index, _native.stream_of(gpu).value)]
-    floors = workspace[:4 * rows].view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+    pair = workspace[:8 * rows].view(torch.int32).view(rows, 2).to(torch.int64) & 0xFFFFFFFF
+    floors = pair.min(dim=1).values
     assert (floors != 0).all()
     radix = _radix(scores)
     candidates = radix >= floors[:, None]
@@ -116,7 +117,7 @@ def test_select_config1_lists_only_candidates(gpu):
     assert per_row.max().item() <= 8192
     assert per_row.sum().item() * 8 <= 6 * 2**20, "more than 6 MiB of candidate keys"
     splits, per = _split_plan(rows, columns, gpu)
-    records_at = (4 * rows + 255) // 256 * 256
+    records_at = (8 * rows + 255) // 256 * 256
     rec = workspace[records_at:records_at + rows * splits * 8].view(torch.int32).view(rows, splits, 2)
     live = [sp for sp in range(splits) if sp * per < columns]
     assert (rec[:, live, 1] == 0x7FFFFFFF).all(), "a split spilled"
@@ -214,12 +215,12 @@ def test_layer_prologue_floors(gpu):
     index_q, weights = inputs.index_q.to(gpu), inputs.weights.to(gpu)
     index_k = inputs.index_k[history:].to(gpu).contiguous()
     mla_q, kv = inputs.mla_q.to(gpu), inputs.kv[history:].to(gpu).contiguous()
-    floors = torch.zeros(queries, dtype=torch.int32, device=gpu)
+    floors = torch.zeros((queries, 2), dtype=torch.int32, device=gpu)
     q8, folded, _ = layer._prologue(index_q, index_k, weights, kv, history, floors)
     scores = indexer.logits(q8, layer.index_keys, folded, layer.index_scales, history)
     values, ids = indexer.exact_topk(scores, 2048)
     torch.cuda.synchronize()
-    fl = floors.to(torch.int64) & 0xFFFFFFFF
+    fl = (floors.to(torch.int64) & 0xFFFFFFFF).min(dim=1).values
     assert (fl > 0).all()
     assert (fl <= _radix(values[:, -1])).all(), "a floor above the row's 2048th score"
     per_row = (_radix(scores) >= fl[:, None]).sum(dim=1)
