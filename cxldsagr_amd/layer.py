@@ -29,6 +29,54 @@ from cxldsagr_amd.contracts import AttentionContext, TokenSelection
 PAGE_TOKENS = 64
 
 
+def index_prologue_applies(index_q, index_k, weights, device):
+    """The one-launch prologue covers the model shapes (bf16 index Q
+    ``[rows, 64, 128]`` and K ``[rows, 128]``, f32 weights ``[rows, 64]``)."""
+    rows = len(index_q)
+    return (index_q.dtype == torch.bfloat16 and index_q.ndim == 3
+            and index_q.shape[1:] == (64, 128) and index_k.dtype == torch.bfloat16
+            and tuple(index_k.shape) == (rows, 128) and weights.dtype == torch.float32
+            and tuple(weights.shape) == (rows, 64)
+            and all(t.device == device for t in (index_q, index_k, weights)))
+
+
+def index_prologue(index_q, index_k, weights, index_keys, index_scales, position, topk, floors,
+                   *, kv=None, page_table=None, kv_cache=None):
+    """The small stages before the indexer's logits in one launch
+    (``dsa_layer_prologue_floors_fp8``): Q quantisation + weight fold, the new
+    index K quantised into the resident cache at ``position``, the new KV
+    records packed into the fp8 paged cache (when ``kv`` is given), and, with
+    ``floors`` (int32 ``[rows, 2]``), the candidate top-k's per-row floors -
+    the same bits as the separate operators. Returns ``(q8, folded, q_fold)``,
+    ``q_fold`` the partial folded queries ``[rows, 4, 128]`` that let the
+    logits kernel skip forming them (same logits bits)."""
+    device = index_q.device
+    rows = len(index_q)
+    end = position + rows
+    index_q, index_k, weights = (t.contiguous() for t in (index_q, index_k, weights))
+    index_q, index_k = (attention._aligned(t) for t in (index_q, index_k))
+    q8 = torch.empty(index_q.shape, dtype=torch.float8_e4m3fn, device=device)
+    q_scales = torch.empty((*index_q.shape[:-1], 1), dtype=torch.float32, device=device)
+    folded = torch.empty_like(weights)
+    q_fold = torch.empty((rows, 4, 128), dtype=torch.float32, device=device)
+    if kv is not None:
+        kv = attention._aligned(kv.contiguous())
+    with torch.cuda.device(device):
+        _native.call(
+            "dsa_layer_prologue_floors_fp8",
+            _native.ptr(index_q), rows * 64, _native.ptr(weights), _native.ptr(q8),
+            _native.ptr(q_scales), _native.ptr(folded), _native.ptr(q_fold),
+            _native.ptr(index_k), rows, _native.ptr(index_keys[position:end]),
+            _native.ptr(index_scales[position:end]),
+            _native.ptr(kv), rows if kv is not None else 0, position if kv is not None else 0,
+            _native.ptr(page_table),
+            kv_cache.shape[0] if kv is not None else 0, _native.ptr(kv_cache), None,
+            _native.ptr(index_keys), _native.ptr(index_scales), position, topk,
+            _native.ptr(floors), _native.stream_of(device),
+        )
+    return q8, folded, q_fold
+
+
 class DSALayer:
     """Resident HBM caches for one layer of one sequence.
 
@@ -106,6 +154,14 @@ class DSALayer:
         end = position + rows
         if end > self.capacity:
             raise ValueError("query batch exceeds the layer capacity")
+        if index_prologue_applies(index_q, index_k, weights, self.device):
+            floors = indexer.select_floors_buffer(self.device, rows, end)
+            q8, folded, q_fold = index_prologue(index_q, index_k, weights, self.index_keys,
+                                                self.index_scales, position, self.topk, floors)
+            _, ids = indexer.select_topk(q8, self.index_keys[:end], folded,
+                                         self.index_scales[:end], position, self.topk,
+                                         _q_fold=q_fold, _floors_ready=True)
+            return TokenSelection(ids)
         q8, _, weights = indexer.quantize_index_folded(index_q, weights)
         indexer.quantize_into(index_k, self.index_keys[position:end],
                               self.index_scales[position:end])
@@ -131,34 +187,11 @@ class DSALayer:
 
     def _prologue(self, index_q, index_k, weights, kv, position, floors=None):
         """Q quantisation + weight fold, new index K into the cache and the new
-        KV records into the fp8 paged cache, in one launch
-        (``dsa_layer_prologue_fp8``; the same bits as the three separate
-        operators). Also returns the partial folded queries ``[rows, 4, 128]``
-        that let the logits kernel skip forming them (same logits bits). With
-        ``floors`` (int32 ``[rows]``), the same launch also estimates the
-        candidate top-k's per-row floors into it
-        (``dsa_layer_prologue_floors_fp8``)."""
-        rows = len(index_q)
-        end = position + rows
-        index_q, index_k, weights, kv = (t.contiguous() for t in (index_q, index_k, weights, kv))
-        index_q, index_k, kv = (attention._aligned(t) for t in (index_q, index_k, kv))
-        q8 = torch.empty(index_q.shape, dtype=torch.float8_e4m3fn, device=self.device)
-        q_scales = torch.empty((*index_q.shape[:-1], 1), dtype=torch.float32, device=self.device)
-        folded = torch.empty_like(weights)
-        q_fold = torch.empty((rows, 4, 128), dtype=torch.float32, device=self.device)
-        with torch.cuda.device(self.device):
-            _native.call(
-                "dsa_layer_prologue_floors_fp8",
-                _native.ptr(index_q), rows * 64, _native.ptr(weights), _native.ptr(q8),
-                _native.ptr(q_scales), _native.ptr(folded), _native.ptr(q_fold),
-                _native.ptr(index_k), rows, _native.ptr(self.index_keys[position:end]),
-                _native.ptr(self.index_scales[position:end]),
-                _native.ptr(kv), rows, position, _native.ptr(self.page_table),
-                self.kv_cache.shape[0], _native.ptr(self.kv_cache), None,
-                _native.ptr(self.index_keys), _native.ptr(self.index_scales), position, self.topk,
-                _native.ptr(floors), _native.stream_of(self.device),
-            )
-        return q8, folded, q_fold
+        KV records into the fp8 paged cache, in one launch (``index_prologue``).
+        Returns ``(q8, folded, q_fold)``."""
+        return index_prologue(index_q, index_k, weights, self.index_keys, self.index_scales,
+                              position, self.topk, floors, kv=kv, page_table=self.page_table,
+                              kv_cache=self.kv_cache)
 
     def _attend(self, q, ids, end):
         if self.kv_format == "fp8_paged":
@@ -181,6 +214,11 @@ class DSALayer:
         if self._fused_prologue_applies(index_q, index_k, weights, kv):
             floors = indexer.select_floors_buffer(self.device, rows, end)
             q8, folded, q_fold = self._prologue(index_q, index_k, weights, kv, position, floors)
+        elif index_prologue_applies(index_q, index_k, weights, self.device):
+            floors = indexer.select_floors_buffer(self.device, rows, end)
+            q8, folded, q_fold = index_prologue(index_q, index_k, weights, self.index_keys,
+                                                self.index_scales, position, self.topk, floors)
+            self._append_kv(kv, position)
         else:
             indexer.quantize_into(index_k, self.index_keys[position:end],
                                   self.index_scales[position:end])
@@ -301,6 +339,16 @@ class OffloadDSALayer:
         end = position + len(index_q)
         if end > self.capacity or len(index_k) != len(index_q) or len(weights) != len(index_q):
             raise ValueError("query batch exceeds the layer capacity or inputs disagree in length")
+        rows = len(index_q)
+        if index_prologue_applies(index_q, index_k, weights, self.device):
+            # Quantisers and the candidate top-k's floors in one launch.
+            floors = indexer.select_floors_buffer(self.device, rows, end)
+            q8, folded, q_fold = index_prologue(index_q, index_k, weights, self.index_keys,
+                                                self.index_scales, position, self.topk, floors)
+            _, ids = indexer.select_topk(q8, self.index_keys[:end], folded,
+                                         self.index_scales[:end], position, self.topk,
+                                         _q_fold=q_fold, _floors_ready=True)
+            return ids
         q8, _, folded = indexer.quantize_index_folded(index_q, weights)
         indexer.quantize_into(index_k, self.index_keys[position:end], self.index_scales[position:end])
         _, ids = indexer.select_topk(q8, self.index_keys[:end], folded,
