@@ -278,23 +278,24 @@ extern "C" int dsa_pool_workspace_bytes(int64_t slots, int64_t history_capacity,
 namespace dsa {
 namespace {
 
-// The event that orders a recall's gather after its assignment when the
-// gather runs on a stream of its own (one per device; a wait captures the
-// event's state when it is enqueued, so one event serves every call).
-hipEvent_t assign_event(int* rc) {
+// Orders `later` after the work enqueued so far on `earlier`, through one
+// event per device. A wait captures the event's state when it is enqueued,
+// so one event serves every call, provided no other thread records it between
+// this call's record and wait: the lock is held across both.
+int order_streams(hipStream_t earlier, hipStream_t later) {
   static std::mutex lock;
   static hipEvent_t events[64] = {};
   int device = 0;
-  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) {
-    *rc = kLaunchFailed;
-    return nullptr;
-  }
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return kLaunchFailed;
   std::lock_guard<std::mutex> guard(lock);
   if (!events[device] && hipEventCreateWithFlags(&events[device], hipEventDisableTiming) != hipSuccess) {
     events[device] = nullptr;
-    *rc = kLaunchFailed;
+    return kLaunchFailed;
   }
-  return events[device];
+  if (hipEventRecord(events[device], earlier) != hipSuccess ||
+      hipStreamWaitEvent(later, events[device], 0) != hipSuccess)
+    return kLaunchFailed;
+  return kOk;
 }
 
 // One recall on `stream` (the steps in the header). keep_floor >= 0 also
@@ -381,10 +382,7 @@ int recall_impl(const int32_t* indices, int64_t n, const int32_t* page_table,
     if (blocks < 1) blocks = 1;
     hipStream_t gs = stream;
     if (gather_stream != stream) {
-      int erc = kOk;
-      hipEvent_t ev = assign_event(&erc);
-      if (erc != kOk || hipEventRecord(ev, stream) != hipSuccess ||
-          hipStreamWaitEvent(gather_stream, ev, 0) != hipSuccess) {
+      if (order_streams(stream, gather_stream) != kOk) {
         set_error("could not order the gather stream after the recall");
         return kLaunchFailed;
       }

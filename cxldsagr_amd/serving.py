@@ -105,11 +105,12 @@ class SessionLRU:
         if type(capacity) is not int or capacity <= 0:
             raise ValueError("capacity must be a positive integer")
         pages = (capacity + PAGE_SIZE - 1) // PAGE_SIZE
-        # An impossible request must not destroy any existing reusable state.
+        # Feasibility first: a request larger than the whole arena fails here,
+        # before the LRU is touched, so it evicts no other user's session.
         if pages > self.host_page_capacity:
             raise CacheBudgetExceeded(
-                f"session requires {pages} host pages, exceeds arena capacity "
-                f"{self.host_page_capacity}")
+                f"a {capacity}-token session needs {pages} host pages but the arena "
+                f"holds only {self.host_page_capacity}")
         prior = self._entries.get(key)
         if (prior is not None and prior.ready and prior.signature == signature
                 and prior.capacity >= capacity):

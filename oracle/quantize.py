@@ -71,8 +71,3 @@ def quantize_index(x, scale_fmt="ue8m0"):
     codes = fp8.encode(np.where(nan, np.float32(0.0), y))
     codes[nan] = 0x7F
     return codes, scale
-
-
-def dequantize(codes, scale):
-    """e4m3 codes ``[..., D]`` and scales ``[..., 1]`` -> float32 values."""
-    return (fp8.decode(codes) * np.asarray(scale, dtype=np.float32)).astype(np.float32)

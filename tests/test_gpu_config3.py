@@ -15,8 +15,11 @@ pool (``OffloadDSALayer.forward(..., transient=True)``). Checked:
   ``oracle.recall.check_maps``): sentinel slot, h2d/d2h inverse, free slots
   at priority -1, live priorities below the clock, live records equal to
   their host rows;
-* the first user's recall from the cold pool leaves the same h2d, d2h,
-  priority and record state as the oracle's recall of the same selection.
+* the first user's recall from the cold pool, and the same user's recall in
+  round 2 from the full pool (a warm recall that evicts other users'
+  records: the oracle's pool is mirrored from the device state just before
+  it), leave the same h2d, d2h, priority and record state as the oracle's
+  recall of the same selection.
 """
 
 import numpy as np
@@ -84,9 +87,19 @@ def test_config3_multi_user_two_rounds(gpu):
             fresh = make_layer_inputs(0, QUERIES, seed=100_000 * (rnd + 1) + u)
             x = {name: getattr(fresh, name).to(gpu) for name in
                  ("index_q", "index_k", "weights", "mla_q", "kv")}
-            if rnd == 0 and u == 0:
+            if u == 0:
                 mirror = orecall.Pool(pool.host_capacity, SLOTS, 656, QUERIES)
                 mirror.host[:] = pool.host.numpy()
+                if rnd == 1:
+                    # The device pool's state before this warm recall.
+                    h2d, d2h, priority = _host_state(pool)
+                    mirror.h2d[:], mirror.d2h[:], mirror.priority[:] = h2d, d2h, priority
+                    records = pool.records.view(-1, 656)[:len(mirror.records)].cpu().numpy()
+                    mirror.records[:] = records
+                    mirror.clock = pool.clock
+                    free_before = int((d2h[1:] == orecall.MISSING).sum())
+                    recalled_before = mirror.recalled
+                    del records
             out, selection = layer.forward(x["index_q"], x["index_k"], x["weights"], x["mla_q"],
                                            x["kv"], transient=True)
             pack_kv_fp8(x["kv"], resident, identity, token_offset=HISTORY)
@@ -98,10 +111,15 @@ def test_config3_multi_user_two_rounds(gpu):
             # Every row selects TOPK real tokens (no padding, no non-finite score).
             assert bool((selection.token_ids >= 0).all())
             assert torch.equal(out.view(torch.int16), expected.view(torch.int16)), (rnd, u)
-            if rnd == 0 and u == 0:
+            if u == 0:
                 ids = selection.token_ids.cpu().numpy()
                 table = layer.session.page_table.cpu().numpy()
                 orecall.ensure(mirror, ids, table, written=tokens, transient_start=HISTORY)
+                if rnd == 1:
+                    misses = mirror.recalled - recalled_before
+                    print(f"config3 round 2 user 0: {misses} misses, {free_before} free slots",
+                          flush=True)
+                    assert misses > free_before, "the warm recall must evict"
                 h2d, d2h, priority = _host_state(pool)
                 np.testing.assert_array_equal(h2d, mirror.h2d)
                 np.testing.assert_array_equal(d2h, mirror.d2h)

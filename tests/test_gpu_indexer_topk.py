@@ -156,6 +156,60 @@ def test_digits_topk_equals_one_part_kernel(gpu, rows, columns, k):
         assert not counts.any()
 
 
+def test_digits_topk_past_64_select_parts(gpu):
+    """Rows longer than 64 select parts (2,211,840 columns): the parts are not
+    listed and the finish selects each row alone from its scores, with the
+    threshold digit from the counts."""
+    rows, columns, k = 3, 2_300_001, 2048
+    generator = torch.Generator(device="cuda").manual_seed(2300)
+    scores = torch.randn(rows, columns, device=gpu, generator=generator)
+    scores[0, 1_000_000:1_000_100] = 9.0         # ties at the top, SMALL order
+    scores[1, 2_250_000:] = -torch.inf           # a masked tail past part 64
+    scores[2] = -scores[2].abs()                 # a negative threshold
+    values, ids = _one_part_topk(scores, columns, k)
+    workspace, counts = _workspace(rows, columns, gpu)
+    host = scores.cpu().numpy()
+    expected = torch.from_numpy(otopk.digit_counts(host).astype(np.int32)).to(gpu)
+    for _ in range(2):
+        counts.copy_(expected)
+        got_values, got_ids = _digits_topk(scores, columns, k, workspace)
+        assert torch.equal(got_values.view(torch.int32), values.view(torch.int32))
+        assert torch.equal(got_ids, ids)
+        assert not counts.any()
+    ref_values, ref_ids = otopk.exact_topk(host, k)
+    np.testing.assert_array_equal(got_ids.cpu().numpy(), ref_ids)
+    np.testing.assert_array_equal(got_values.cpu().numpy().view(np.uint32), ref_values.view(np.uint32))
+
+
+def _digit_histogram(scores, columns):
+    """[rows, 2048] counts of the radix digits (radix key >> 21) of the first
+    ``columns`` scores of each row, on the GPU (torch.bincount)."""
+    rows = len(scores)
+    bits = scores[:, :columns].contiguous().view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+    keys = torch.where(bits >= 2**31, bits ^ 0xFFFFFFFF, bits | 2**31)
+    flat = (keys >> 21) + torch.arange(rows, device=scores.device)[:, None] * 2048
+    del bits, keys
+    return torch.bincount(flat.view(-1), minlength=rows * 2048).view(rows, 2048)
+
+
+def test_counted_logits_capped_split(gpu):
+    """4,096 rows over 66,000 keys: one key split per query group would span
+    66,048 keys, past what the 16-bit LDS counters hold (65,408), so the
+    launcher caps the split and the row takes two. Scores equal the plain
+    kernel's, counts equal a histogram of them."""
+    from cxldsagr_amd.indexer import logits
+
+    rows, columns = 4096, 66_000
+    q, k, w, s = _logit_inputs(rows, columns, gpu, seed=4096)
+    plain = logits(q, k, w, s, columns - rows, _pad_to_stride=True)
+    out, counts = _counted_logits(q, k, w, s, columns - rows)
+    assert torch.equal(out.view(torch.int32), plain.view(torch.int32))
+    del out
+    expected = _digit_histogram(plain, columns)
+    assert torch.equal(counts.to(torch.int64), expected)
+    assert (counts.sum(dim=1) == columns).all()
+
+
 def test_digits_topk_ignores_counts_that_do_not_sum_to_the_row(gpu):
     rows, columns, k = 6, 65664, 2048
     generator = torch.Generator(device="cuda").manual_seed(77)

@@ -10,8 +10,11 @@ sample of query rows:
 * top-k: the id sets agree except for elements whose score lies within 1e-3
   (relative) of the k-th score, where GPU and CPU rounding may order a tie
   differently;
-* sparse MLA: GPU output against the oracle over the GPU's own selection,
-  cosine >= 0.9999 and max-abs <= 2e-2.
+* sparse MLA: GPU output against the oracle over the GPU's own selection on
+  every query row (16 spread rows at config 4): elementwise within the
+  reference's tolerance (|a - e| <= 4e-3 + 2e-2 |e|,
+  operators/deepseek_v32/attention/device_only/tests/test_deepseek_mla.py:76),
+  and the north-star bar, cosine >= 0.9999 per row and max-abs <= 2e-2.
 """
 
 import numpy as np
@@ -70,22 +73,27 @@ def _check_selection(gpu_ids, ref_ids, ref_scores_row, kth):
 
 
 def _check_attention(actual, expected):
-    a = actual.astype(np.float64).ravel()
-    e = expected.astype(np.float64).ravel()
+    """actual, expected [rows, heads, 512]: the reference's elementwise
+    tolerance, then max-abs and cosine per row."""
+    a = actual.astype(np.float64).reshape(len(actual), -1)
+    e = expected.astype(np.float64).reshape(len(expected), -1)
+    excess = np.abs(a - e) - (4e-3 + 2e-2 * np.abs(e))
+    assert excess.max() <= 0, f"outside atol 4e-3 / rtol 2e-2 by {excess.max():.3g}"
     assert np.abs(a - e).max() <= 2e-2
-    denom = np.linalg.norm(a) * np.linalg.norm(e)
-    assert denom == 0 or a @ e / denom >= 0.9999
+    norms = np.linalg.norm(a, axis=1) * np.linalg.norm(e, axis=1)
+    cosine = np.where(norms > 0, (a * e).sum(axis=1) / np.where(norms > 0, norms, 1), 1.0)
+    assert cosine.min() >= 0.9999, f"row cosine {cosine.min():.6f}"
 
 
 @pytest.mark.parametrize(
     ("history", "queries", "rows", "mla_rows"),
     [
-        (4096, 128, list(range(128)), [0, 1, 63, 127]),         # BASELINE config 0 shape
-        (65536, 128, list(range(128)), [0, 31, 64, 127]),       # configs 1/2: the benchmark
+        (4096, 128, list(range(128)), list(range(128))),   # BASELINE config 0 shape
+        (65536, 128, list(range(128)), list(range(128))),  # configs 1/2: the benchmark
     ],
 )
 def test_layer_matches_oracle(gpu, history, queries, rows, mla_rows):
-    """Logits and selections on every query row; sparse MLA on a sample."""
+    """Logits, selections and sparse MLA on every query row."""
     inputs, out, ids, scores = _run_layer(gpu, history, queries, seed=947)
     cache, ref_scores, ref_values, ref_ids = _oracle(inputs, np.asarray(rows))
     tokens = history + queries
@@ -109,8 +117,8 @@ def test_layer_matches_oracle(gpu, history, queries, rows, mla_rows):
 @pytest.mark.parametrize("kv_format", ["fp8_paged", "bf16"])
 def test_config4_long_context_layer(gpu, kv_format):
     """131072 history + 512 queries, 10 % heavy hitters in 8
-    contiguous spans. Oracle parity on three rows (logits, selection, MLA),
-    selection properties on all 512 rows."""
+    contiguous spans. Oracle parity on 16 spread rows (logits, selection,
+    MLA), selection properties on all 512 rows."""
     from cxldsagr_amd.layer import DSALayer
     from cxldsagr_amd.workloads import CONFIGS, make_layer_inputs
 
@@ -132,7 +140,7 @@ def test_config4_long_context_layer(gpu, kv_format):
     ends = history + torch.arange(queries, device=gpu)
     assert bool((ids >= 0).all()) and bool((ids.max(dim=1).values <= ends).all())
 
-    rows = np.array([0, 255, 511])
+    rows = np.array([round(i * (queries - 1) / 15) for i in range(16)])
     cache, ref_scores, ref_values, ref_ids = _oracle(inputs, rows,
                                                      fp8_records=kv_format == "fp8_paged")
     gpu_ids = ids.cpu().numpy()[rows]
