@@ -58,6 +58,9 @@ SIGNATURES = {
     "dsa_index_producer_fp8": [_ptr, _i64, _ptr, _f32, _f32, _ptr, _ptr, _ptr, _f32, _ptr, _i64,
                                _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _ptr, _i64,
                                _ptr, _ptr, _ptr],
+    "dsa_index_producer_floors_fp8": [_ptr, _i64, _ptr, _f32, _f32, _ptr, _ptr, _ptr, _f32, _ptr,
+                                      _i64, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64,
+                                      _ptr, _i64, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _ptr, _ptr],
     "dsa_sparse_mla_bf16": [_ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _f32, _ptr, _ptr],
     "dsa_sparse_mla_fp8_paged": [_ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i64, _f32,
                                  _ptr, _ptr],

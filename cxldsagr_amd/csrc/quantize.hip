@@ -322,6 +322,18 @@ struct FloorArgs {
   uint32_t* floors;         // [rows][2]
 };
 
+// The floor blocks of the index producer take the index-Q row before RoPE
+// (the Q projection's output) and form the head weights from the head
+// logits: the query's RoPE row and the weight inputs. With `cos_sin` null the
+// query rows are already rotated and `weights` holds the head weights.
+struct FloorProducer {
+  const float* cos_sin;  // [table_rows, 64]: cos of the 32 angles, then their sin
+  const int32_t* rows;   // RoPE table row of each query, or null: query i uses row i
+  int64_t table_rows;
+  const float* head;     // head logits [queries * 64]
+  float pre, post;       // weight = ((head * pre) * q_scale) * post
+};
+
 // Max over the four consecutive lanes of a quad (DPP quad permutes).
 __device__ __forceinline__ uint32_t quad_max(uint32_t v) {
   uint32_t o = __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);  // lane ^ 1
@@ -330,8 +342,10 @@ __device__ __forceinline__ uint32_t quad_max(uint32_t v) {
   return v > o ? v : o;
 }
 
+template <bool kProducer>
 __device__ void prologue_floor(int64_t i, int half, const uint16_t* __restrict__ q,
-                               const float* __restrict__ weights, const FloorArgs fa) {
+                               const float* __restrict__ weights, const FloorArgs fa,
+                               const FloorProducer fp) {
   using namespace logits_core;
   __shared__ __align__(16) uint32_t codes[kHeads][36];  // 144-byte rows: fewer bank conflicts
   __shared__ float folded[kHeads];
@@ -398,6 +412,35 @@ __device__ void prologue_floor(int64_t i, int half, const uint16_t* __restrict__
         v[8 * c + 2 * j + 1] = bf16_to_f32(words[j] >> 16);
       }
     }
+    if constexpr (kProducer) {
+      // The producer's RoPE on dims [0, 64): dim j < 32 (part 0) pairs with
+      // dim j + 32 (part 1, the next lane); each product and sum rounded to
+      // fp32, the result to bf16, as the producer's own Q rows.
+#pragma clang fp contract(off)
+      int64_t trow = fp.rows ? (int64_t)fp.rows[i] : i;
+      if (trow < 0 || trow >= fp.table_rows) trow = 0;  // the Q blocks flag it
+      const float* trig = fp.cos_sin + trow * 64;
+      float other[32];
+#pragma unroll
+      for (int j = 0; j < 32; ++j)
+        other[j] = __uint_as_float((uint32_t)__builtin_amdgcn_mov_dpp(
+            (int)__float_as_uint(v[j]), 0xB1, 0xF, 0xF, false));  // lane ^ 1
+      if (part < 2) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const float4 cs = *reinterpret_cast<const float4*>(trig + 4 * c);
+          const float4 sn = *reinterpret_cast<const float4*>(trig + 32 + 4 * c);
+          const float cv[4] = {cs.x, cs.y, cs.z, cs.w};
+          const float sv[4] = {sn.x, sn.y, sn.z, sn.w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float x = v[4 * c + j] * cv[j];
+            const float y = other[4 * c + j] * sv[j];
+            v[4 * c + j] = bf16_to_f32(f32_to_bf16(part == 0 ? x - y : x + y));
+          }
+        }
+      }
+    }
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
       const uint32_t a = __float_as_uint(v[j]) & 0x7FFFFFFFu;
@@ -415,7 +458,14 @@ __device__ void prologue_floor(int64_t i, int half, const uint16_t* __restrict__
       word = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], word, true);
       codes[h][8 * part + c] = word;
     }
-    if (part == 0) folded[h] = weights[i * kHeads + h] * scale;
+    if (part == 0) {
+      if constexpr (kProducer) {
+#pragma clang fp contract(off)
+        folded[h] = ((fp.head[i * kHeads + h] * fp.pre) * scale) * fp.post;
+      } else {
+        folded[h] = weights[i * kHeads + h] * scale;
+      }
+    }
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) hist[8 * tid + j] = 0;
@@ -483,7 +533,7 @@ __global__ __launch_bounds__(256) void layer_prologue(
   // The floor blocks (the longest) come first in the grid, so that they
   // start at once and the short blocks fill the CUs around them.
   if ((int64_t)blockIdx.x < nf) {
-    prologue_floor(blockIdx.x >> 1, (int)(blockIdx.x & 1), q, weights, fa);
+    prologue_floor<false>(blockIdx.x >> 1, (int)(blockIdx.x & 1), q, weights, fa, FloorProducer{});
     return;
   }
   const int64_t b = blockIdx.x - nf;
@@ -726,7 +776,8 @@ __device__ __forceinline__ QuantLane produce_rows_d128(
   return QuantLane{lo, hi, fold};
 }
 
-// Blocks [0, nq): index Q rows (RoPE, quantise, weight fold, partial folded
+// Blocks [0, nf): the candidate top-k's per-row floors (when asked for),
+// then [0, nq): index Q rows (RoPE, quantise, weight fold, partial folded
 // queries); [nq, nq + nk): index K rows (LayerNorm, RoPE, quantise into the
 // resident cache); the rest: new KV tokens into the fp8 paged cache.
 __global__ __launch_bounds__(256) void index_producer(
@@ -737,8 +788,14 @@ __global__ __launch_bounds__(256) void index_producer(
     uint8_t* __restrict__ k_codes, float* __restrict__ k_scales, const RopeTable rope,
     const uint16_t* __restrict__ kv, int64_t token_offset, const int32_t* __restrict__ page_table,
     int64_t pages, uint8_t* __restrict__ cache, int32_t* __restrict__ status, int64_t nq,
-    int64_t nk) {
-  const int64_t b = blockIdx.x;
+    int64_t nk, int64_t nf, FloorArgs fa) {
+  // Floor blocks first (the longest), two per query, as in layer_prologue.
+  if ((int64_t)blockIdx.x < nf) {
+    const FloorProducer fp{rope.cos_sin, rope.rows, rope.table_rows, head, pre, post};
+    prologue_floor<true>(blockIdx.x >> 1, (int)(blockIdx.x & 1), q, nullptr, fa, fp);
+    return;
+  }
+  const int64_t b = blockIdx.x - nf;
   if (b < nq) {
     const QuantLane mine = produce_rows_d128<false>(b, q, q_rows, 64, rope, nullptr, nullptr, 0.0f,
                                                     q_codes, q_scales, head, pre, post, w_folded,
@@ -762,6 +819,23 @@ extern "C" int dsa_index_producer_fp8(
     void* q_codes, float* q_scales, float* weights_out, float* q_fold, void* k_codes,
     float* k_scales, const void* kv, int64_t token_offset, const int32_t* page_table,
     int64_t pages, void* cache, int32_t* status, hipStream_t stream) {
+  return dsa_index_producer_floors_fp8(q_proj, tokens, head_logits, head_pre_scale,
+                                       head_post_scale, k_proj, norm_weight, norm_bias, norm_eps,
+                                       cos_sin, table_rows, rope_rows, q_codes, q_scales,
+                                       weights_out, q_fold, k_codes, k_scales, kv, token_offset,
+                                       page_table, pages, cache, status, nullptr, nullptr, 0, 0,
+                                       nullptr, stream);
+}
+
+extern "C" int dsa_index_producer_floors_fp8(
+    const void* q_proj, int64_t tokens, const float* head_logits, float head_pre_scale,
+    float head_post_scale, const void* k_proj, const float* norm_weight, const float* norm_bias,
+    float norm_eps, const float* cos_sin, int64_t table_rows, const int32_t* rope_rows,
+    void* q_codes, float* q_scales, float* weights_out, float* q_fold, void* k_codes,
+    float* k_scales, const void* kv, int64_t token_offset, const int32_t* page_table,
+    int64_t pages, void* cache, int32_t* status, const void* key_cache,
+    const float* key_cache_scales, int64_t history, int64_t topk, uint32_t* floors,
+    hipStream_t stream) {
   using namespace dsa;
   DSA_CHECK_ARG(tokens >= 0 && table_rows >= 0 && token_offset >= 0 && pages >= 0,
                 "invalid producer shape");
@@ -788,14 +862,27 @@ extern "C" int dsa_index_producer_fp8(
   const int64_t nq = (tokens * 64 * 16 + 255) / 256;
   const int64_t nk = (tokens * 16 + 255) / 256;
   const int64_t nt = pack ? (tokens + 3) / 4 : 0;
+  // Floor blocks: two per query, sampling the resident key cache's first
+  // `history` columns (the query at position history + i sees history + i + 1).
+  int64_t nf = 0;
+  if (floors != nullptr) {
+    DSA_CHECK_ARG(key_cache && key_cache_scales && history >= 0 && topk >= 1 && topk <= 2048 &&
+                      aligned(key_cache, 16) && aligned(floors, 4),
+                  "floors need the resident key cache (16-byte aligned) and k in [1, 2048]");
+    DSA_CHECK_ARG(history < ((int64_t)1 << 25), "the key cache must be addressable with 32-bit offsets");
+    nf = 2 * tokens;
+  }
+  const int64_t columns = history + tokens;
+  const FloorArgs fa{static_cast<const uint8_t*>(key_cache), key_cache_scales, history,
+                     (int)(topk < columns ? topk : columns), floors};
   const RopeTable rope{cos_sin, rope_rows, table_rows};
-  hipLaunchKernelGGL(index_producer, dim3((unsigned)(nq + nk + nt)), dim3(256), 0, stream,
+  hipLaunchKernelGGL(index_producer, dim3((unsigned)(nf + nq + nk + nt)), dim3(256), 0, stream,
                      static_cast<const uint16_t*>(q_proj), tokens * 64, head_logits,
                      head_pre_scale, head_post_scale, static_cast<uint8_t*>(q_codes), q_scales,
                      weights_out, q_fold, static_cast<const uint16_t*>(k_proj), tokens,
                      norm_weight, norm_bias, norm_eps, static_cast<uint8_t*>(k_codes), k_scales,
                      rope, static_cast<const uint16_t*>(kv), token_offset, page_table, pages,
-                     static_cast<uint8_t*>(cache), status, nq, nk);
+                     static_cast<uint8_t*>(cache), status, nq, nk, nf, fa);
   DSA_CHECK_LAUNCH("index producer");
   return kOk;
 }

@@ -248,16 +248,18 @@ class DSALayer:
                 or projected.k_proj.shape[0] != rows):
             raise ValueError("query batch exceeds the layer capacity or inputs disagree in length")
         paged = self.kv_format == "fp8_paged"
+        floors = indexer.select_floors_buffer(self.device, rows, end)
         q8, _, folded, _, _, q_fold = projection.produce(
             projected, index_keys=self.index_keys[position:end],
             index_scales=self.index_scales[position:end], q_fold=True,
             kv=kv if paged else None, kv_cache=self.kv_cache, page_table=self.page_table,
-            token_offset=position)
+            token_offset=position, floors=floors, key_cache=self.index_keys,
+            key_cache_scales=self.index_scales, topk=self.topk)
         if not paged:
             self._append_kv(kv, position)
         _, ids = indexer.select_topk(q8, self.index_keys[:end], folded,
                                      self.index_scales[:end], position, self.topk,
-                                     _q_fold=q_fold)
+                                     _q_fold=q_fold, _floors_ready=True)
         out = self._attend(q, ids, end)
         self.written = end
         return out, TokenSelection(ids)

@@ -80,7 +80,8 @@ def rotary_table(positions, frequencies):
 def index_producer(q_proj, k_proj, head_logits, norm_weight, norm_bias, eps, cos_sin,
                    rope_rows=None, *, index_keys=None, index_scales=None, q_fold=False,
                    kv=None, kv_cache=None, page_table=None, token_offset=0, status=None,
-                   head_scales=(INDEX_HEADS ** -0.5, INDEX_DIM ** -0.5)):
+                   head_scales=(INDEX_HEADS ** -0.5, INDEX_DIM ** -0.5), floors=None,
+                   key_cache=None, key_cache_scales=None, topk=2048):
     """Index Q/K from their GEMM outputs, in one launch.
 
     ``q_proj`` bf16 ``[T, 64, 128]`` (``index_wq(qr)``), ``k_proj`` bf16
@@ -91,7 +92,12 @@ def index_producer(q_proj, k_proj, head_logits, norm_weight, norm_bias, eps, cos
     ``t``). Index K goes to ``index_keys``/``index_scales`` when given (the
     resident cache rows of these tokens), else to new tensors. With ``kv``
     (bf16 ``[T, 576]``) the tokens' fp8 records are also packed into
-    ``kv_cache`` behind ``page_table`` at ``token_offset``.
+    ``kv_cache`` behind ``page_table`` at ``token_offset``. With ``floors``
+    (int32 ``[T, 2]``) the same launch writes the candidate top-k's per-row
+    floors (``indexer.select_topk``) for queries at positions
+    ``token_offset ..`` over the resident index cache ``key_cache`` fp8
+    ``[>= token_offset, 128]`` / ``key_cache_scales`` f32, sampled from its
+    first ``token_offset`` rows.
 
     Returns ``(index_q fp8 [T,64,128], q_scale f32 [T,64,1], weights f32
     [T,64], index_k fp8 [T,128], k_scale f32 [T], q_fold f32 [T,4,128] or
@@ -158,12 +164,28 @@ def index_producer(q_proj, k_proj, head_logits, norm_weight, norm_bias, eps, cos
             raise ValueError("page_table does not cover the appended tokens")
         kv = _aligned(kv.contiguous())
         pages = kv_cache.shape[0]
+    floor_args = ()
+    if floors is not None:
+        if (floors.dtype != torch.int32 or tuple(floors.shape) != (tokens, 2)
+                or not floors.is_contiguous() or floors.device != device):
+            raise ValueError("floors must be contiguous int32 [tokens, 2]")
+        if (key_cache is None or key_cache.dtype != torch.float8_e4m3fn or key_cache.ndim != 2
+                or key_cache.shape[1] != INDEX_DIM or key_cache.shape[0] < token_offset
+                or not key_cache.is_contiguous() or key_cache.device != device
+                or key_cache_scales is None or key_cache_scales.dtype != torch.float32
+                or key_cache_scales.shape[0] < token_offset or key_cache_scales.device != device):
+            raise ValueError("floors need the resident index cache: fp8 [>= token_offset, 128] "
+                             "keys and FP32 scales")
+        if type(topk) is not int or not 1 <= topk <= 2048:
+            raise ValueError("topk must be an integer in [1, 2048]")
+        floor_args = (_native.ptr(key_cache), _native.ptr(key_cache_scales), int(token_offset),
+                      topk, _native.ptr(floors))
     if tokens == 0:
         return q8, q_scales, weights, index_keys, index_scales, fold
     pre, post = head_scales
     with torch.cuda.device(device):
         _native.call(
-            "dsa_index_producer_fp8",
+            "dsa_index_producer_floors_fp8" if floor_args else "dsa_index_producer_fp8",
             _native.ptr(q_proj), tokens, _native.ptr(head_logits), float(pre), float(post),
             _native.ptr(k_proj), _native.ptr(norm_weight), _native.ptr(norm_bias), float(eps),
             _native.ptr(cos_sin), cos_sin.shape[0], _native.ptr(rope_rows),
@@ -171,7 +193,7 @@ def index_producer(q_proj, k_proj, head_logits, norm_weight, norm_bias, eps, cos
             _native.ptr(index_keys), _native.ptr(index_scales),
             _native.ptr(kv), int(token_offset), _native.ptr(page_table), pages,
             _native.ptr(kv_cache if kv is not None else None), _native.ptr(status),
-            _native.stream_of(device),
+            *floor_args, _native.stream_of(device),
         )
     return q8, q_scales, weights, index_keys, index_scales, fold
 

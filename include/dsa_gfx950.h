@@ -362,6 +362,28 @@ int dsa_index_producer_fp8(const void* q_proj, int64_t tokens, const float* head
                            int32_t* status, hipStream_t stream);
 
 /*
+ * dsa_index_producer_fp8 that also writes the per-row floors of the
+ * candidate top-k into `floors` (uint32 [tokens][2], as
+ * dsa_layer_prologue_floors_fp8 writes them), for a layer step whose queries
+ * are the causal rows history .. history + tokens - 1 over the resident
+ * index keys key_cache e4m3 [history + ..., 128] / key_cache_scales f32:
+ * each row's floor is sampled from columns [0, history), scored with the
+ * query's own rotated, quantised rows and head weights (the same bits the
+ * launch writes to q_codes and weights_out). No reference counterpart (the
+ * reference has no floors); the same producer outputs as
+ * dsa_index_producer_fp8.
+ */
+int dsa_index_producer_floors_fp8(
+    const void* q_proj, int64_t tokens, const float* head_logits, float head_pre_scale,
+    float head_post_scale, const void* k_proj, const float* norm_weight, const float* norm_bias,
+    float norm_eps, const float* cos_sin, int64_t table_rows, const int32_t* rope_rows,
+    void* q_codes, float* q_scales, float* weights_out, float* q_fold, void* k_codes,
+    float* k_scales, const void* kv, int64_t token_offset, const int32_t* page_table,
+    int64_t pages, void* cache, int32_t* status, const void* key_cache,
+    const float* key_cache_scales, int64_t history, int64_t topk, uint32_t* floors,
+    hipStream_t stream);
+
+/*
  * A7 - sparse MLA over flat bf16 records. Replaces sparse_mla /
  * sparse_mla_from_pool (FlashMLA flash_mla_sparse_fwd),
  * operators/deepseek_v32/attention/device_only/mla.py:90-115 and

@@ -147,12 +147,15 @@ def test_layer_forward_projected_equals_forward(gpu, kv_format):
     """The layer step from GEMM outputs equals ``forward``, bit for bit, on
     the oracle's post-RoPE bf16 indexer inputs and the head weights scaled by
     64**-0.5 and 128**-0.5 (the fold multiplies by the power-of-two q-scale
-    in between, which commutes exactly with the roundings)."""
+    in between, which commutes exactly with the roundings). The candidate
+    top-k's floors, estimated in the producer launch from the queries it
+    rotates, equal those of forward's prologue bit for bit."""
+    from cxldsagr_amd import indexer
     from cxldsagr_amd.layer import DSALayer
     from cxldsagr_amd.projections import IndexProjected, IndexerProjection, rotary_frequencies
     from cxldsagr_amd.workloads import make_layer_inputs
 
-    history, queries = 4096, 128
+    history, queries = 16384, 128  # past the 8192 visible keys below which rows get no floor
     inputs = make_layer_inputs(history, queries, seed=11)
     tokens = history + queries
     q_proj, k_proj, head, norm_w, norm_b, table = _inputs(queries, seed=12, start=history)
@@ -167,6 +170,7 @@ def test_layer_forward_projected_equals_forward(gpu, kv_format):
     projected = IndexProjected(q_proj.to(gpu), k_proj.to(gpu), head.to(gpu), table.to(gpu))
     mla_q, kv = inputs.mla_q.to(gpu), inputs.kv[history:].to(gpu)
     out_a, sel_a = a.forward_projected(projection, projected, mla_q, kv)
+    floors_a = indexer.select_floors_buffer(gpu, queries, tokens).clone()
 
     # The same step through forward(): bf16 index Q/K after RoPE from the
     # oracle, weights scaled so that their fold equals the producer's.
@@ -178,7 +182,10 @@ def test_layer_forward_projected_equals_forward(gpu, kv_format):
     to_bf16 = lambda x: torch.from_numpy(x).bfloat16().to(gpu)  # noqa: E731 (exact: bf16 values)
     out_b, sel_b = b.forward(to_bf16(index_q), to_bf16(index_k), torch.from_numpy(weights).to(gpu),
                              mla_q, kv)
+    floors_b = indexer.select_floors_buffer(gpu, queries, tokens).clone()
     torch.cuda.synchronize()
+    assert (floors_a != 0).all()
+    assert torch.equal(floors_a, floors_b)
     assert torch.equal(a.index_keys.view(torch.uint8), b.index_keys.view(torch.uint8))
     if kv_format == "fp8_paged":
         assert torch.equal(a.kv_cache, b.kv_cache)
