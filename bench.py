@@ -370,9 +370,11 @@ def main():
         torch, layer, history, tokens, topk, args.steps,
         (index_q, index_k_new, weights, mla_q, kv_new))
     # Kernel figures are the launches inside the layer step (the clock of the
-    # timed region); the isolated stage loops are reported beside them.
+    # timed region), each stage's event interval less the cost of one marker
+    # (the empty bracket); the isolated stage loops are reported beside them.
     kernel_us = dict(isolated_us)
-    kernel_us.update(in_layer)
+    kernel_us.update({name: us - in_layer["marker"] for name, us in in_layer.items()})
+    kernel_us["marker"] = in_layer["marker"]
     pairs = queries * history + queries * (queries + 1) // 2
     logits_flop = 2 * 64 * 128 * pairs
     mla_flop = 2 * queries * topk * 128 * (576 + 512)
@@ -405,6 +407,8 @@ def main():
         # cache, the new KV records packed, and the candidate top-k's per-row
         # floors.
         "prologue": {"us": round(kernel_us["prologue"], 2), "with_floors": True},
+        # Each stage's event interval before the marker is taken off.
+        "stage_us": {name: round(in_layer[name], 2) for name in STAGES[1:]},
         # Algorithmic bytes of the producer launch: per 128-value row 256 B in,
         # 128 B codes + 4 B scale out, 256 B of its RoPE row; per Q row 4 B head
         # logit in + 4 B weight out; the partial folded queries; per KV token
@@ -415,14 +419,15 @@ def main():
             "bytes": producer_bytes,
         },
         "isolated_us": {name: round(us, 2) for name, us in isolated_us.items()},
-        # The stage times come from HIP events recorded between the layer's
-        # launches, so each carries one marker (`marker_us`, an empty bracket
-        # timed the same way) and they sum above `value`, the plain step.
+        # The stage intervals come from HIP events recorded between the
+        # layer's launches, so each carries one marker (`marker_us`, an empty
+        # bracket timed the same way): they sum above `value`, the plain
+        # step; the kernel figures above have the marker taken off, and sum
+        # below `value` by the launch gaps of the plain step.
         "marker_us": round(kernel_us["marker"], 2),
-        "stage_sum_us": round(sum(kernel_us[name] for name in STAGES[1:]), 2),
-        "stage_sum_less_markers_us": round(sum(kernel_us[name] for name in STAGES[1:])
-                                           - (len(STAGES) - 1) * kernel_us["marker"], 2),
-        "stage_note": "in-layer stage times carry one event marker each; their sum exceeds value",
+        "stage_sum_us": round(sum(in_layer[name] for name in STAGES[1:]), 2),
+        "kernel_sum_us": round(sum(kernel_us[name] for name in STAGES[1:]), 2),
+        "stage_note": "kernel us = in-layer stage interval less one event marker",
     }
     dominant = max(("logits", "topk", "sparse_mla"), key=lambda k: kernel_us[k])
     traffic = None
@@ -554,18 +559,21 @@ def config4_layer(torch, args, formats=("fp8_paged", "bf16")):
         mla_flop = 2 * queries * topk * 128 * (576 + 512)
         record = 656 if kv_format == "fp8_paged" else 1152
         ids = selection.token_ids
+        # Kernel estimates: each stage interval less one event marker.
+        kernel = {name: times[name] - times["marker"] for name in STAGES[1:]}
         if reference is None:
             reference = mla_reference_f32(torch, mla_q, kv_all, ids, sample_rows, layer.scale)
         outputs[kv_format] = (out[sample_rows].float(), ids)
         result["formats"][kv_format] = {
             "layer_us": round(layer_us, 2),
+            "kernel_us": {name: round(us, 2) for name, us in kernel.items()},
             "stage_us": {name: round(us, 2) for name, us in times.items()},
-            "stage_note": "in-layer stage times carry one event marker each",
+            "stage_note": "kernel us = in-layer stage interval less one event marker (stage 'marker')",
             "candidates": candidates,
             "spilled_splits": spilled,
-            "logits_frac_fp8_peak": round(logits_flop / times["logits"] / 1e6 / PEAKS["fp8_TFLOPs"], 4),
-            "mla_frac_bf16_peak": round(mla_flop / times["sparse_mla"] / 1e6 / PEAKS["bf16_TFLOPs"], 4),
-            "gather_GBps": round(queries * topk * record / times["sparse_mla"] / 1e3, 1),
+            "logits_frac_fp8_peak": round(logits_flop / kernel["logits"] / 1e6 / PEAKS["fp8_TFLOPs"], 4),
+            "mla_frac_bf16_peak": round(mla_flop / kernel["sparse_mla"] / 1e6 / PEAKS["bf16_TFLOPs"], 4),
+            "gather_GBps": round(queries * topk * record / kernel["sparse_mla"] / 1e3, 1),
             "vs_fp32_over_bf16_kv": accuracy(torch, out[sample_rows], reference),
         }
         del layer, out
