@@ -1189,16 +1189,14 @@ __device__ __forceinline__ bool counting_sort_mask(FinishSort& fs, const uint64_
     c4[j] = fs.cursor[4 * tid + j];
     own += c4[j];
   }
-  uint32_t incl = own;  // keys in buckets of this and higher threads of the wave
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const uint32_t o = __shfl_down(incl, d);
-    if (lane + d < 64) incl += o;
-  }
+  // Keys in buckets of this and higher threads of the wave.
+  const uint32_t incl = logits_core::wave_suffix_sum(own);
   if (lane == 0) fs.wave_sums[wave] = incl;
   __syncthreads();
-  uint32_t higher = incl - own;
-  for (int w = wave + 1; w < kThreads / 64; ++w) higher += fs.wave_sums[w];
+  // Keys of the higher waves: one read of the wave totals per wave (lanes
+  // 0-15), their suffix sum, then lane wave + 1's.
+  const uint32_t totals = logits_core::wave_suffix_sum(lane < kThreads / 64 ? fs.wave_sums[lane] : 0u);
+  uint32_t higher = incl - own + __builtin_amdgcn_readlane(totals, wave + 1);
 #pragma unroll
   for (int j = 3; j >= 0; --j) {
     fs.start[4 * tid + j] = higher;
@@ -1417,14 +1415,47 @@ __global__ __launch_bounds__(kThreads, 1) void topk_candidates(float* __restrict
                                                               int64_t out_ld, CandidateLists cl,
                                                               LogitsInputs li) {
   __shared__ FinishShared lds;
-  __shared__ uint32_t info[8];  // fill, largest radix key, misfit, digit, above, bucket
+  __shared__ uint32_t info[8];  // fill, largest radix key, -, digit, above, bucket
+  __shared__ uint4 wave_parts[kThreads / 64];  // per wave: listed keys, largest radix key, misfit
   FinishSort& fs = lds.fs;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int64_t r = blockIdx.x;
   const int count = total_count < cols ? total_count : (int)cols;
+
+  // The split records and list entries are loaded first, before anything
+  // waits on memory: thread t serves key split t / T (T = kThreads / splits
+  // threads per split) and loads entries u, u + T, ... (u = t % T) of its
+  // list, whatever the record says (entries below the list's capacity, so
+  // in bounds). On the fast path - no split spilled and every list fits its
+  // threads' kSortPerThread slots - the listed ones go straight into the
+  // sort's registers.
+  constexpr int kWaves = kThreads / 64;
+  const int splits = (int)cl.splits;
+  const int per_split = kThreads / splits;  // >= 2 (splits <= 512)
+  const int sp = tid / per_split, u = tid % per_split;
+  const bool sp_live = sp < splits && (int64_t)sp * cl.per < cols;
+  const int64_t sp_at = r * cl.splits + (sp_live ? sp : 0);
+  uint64_t key[kSortPerThread];
+  uint32_t rec0, rec1;
+  {
+    const uint32_t* rec = cl.records + sp_at * 2;
+    rec0 = rec[0];
+    rec1 = rec[1];
+    const uint64_t* src = cl.lists + sp_at * cl.cap;
+#pragma unroll
+    for (int j = 0; j < kSortPerThread; ++j) {
+      const int64_t e = u + (int64_t)per_split * j;
+      key[j] = src[e < cl.cap ? e : cl.cap - 1];  // unused past the capacity
+    }
+  }
   const uint32_t floor = logits_core::row_floor(cl.floors, r);
+  // The loads stay above the floor test: without these uses the compiler
+  // sinks them into the branch that reads them, behind the floor's wait.
+  asm volatile("" : "+v"(rec0), "+v"(rec1));
+#pragma unroll
+  for (int j = 0; j < kSortPerThread; ++j) asm volatile("" : "+v"(key[j]));
   if (floor == 0) {
     select_row<kResidentVecSmall>(lds.sh, scores, cols, ld, total_count, values, ids, out_ld,
                                   nullptr, r, 0, 1);
@@ -1443,39 +1474,20 @@ __global__ __launch_bounds__(kThreads, 1) void topk_candidates(float* __restrict
     iout[i] = finite ? (int32_t)(~(uint32_t)k) : -1;
   };
   for (int i = tid; i < kSortBins; i += kThreads) fs.cursor[i] = 0;
-  if (tid < 3) info[tid] = 0;  // listed keys, largest radix key, any split not taken in registers
   if (tid == 0) fs.crowded = 0;
 
-  // Fast path: the candidates go straight into the sort's registers. Thread
-  // t serves key split t / T (T = kThreads / splits threads per split) and
-  // holds entries u, u + T, ... (u = t % T) of its list, when no split
-  // spilled and every list fits its threads' kSortPerThread slots.
-  constexpr int kWaves = kThreads / 64;
-  const int splits = (int)cl.splits;
-  const int per_split = kThreads / splits;  // >= 2 (splits <= 512)
-  const int sp = tid / per_split, u = tid % per_split;
-  uint32_t n_sp = 0;
-  int32_t spill_sp = 0x7FFFFFFF;
-  if (sp < splits && (int64_t)sp * cl.per < cols) {
-    const uint32_t* rec = cl.records + (r * cl.splits + sp) * 2;
-    n_sp = rec[0];
-    spill_sp = (int32_t)rec[1];
-  }
+  const uint32_t n_sp = sp_live ? rec0 : 0u;
+  const int32_t spill_sp = sp_live ? (int32_t)rec1 : 0x7FFFFFFF;
   const bool fits = spill_sp == 0x7FFFFFFF && n_sp <= (uint32_t)(per_split * kSortPerThread);
-  uint64_t key[kSortPerThread];
   uint32_t valid = 0, top_key = 0;
-  {
-    const uint64_t* src = cl.lists + (r * cl.splits + sp) * cl.cap;
 #pragma unroll
-    for (int j = 0; j < kSortPerThread; ++j) {
-      const uint32_t e = (uint32_t)(u + per_split * j);
-      const bool live = fits && e < n_sp;
-      key[j] = live ? src[e] : 0ull;
-      valid |= live ? 1u << j : 0u;
-      top_key = max(top_key, (uint32_t)(key[j] >> 32));
-    }
+  for (int j = 0; j < kSortPerThread; ++j) {
+    const uint32_t e = (uint32_t)(u + per_split * j);
+    const bool live = fits && e < n_sp;
+    key[j] = live ? key[j] : 0ull;
+    valid |= live ? 1u << j : 0u;
+    top_key = max(top_key, (uint32_t)(key[j] >> 32));
   }
-  __syncthreads();  // the LDS state above is set
   {
     uint32_t total = 0;
     (void)wave_prefix_any(u == 0 ? n_sp : 0u, &total);
@@ -1486,21 +1498,38 @@ __global__ __launch_bounds__(kThreads, 1) void topk_candidates(float* __restrict
     top_key = max(top_key, lane_xor<8>(top_key));
     top_key = max(top_key, lane_xor<16>(top_key));
     top_key = max(top_key, lane_xor<32>(top_key));
-    if (lane == 0) {
-      if (total) atomicAdd(&info[0], total);
-      atomicMax(&info[1], top_key);
-      if (misfit) atomicOr(&info[2], 1u);
-    }
+    if (lane == 0) wave_parts[wave] = uint4{total, top_key, misfit ? 1u : 0u, 0u};
   }
-  __syncthreads();
-  uint32_t n_cand = info[0];
-  if (info[2]) {
+  __syncthreads();  // the wave parts and the LDS state above are set
+  // The totals: lanes 0-15 of each wave read one wave's part each.
+  uint32_t n_cand, top_all;
+  bool misfit_any;
+  {
+    const uint4 part = lane < kWaves ? wave_parts[lane] : uint4{0u, 0u, 0u, 0u};
+    uint32_t tot = part.x, top = part.y;
+    // row_shl:k (0x100 + k): lane l reads lane l + k of its 16-lane row, 0 past it.
+    tot += __builtin_amdgcn_update_dpp(0u, tot, 0x101, 0xF, 0xF, false);
+    top = max(top, (uint32_t)__builtin_amdgcn_update_dpp(0u, top, 0x101, 0xF, 0xF, false));
+    tot += __builtin_amdgcn_update_dpp(0u, tot, 0x102, 0xF, 0xF, false);
+    top = max(top, (uint32_t)__builtin_amdgcn_update_dpp(0u, top, 0x102, 0xF, 0xF, false));
+    tot += __builtin_amdgcn_update_dpp(0u, tot, 0x104, 0xF, 0xF, false);
+    top = max(top, (uint32_t)__builtin_amdgcn_update_dpp(0u, top, 0x104, 0xF, 0xF, false));
+    tot += __builtin_amdgcn_update_dpp(0u, tot, 0x108, 0xF, 0xF, false);
+    top = max(top, (uint32_t)__builtin_amdgcn_update_dpp(0u, top, 0x108, 0xF, 0xF, false));
+    n_cand = __builtin_amdgcn_readfirstlane(tot);
+    top_all = __builtin_amdgcn_readfirstlane(top);
+    misfit_any = __builtin_amdgcn_ballot_w64(part.z != 0u) != 0;
+  }
+  if (misfit_any) {
     // Candidates into the LDS buffer in no order (the sort does not need
     // one): wave w takes the key splits w, w + 16, ... - lane j holds split
     // w + 16 j's record - and one LDS atomic places all their listed keys;
     // the lists are copied in chunks of 64 keys, eight chunks of loads in
     // flight at a time. Spilled scores at or above the floor follow.
-    if (tid == 0) info[0] = 0;
+    if (tid == 0) {
+      info[0] = 0;        // fill
+      info[1] = top_all;  // largest radix key
+    }
     __syncthreads();
     const int my_split = wave + kWaves * lane;
     uint32_t n_l = 0;
@@ -1569,6 +1598,7 @@ __global__ __launch_bounds__(kThreads, 1) void topk_candidates(float* __restrict
     if (lane == 0) atomicMax(&info[1], top);
     __syncthreads();
     n_cand = info[0];
+    top_all = info[1];
     valid = n_cand <= (uint32_t)kSortCap ? prefix_slots(n_cand) : 0u;
 #pragma unroll
     for (int j = 0; j < kSortPerThread; ++j)
@@ -1578,7 +1608,7 @@ __global__ __launch_bounds__(kThreads, 1) void topk_candidates(float* __restrict
   // Fewer than `count` candidates: the floor was above the count-th
   // largest score, and scores below it are missing.
   if (n_cand <= (uint32_t)kSortCap && n_cand >= (uint32_t)count) {
-    if (counting_sort_mask(fs, key, valid, n_cand, floor, info[1], count, emit)) return;
+    if (counting_sort_mask(fs, key, valid, n_cand, floor, top_all, count, emit)) return;
     // A crowded bucket: the threshold digit from the candidates' digit
     // histogram, then its keys split to exactly count - above (select_row's
     // refinement).
