@@ -78,6 +78,10 @@ def _radix(values):
         (17, 9000, 8983, 2048),      # visible counts across the no-floor bound (8192)
         (3, 140000, 139997, 1000),
         (24, 50000, 49976, 1),
+        # Many rows: one or two key splits per row, so each split's list is
+        # served by 1024 or 512 threads of the top-k work-group.
+        (2048, 20000, 17952, 2048),
+        (4096, 12000, 7904, 2048),
     ],
 )
 def test_select_equals_unfused(gpu, rows, columns, query_start, topk):
