@@ -100,11 +100,10 @@ def select_workspace(rows, tokens, device):
 
 
 def indexer_stage_calls(layer, tokens, topk, q8, folded, q_fold, workspace):
-    """The launches of the layer's indexer step (``indexer.select_topk``) as
-    separate calls: the per-row floors (in the layer prologue when it runs
-    fused, else their own launch), the logits kernel writing only the
-    candidates at or above them, and the top-k of the candidates. Returns
-    (floors_fn, logits_fn, topk_fn, ids)."""
+    """The launches of the layer's indexer step after its prologue (which
+    writes the per-row floors into ``workspace``) as separate calls: the
+    logits kernel writing only the candidates at or above the floors, and the
+    top-k of the candidates. Returns (logits_fn, topk_fn, ids)."""
     import torch
 
     from cxldsagr_amd import _native, indexer
@@ -120,10 +119,6 @@ def indexer_stage_calls(layer, tokens, topk, q8, folded, q_fold, workspace):
     head = (_native.ptr(q8), _native.ptr(keys), _native.ptr(folded), _native.ptr(kscale), None,
             None, history, rows, tokens)
 
-    def floors_fn():
-        _native.call("dsa_indexer_floors_fp8", *head, topk, _native.ptr(workspace),
-                     _native.stream_of(device))
-
     def logits_fn():
         _native.call("dsa_indexer_logits_fp8_emit", *head, width, _native.ptr(q_fold),
                      _native.ptr(scores), 0, _native.ptr(workspace), workspace.numel(),
@@ -134,7 +129,7 @@ def indexer_stage_calls(layer, tokens, topk, q8, folded, q_fold, workspace):
                      _native.ptr(values), _native.ptr(ids), count, 0, _native.ptr(workspace),
                      workspace.numel(), _native.stream_of(device))
 
-    return floors_fn, logits_fn, topk_fn, ids
+    return logits_fn, topk_fn, ids
 
 
 # "marker" is an empty bracket: two events recorded back to back, the cost
@@ -171,7 +166,7 @@ def in_layer_stage_us(torch, layer, history, tokens, topk, iters, args):
 
     layer.written = history
     q8, folded, q_fold = prologue()
-    floors_fn, logits_fn, topk_fn, ids = indexer_stage_calls(
+    logits_fn, topk_fn, ids = indexer_stage_calls(
         layer, tokens, topk, q8, folded, q_fold, workspace)
     torch.cuda.synchronize()
     for ev in marks:

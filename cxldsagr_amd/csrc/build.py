@@ -33,6 +33,12 @@ FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # The first kernel arguments arrive in SGPRs at wave launch (gfx950 kernarg
+    # preloading; the code object keeps a 256-byte prologue that loads them
+    # for firmware without it), so a kernel's first loads do not wait on the
+    # kernarg segment.
+    "-mllvm",
+    "-amdgpu-kernarg-preload-count=16",
     f"-I{ROOT / 'include'}",
 ]
 
