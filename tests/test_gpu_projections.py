@@ -228,3 +228,44 @@ def test_projection_gemms_then_producer(gpu):
     assert torch.equal(projected.q_proj, expect_q)
     expect_w = torch.nn.functional.linear(x.float(), projection.weights_proj)
     assert torch.equal(projected.head_logits, expect_w)
+
+
+def test_producer_floors_follow_rope_rows(gpu):
+    """The producer's floor blocks rotate each query with its own RoPE table
+    row (``rope_rows``): their floors equal those the layer prologue
+    estimates from the oracle's rotated queries and the matching weights."""
+    from cxldsagr_amd import indexer
+    from cxldsagr_amd.layer import index_prologue
+    from cxldsagr_amd.projections import index_producer
+
+    history, tokens = 16384, 64
+    q_proj, k_proj, head, norm_w, norm_b, _ = _inputs(tokens, seed=31)
+    _, _, _, _, _, table = _inputs(200, seed=32, start=5000)
+    rows = torch.randperm(200, generator=torch.Generator().manual_seed(33))[:tokens].int()
+    g = torch.Generator().manual_seed(34)
+    history_keys = torch.randn(history, 128, generator=g).bfloat16().to(gpu)
+    caches = []
+    for _ in range(2):
+        keys = torch.zeros((history + tokens, 128), dtype=torch.float8_e4m3fn, device=gpu)
+        scales = torch.zeros(history + tokens, dtype=torch.float32, device=gpu)
+        indexer.quantize_into(history_keys, keys[:history], scales[:history])
+        caches.append((keys, scales))
+
+    floors_a = torch.zeros((tokens, 2), dtype=torch.int32, device=gpu)
+    keys, scales = caches[0]
+    index_producer(q_proj.to(gpu), k_proj.to(gpu), head.to(gpu), norm_w.to(gpu), norm_b.to(gpu),
+                   1e-6, table.to(gpu), rows.to(gpu), index_keys=keys[history:],
+                   index_scales=scales[history:], token_offset=history, floors=floors_a,
+                   key_cache=keys, key_cache_scales=scales)
+
+    picked = table.numpy()[rows.numpy()]
+    index_q = oproj.index_q(_bits(q_proj), picked[:, :32], picked[:, 32:])
+    weights = (head.numpy() * oproj.INV_SQRT_HEADS).astype(np.float32)
+    weights = (weights * oproj.INV_SQRT_DIM).astype(np.float32)
+    floors_b = torch.zeros((tokens, 2), dtype=torch.int32, device=gpu)
+    keys, scales = caches[1]
+    index_prologue(torch.from_numpy(index_q).bfloat16().to(gpu), k_proj.to(gpu),
+                   torch.from_numpy(weights).to(gpu), keys, scales, history, 2048, floors_b)
+    torch.cuda.synchronize()
+    assert (floors_a != 0).all()
+    assert torch.equal(floors_a, floors_b)
