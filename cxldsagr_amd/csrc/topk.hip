@@ -875,6 +875,10 @@ constexpr int kSortCap = kListCap;  // candidates the one-pass counting sort tak
 constexpr int kSortBins = 4096;     // its linear buckets
 constexpr uint32_t kSortBucketMax = 128;  // keys per bucket it ranks by comparison
 constexpr int kSortPerThread = kSortCap / kThreads;
+// List slots per thread the candidate top-k loads before it knows the lists'
+// lengths (the rest after): at configs 1+2 a key split lists ~140 keys for its
+// 32 threads, i.e. ~4.4 slots per thread.
+constexpr int kSpecSlots = 5;
 constexpr int kSortEager = 4;  // key slots per thread loaded before the row's count is known
 
 struct DigitWorkspace {
@@ -1424,13 +1428,15 @@ __global__ __launch_bounds__(kThreads, 1) void topk_candidates(float* __restrict
   const int64_t r = blockIdx.x;
   const int count = total_count < cols ? total_count : (int)cols;
 
-  // The split records and list entries are loaded first, before anything
-  // waits on memory: thread t serves key split t / T (T = kThreads / splits
-  // threads per split) and loads entries u, u + T, ... (u = t % T) of its
-  // list, whatever the record says (entries below the list's capacity, so
-  // in bounds). On the fast path - no split spilled and every list fits its
-  // threads' kSortPerThread slots - the listed ones go straight into the
-  // sort's registers.
+  // The split records and the first list entries are loaded first, before
+  // anything waits on memory: thread t serves key split t / T (T = kThreads /
+  // splits threads per split) and loads entries u, u + T, ... (u = t % T) of
+  // its first kSpecSlots slots whatever the record says (entries below the
+  // list's capacity, so in bounds; slots past the list's length are wasted
+  // reads, so not all kSortPerThread are loaded blind); the later slots
+  // follow once the record says they are listed. On the fast path - no split
+  // spilled and every list fits its threads' kSortPerThread slots - the
+  // listed ones go straight into the sort's registers.
   constexpr int kWaves = kThreads / 64;
   const int splits = (int)cl.splits;
   const int per_split = kThreads / splits;  // >= 2 (splits <= 512)
@@ -1445,7 +1451,7 @@ __global__ __launch_bounds__(kThreads, 1) void topk_candidates(float* __restrict
     rec1 = rec[1];
     const uint64_t* src = cl.lists + sp_at * cl.cap;
 #pragma unroll
-    for (int j = 0; j < kSortPerThread; ++j) {
+    for (int j = 0; j < kSpecSlots; ++j) {
       const int64_t e = u + (int64_t)per_split * j;
       key[j] = src[e < cl.cap ? e : cl.cap - 1];  // unused past the capacity
     }
@@ -1455,7 +1461,7 @@ __global__ __launch_bounds__(kThreads, 1) void topk_candidates(float* __restrict
   // sinks them into the branch that reads them, behind the floor's wait.
   asm volatile("" : "+v"(rec0), "+v"(rec1));
 #pragma unroll
-  for (int j = 0; j < kSortPerThread; ++j) asm volatile("" : "+v"(key[j]));
+  for (int j = 0; j < kSpecSlots; ++j) asm volatile("" : "+v"(key[j]));
   if (floor == 0) {
     select_row<kResidentVecSmall>(lds.sh, scores, cols, ld, total_count, values, ids, out_ld,
                                   nullptr, r, 0, 1);
@@ -1479,6 +1485,14 @@ __global__ __launch_bounds__(kThreads, 1) void topk_candidates(float* __restrict
   const uint32_t n_sp = sp_live ? rec0 : 0u;
   const int32_t spill_sp = sp_live ? (int32_t)rec1 : 0x7FFFFFFF;
   const bool fits = spill_sp == 0x7FFFFFFF && n_sp <= (uint32_t)(per_split * kSortPerThread);
+  {
+    const uint64_t* src = cl.lists + sp_at * cl.cap;
+#pragma unroll
+    for (int j = kSpecSlots; j < kSortPerThread; ++j) {
+      const uint32_t e = (uint32_t)(u + per_split * j);
+      key[j] = fits && e < n_sp ? src[e] : 0ull;
+    }
+  }
   uint32_t valid = 0, top_key = 0;
 #pragma unroll
   for (int j = 0; j < kSortPerThread; ++j) {
