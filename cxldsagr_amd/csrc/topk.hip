@@ -1457,6 +1457,7 @@ __global__ __launch_bounds__(kThreads, 1) void topk_candidates(float* __restrict
     }
   }
   const uint32_t floor = logits_core::row_floor(cl.floors, r);
+  uint32_t sort_lo = floor;  // the smallest radix key the sort can meet
   // The loads stay above the floor test: without these uses the compiler
   // sinks them into the branch that reads them, behind the floor's wait.
   asm volatile("" : "+v"(rec0), "+v"(rec1));
@@ -1613,6 +1614,71 @@ __global__ __launch_bounds__(kThreads, 1) void topk_candidates(float* __restrict
     __syncthreads();
     n_cand = info[0];
     top_all = info[1];
+    if (n_cand > (uint32_t)kSortCap && n_cand >= (uint32_t)count) {
+      // More candidates than the sort holds (the floor was low): raise the
+      // floor to the level-0 digit of the row's count-th largest candidate,
+      // from a histogram of all of them, and list again those at or above
+      // it. Each pass streams the lists and the spilled scores as above.
+      auto stream = [&](auto&& sink) __attribute__((always_inline)) {
+        for (uint32_t c0 = 0; c0 < chunks_wave; c0 += kChunks) {
+          uint64_t v[kChunks];
+          bool ok[kChunks];
+#pragma unroll
+          for (int q = 0; q < kChunks; ++q) {
+            const uint32_t c = c0 + q;
+            int j = 0;
+            for (int t = 1; t < wave_splits && t < 64; ++t)
+              if (__builtin_amdgcn_readlane(chunk_pre, t) <= c) j = t;
+            const uint32_t n_j = __builtin_amdgcn_readlane(n_l, j);
+            const uint32_t i = 64 * (c - __builtin_amdgcn_readlane(chunk_pre, j)) + lane;
+            ok[q] = c < chunks_wave && i < n_j;
+            const uint64_t* src = cl.lists + (r * cl.splits + wave + kWaves * j) * cl.cap;
+            v[q] = ok[q] ? src[i] : 0ull;
+          }
+#pragma unroll
+          for (int q = 0; q < kChunks; ++q) sink(ok[q], v[q]);
+        }
+        for (int j = 0; j < wave_splits && j < 64; ++j) {
+          const int32_t spill = __builtin_amdgcn_readlane(spill_l, j);
+          if (spill == 0x7FFFFFFF) continue;
+          const int64_t kb = (int64_t)(wave + kWaves * j) * cl.per;
+          int64_t lo = spill, hi = kb + cl.per;
+          if (lo < vis_lo) lo = vis_lo;
+          if (hi > vis_hi) hi = vis_hi;
+          for (int64_t c0 = lo; c0 < hi; c0 += 64) {
+            const int64_t c = c0 + lane;
+            const float v = c < hi ? row[c] : 0.0f;
+            sink(c < hi && radix_key(v) >= floor, composite(v, c));
+          }
+        }
+      };
+      for (int i = tid; i < kBins; i += kThreads) fs.start[i] = 0;
+      __syncthreads();
+      stream([&](bool ok, uint64_t k) {
+        if (ok) atomicAdd(&fs.start[k >> 53], 1u);
+      });
+      __syncthreads();
+      if (wave == 0) {
+        const Threshold t = row_threshold(fs.start, (uint32_t)count);
+        if (lane == 0) {
+          info[3] = t.digit;
+          info[4] = t.above + t.bucket;
+        }
+      }
+      if (tid == 0) info[0] = 0;
+      __syncthreads();
+      if (info[4] <= (uint32_t)kSortCap) {
+        const uint32_t raised = max(floor, info[3] << 21);
+        stream([&](bool ok, uint64_t k) {
+          const bool keep = ok && (uint32_t)(k >> 32) >= raised;
+          const uint32_t slot = wave_slot(&info[0], keep);
+          if (keep && slot < (uint32_t)kSortCap) fs.sorted[slot] = k;
+        });
+        __syncthreads();
+        n_cand = info[0];  // == info[4]
+        sort_lo = raised;
+      }
+    }
     valid = n_cand <= (uint32_t)kSortCap ? prefix_slots(n_cand) : 0u;
 #pragma unroll
     for (int j = 0; j < kSortPerThread; ++j)
@@ -1622,7 +1688,7 @@ __global__ __launch_bounds__(kThreads, 1) void topk_candidates(float* __restrict
   // Fewer than `count` candidates: the floor was above the count-th
   // largest score, and scores below it are missing.
   if (n_cand <= (uint32_t)kSortCap && n_cand >= (uint32_t)count) {
-    if (counting_sort_mask(fs, key, valid, n_cand, floor, top_all, count, emit)) return;
+    if (counting_sort_mask(fs, key, valid, n_cand, sort_lo, top_all, count, emit)) return;
     // A crowded bucket: the threshold digit from the candidates' digit
     // histogram, then its keys split to exactly count - above (select_row's
     // refinement).

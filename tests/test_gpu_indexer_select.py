@@ -152,6 +152,26 @@ def test_select_forced_recompute(gpu):
     _same(got, (values, ids))
 
 
+@pytest.mark.parametrize("cap", [0, 512])
+def test_select_more_candidates_than_the_sort_holds(gpu, cap):
+    """Floors far below the count-th score (~16K candidates per row, more than
+    the 8,192 the sort holds): the top-k raises the floor to the threshold
+    digit of the candidates and lists again, with the lists spilling (default
+    capacity) or holding every candidate (512 slots per split); the result
+    must not change."""
+    from cxldsagr_amd import indexer
+
+    rows, columns, query_start, topk = 32, 50000, 49968, 2048
+    q, k, w, s = _inputs(rows, columns, gpu, seed=16000 + cap)
+    scores, values, ids = _unfused(q, k, w, s, query_start, topk)
+    low = torch.topk(scores[:, :columns], 16000, dim=1).values[:, -1]
+    radix = _radix(low)
+    floors = torch.where(radix >= 2**31, radix - 2**32, radix).to(torch.int32)
+    got = indexer.select_topk(q, k, w, s, query_start, topk, _floors=floors, _list_cap=cap)
+    torch.cuda.synchronize()
+    _same(got, (values, ids))
+
+
 @pytest.mark.parametrize("cap", [64, 128, 192])
 def test_select_spills(gpu, cap):
     """Short candidate lists make the splits spill their scores to the score
