@@ -1389,10 +1389,12 @@ __global__ __launch_bounds__(kThreads, 1) void topk_digit_finish(const float* __
 // row. A row with F = 0 was stored in full. The candidates - listed keys and
 // spilled scores at or above F - hold every score of the row at or above F,
 // so when there are at least `count` of them they hold the row's top
-// `count` (and the top-k of the candidates is the row's). Otherwise (F was
-// above the row's count-th largest score), or when they do not fit the
-// work-group, the row's scores are recomputed here with the logits kernel's
-// arithmetic (logits_core.h) and selected from in full.
+// `count` (and the top-k of the candidates is the row's). When there are
+// more than the sort holds, the floor is raised to the level-0 digit of the
+// count-th largest candidate and the candidates are listed again. Otherwise
+// (F was above the row's count-th largest score, or the raised floor still
+// leaves too many), the row's scores are recomputed here with the logits
+// kernel's arithmetic (logits_core.h) and selected from in full.
 struct CandidateLists {
   const uint32_t* floors;   // [rows][2] the row's floor (row_floor), 0 when stored in full
   const uint32_t* records;  // [rows][splits][2]: keys listed, first spilled column

@@ -222,8 +222,9 @@ def select_topk(q, k, weights, kscale, query_start, topk, *, _bounds=None, _q_fo
     ~1/64 of each row's scores; the logits kernel writing only the composite
     top-k keys of the scores at or above the floor (per key split, ~4K per
     row at 64K keys, instead of every score); the exact top-k of those
-    candidates, which recomputes a row in full when it holds fewer than
-    ``min(topk, N)`` of them. This replaces the reference's ``logits`` then
+    candidates, which raises a row's floor when it holds more candidates
+    than its sort takes (8,192) and recomputes a row in full when it holds
+    fewer than ``min(topk, N)`` of them. This replaces the reference's ``logits`` then
     ``exact_topk`` (``models/deepseek_v32/attention.py:338-363``); the
     per-query score buckets of its fused ECHO kernel play the same role
     (``indexer/csrc/echo_logits.cuh:497-561``).
@@ -233,7 +234,7 @@ def select_topk(q, k, weights, kscale, query_start, topk, *, _bounds=None, _q_fo
     floors launch is skipped. ``_list_cap`` (candidate slots per row and key
     split, 0 = default) and ``_floors`` (uint32 ``[Q]`` radix keys replacing
     the estimated floors, as int32) are test hooks: small lists force
-    spills, high floors force the recompute.
+    spills, high floors force the recompute and low ones the raised floor.
     """
     if type(topk) is not int or not 1 <= topk <= 2048:
         raise ValueError("k must be an integer in [1, 2048]")
