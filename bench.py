@@ -650,11 +650,14 @@ def bench_config3(args):
     user. Per user and layer: logits -> top-k -> exact recall (gather of the misses from pinned
     host) -> sparse MLA over the pool. Rounds 1-2 run the users one after another, as the
     reference's runner does; rounds 3-4 run them through ``MultiUserStep`` (each user's recall
-    on a second stream, overlapping its neighbours' indexer and sparse MLA)."""
+    on a second stream, overlapping its neighbours' indexer and sparse MLA); rounds 5-8 run the
+    users one after another again, each user's batch through ``ChunkedForward`` in 2 (rounds
+    5-6) or 4 (rounds 7-8) chunks of rows (each chunk's recall overlapping the next chunk's
+    indexer and the previous chunk's sparse MLA, within the one request)."""
     import torch
 
     from cxldsagr_amd.layer import OffloadDSALayer
-    from cxldsagr_amd.multi_user import MultiUserStep
+    from cxldsagr_amd.multi_user import ChunkedForward, MultiUserStep
     from cxldsagr_amd.token_pool import TokenPool
     from cxldsagr_amd.workloads import make_layer_inputs
 
@@ -673,6 +676,7 @@ def bench_config3(args):
         del inputs
     torch.cuda.synchronize()
     step = MultiUserStep(layers)
+    chunked = {c: ChunkedForward(pool, c) for c in (2, 4)}
 
     def round_inputs(round_seed):
         per_user = []
@@ -694,8 +698,16 @@ def bench_config3(args):
             timing.append((e0, e1))
             pool.attend(mla_q, physical, layer.scale)
 
+    def chunked_round(batches, chunks):
+        for layer, batch in zip(layers, batches):
+            if not chunked[chunks].overlaps(layer, queries, transient=True):
+                raise RuntimeError("config 3's pool must hold two users' selections")
+            chunked[chunks].forward(layer, *batch, transient=True)
+
     rounds = []
-    for r, mode in enumerate(("sequential", "sequential", "overlapped", "overlapped")):
+    modes = ("sequential", "sequential", "overlapped", "overlapped",
+             "chunked-2", "chunked-2", "chunked-4", "chunked-4")
+    for r, mode in enumerate(modes):
         batches = round_inputs(r + 1)
         before = pool.metrics()["recalled_records"]
         timing = []
@@ -705,8 +717,10 @@ def bench_config3(args):
         start.record()
         if mode == "sequential":
             sequential(batches, timing)
-        else:
+        elif mode == "overlapped":
             step.transient_round(batches)
+        else:
+            chunked_round(batches, int(mode.split("-")[1]))
         stop.record()
         torch.cuda.synchronize()
         pool.check_status()

@@ -130,13 +130,15 @@ def _check_paged(cache, page_table, device):
 
 
 def sparse_mla_fp8_paged(q, kv_cache, page_table, indices, scale, value_dim=512, *,
-                         n_tokens=None):
+                         n_tokens=None, _out=None):
     """Sparse MLA over the fp8 paged cache; same semantics as ``sparse_mla`` on the
     dequantised records.
 
     ``kv_cache`` is uint8 ``[pages, 64, 656]``; logical token ``t`` lives at
     page ``page_table[t // 64]``, slot ``t % 64``. Ids outside ``[0, n_tokens)``
-    (default: every token the page table covers) are padding.
+    (default: every token the page table covers) are padding. ``_out``
+    (contiguous, ``q``'s dtype and device, ``[Q, H, value_dim]``) receives the
+    result instead of a new tensor.
     """
     if q.ndim != 3 or indices.ndim != 2 or q.shape[0] != indices.shape[0]:
         raise ValueError("Expected q [Q,H,D] and indices [Q,K] with matching Q")
@@ -150,9 +152,18 @@ def sparse_mla_fp8_paged(q, kv_cache, page_table, indices, scale, value_dim=512,
         n_tokens = page_table.numel() * PAGE_TOKENS
     if type(n_tokens) is not int or not 0 <= n_tokens <= page_table.numel() * PAGE_TOKENS:
         raise ValueError("n_tokens must be covered by the page table")
+    shape = (*q.shape[:2], value_dim)
+    if _out is None:
+        out = torch.empty(shape, dtype=q.dtype, device=q.device)
+    elif (not isinstance(_out, torch.Tensor) or tuple(_out.shape) != shape or _out.dtype != q.dtype
+          or _out.device != q.device or not _out.is_contiguous()
+          or _out.data_ptr() % 8):
+        raise ValueError("_out must be a contiguous, 8-byte aligned [Q, H, value_dim] tensor "
+                         "of q's dtype on q's device")
+    else:
+        out = _out
     if not q.shape[0] or not n_tokens or not indices.shape[1]:
-        return torch.zeros((*q.shape[:2], value_dim), dtype=q.dtype, device=q.device)
-    out = torch.empty((*q.shape[:2], value_dim), dtype=q.dtype, device=q.device)
+        return out.zero_()
     q = _aligned(q)
     cache = _aligned(kv_cache)
     table = page_table.contiguous()

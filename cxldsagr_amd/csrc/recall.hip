@@ -14,7 +14,8 @@
 // Everything runs on the stream with the miss count kept on the device, so
 // there is no host read when the history fits the pool (then every union
 // fits too). The (rank, slot) order is one rocPRIM radix sort of 64-bit keys
-// over the pool's slots, the role CUB's radix sort plays in the reference
+// over the pool's slots (on the rank bits only: the keys arrive in slot
+// order and the sort is stable), the role CUB's radix sort plays in the reference
 // (operators/deepseek_v32/indexer/csrc/echo_sparse_recall.cuh:191).
 #include <cstring>
 #include <mutex>
@@ -234,11 +235,18 @@ struct Workspace {
 
 size_t align_up(size_t x) { return (x + 255) & ~size_t(255); }
 
+// The victim order sorts one key per pool slot on a few rank bits. rocPRIM
+// takes its merge sort up to 2^20 keys (about 19 launches whatever the bit
+// range); a merge-sort limit of 0 selects its onesweep radix sort, about one
+// pass per 8 key bits.
+using VictimSortConfig = rocprim::radix_sort_config<rocprim::default_config, rocprim::default_config,
+                                                    rocprim::default_config, 0>;
+
 int plan(int64_t slots, int64_t history_capacity, uint8_t* base, Workspace* ws) {
   size_t sort_bytes = 0;
-  hipError_t err = rocprim::radix_sort_keys(nullptr, sort_bytes, (const uint64_t*)nullptr,
-                                            (uint64_t*)nullptr, (size_t)(slots + 1), 0, 64,
-                                            (hipStream_t)0, false);
+  hipError_t err = rocprim::radix_sort_keys<VictimSortConfig>(
+      nullptr, sort_bytes, (const uint64_t*)nullptr, (uint64_t*)nullptr, (size_t)(slots + 1), 0,
+      64, (hipStream_t)0, false);
   if (err != hipSuccess) {
     set_error("rocprim radix sort sizing failed: %s", hipGetErrorString(err));
     return kLaunchFailed;
@@ -362,9 +370,27 @@ int recall_impl(const int32_t* indices, int64_t n, const int32_t* page_table,
                      ws.misses, ws.counters, stats);
   hipLaunchKernelGGL(recall_victim_keys, dim3((unsigned)((slots + 1 + 255) / 256)), dim3(256), 0,
                      stream, d2h, priority, ws.kept_bits, slots, keep_floor, ws.keys);
-  size_t sort_bytes = ws.sort_bytes;
-  hipError_t err = rocprim::radix_sort_keys(ws.sort_temp, sort_bytes, ws.keys, ws.sorted,
-                                            (size_t)(slots + 1), 0, 64, stream, false);
+  // The keys arrive in slot order and the radix sort is stable, so sorting
+  // only the rank bits (32 .. 32 + rank_bits) gives the (rank, slot) order of
+  // a full 64-bit sort. Every stored priority is an earlier stamp, below
+  // chosen_stamp, so rank + 1 <= chosen_stamp < 2^rank_bits - 1, the value
+  // the kept slots' all-ones keys take in that range: they still sort last.
+  // A few passes instead of eight.
+  int rank_bits = 2;
+  while (((int64_t)1 << (rank_bits - 1)) <= chosen_stamp) ++rank_bits;
+  size_t sort_bytes = 0;
+  hipError_t err = rocprim::radix_sort_keys<VictimSortConfig>(
+      nullptr, sort_bytes, (const uint64_t*)nullptr, (uint64_t*)nullptr, (size_t)(slots + 1), 32,
+      32 + rank_bits, stream, false);
+  if (err == hipSuccess && sort_bytes > ws.sort_bytes) {
+    set_error("rocprim radix sort needs %zu bytes of temporary storage, planned %zu",
+              sort_bytes, ws.sort_bytes);
+    return kLaunchFailed;
+  }
+  if (err == hipSuccess)
+    err = rocprim::radix_sort_keys<VictimSortConfig>(ws.sort_temp, sort_bytes, ws.keys, ws.sorted,
+                                                     (size_t)(slots + 1), 32, 32 + rank_bits,
+                                                     stream, false);
   if (err != hipSuccess) {
     set_error("rocprim radix sort failed: %s", hipGetErrorString(err));
     return kLaunchFailed;

@@ -332,12 +332,15 @@ class OffloadDSALayer:
             out = self.consume(q, ids, written=end)
         return out, TokenSelection(ids)
 
-    def select(self, index_q, index_k, weights):
-        """The indexer half of ``forward`` for a batch at ``session.written``:
-        quantise the batch's index Q (folding its scales into the head
-        weights) and index K (into the resident cache), fp8 logits over every
-        visible key, exact top-k; returns the int32 ``[rows, topk]`` ids."""
-        position = self.session.written
+    def select(self, index_q, index_k, weights, *, position=None):
+        """The indexer half of ``forward`` for a batch at ``position`` (default
+        ``session.written``): quantise the batch's index Q (folding its scales
+        into the head weights) and index K (into the resident cache), fp8
+        logits over every visible key, exact top-k; returns the int32
+        ``[rows, topk]`` ids. Keys before ``position`` must be in the cache."""
+        position = self.session.written if position is None else position
+        if type(position) is not int or position < 0:
+            raise ValueError("position must be a nonnegative integer")
         end = position + len(index_q)
         if end > self.capacity or len(index_k) != len(index_q) or len(weights) != len(index_q):
             raise ValueError("query batch exceeds the layer capacity or inputs disagree in length")

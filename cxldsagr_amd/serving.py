@@ -38,6 +38,7 @@ from typing import Any, Hashable
 import torch
 
 from cxldsagr_amd.layer import OffloadDSALayer
+from cxldsagr_amd.multi_user import ChunkedForward
 from cxldsagr_amd.token_pool import PAGE_SIZE, RECORD_BYTES
 
 
@@ -157,9 +158,14 @@ class GRServingRunner:
     optional ``commit`` (append the candidates to the history instead of a
     transient step, with ``commit_signature`` the identity of the extended
     history).
+
+    ``chunks`` > 1 runs each layer's candidate batch through
+    ``multi_user.ChunkedForward``: the recall of each chunk of rows overlaps
+    the indexer of the next (same outputs; the reference runner recalls after
+    the whole batch's top-k).
     """
 
-    def __init__(self, pools, *, topk=2048, scale=576 ** -0.5):
+    def __init__(self, pools, *, topk=2048, scale=576 ** -0.5, chunks=1):
         if not pools:
             raise ValueError("GRServingRunner needs at least one layer pool")
         arenas = {pool.host_capacity for pool in pools}
@@ -172,6 +178,9 @@ class GRServingRunner:
                               release=self._release)
         self.visits = {}
         self.closed = False
+        if type(chunks) is not int or chunks < 1:
+            raise ValueError("chunks must be a positive integer")
+        self.pipelines = [ChunkedForward(pool, chunks) for pool in self.pools] if chunks > 1 else None
 
     # ------------------------------------------------------------- sessions
     def _allocate(self, capacity):
@@ -235,9 +244,12 @@ class GRServingRunner:
                 raise ValueError("cached history length differs from history_tokens")
             prefixed = time.perf_counter()
             outputs, selections = [], []
-            for layer, (index_q, index_k, weights, q, kv) in zip(layers, request["candidates"]):
-                out, selection = layer.forward(index_q, index_k, weights, q, kv,
-                                               transient=not commit)
+            for index, (layer, batch) in enumerate(zip(layers, request["candidates"])):
+                if self.pipelines is None:
+                    out, selection = layer.forward(*batch, transient=not commit)
+                else:
+                    out, selection = self.pipelines[index].forward(layer, *batch,
+                                                                   transient=not commit)
                 outputs.append(out)
                 selections.append(selection)
             torch.cuda.synchronize(self.device)

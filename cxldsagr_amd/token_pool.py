@@ -254,11 +254,12 @@ class TokenPool:
         if self._second_workspace is None:
             self._second_workspace = torch.empty_like(self.workspace)
 
-    def attend(self, q, physical, scale, value_dim=512):
-        """Sparse MLA over recalled pool records (``sparse_mla_from_pool``)."""
+    def attend(self, q, physical, scale, value_dim=512, *, out=None):
+        """Sparse MLA over recalled pool records (``sparse_mla_from_pool``);
+        ``out`` (optional) receives the result."""
         rows = self.record_pages * PAGE_SIZE
         return attention.sparse_mla_fp8_paged(q, self.records, self.identity_pages, physical,
-                                              scale, value_dim, n_tokens=rows)
+                                              scale, value_dim, n_tokens=rows, _out=out)
 
     def check_status(self):
         """Raise if a recall flagged an unwritten id or an overfull union (synchronises)."""

@@ -453,10 +453,13 @@ int dsa_pool_workspace_bytes(int64_t slots, int64_t history_capacity, int64_t* b
  * d2h / priority int64 [slots + 1] (slot 0 is the sentinel), records
  * [record_rows, record_bytes] on the device, host records pinned
  * [host_rows, record_bytes]. Hits are stamped protect_stamp, recalled slots
- * chosen_stamp. stats int64 [4] accumulates union, recalled, evicted.
+ * chosen_stamp; stamps form a FIFO clock: every priority already stored is
+ * below this call's chosen_stamp (victims are ordered by priority, then slot).
+ * stats int64 [4] accumulates union, recalled, evicted.
  * status bits: 4 = an id at or past `written`, 8 = the union did not fit.
  * With history_end > slots the caller must pass union_checked != 0 after
- * checking the union size. physical: int32 [n].
+ * checking the union size. physical: int32 [n]. Not for HIP graph capture:
+ * the victim sort (rocPRIM) clears its buffers with hipMemsetAsync.
  */
 int dsa_pool_recall(const int32_t* indices, int64_t n, const int32_t* page_table,
                     int64_t history_end, int64_t written, int64_t transient_start, int64_t slots,

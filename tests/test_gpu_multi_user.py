@@ -123,3 +123,88 @@ def test_overlapped_users_equal_sequential_outputs(gpu, users, history, rows, to
         live = _check_maps(pool)
         assert 0 < live <= slots
     assert pool.metrics()["evicted_records"] > 0
+
+
+@pytest.mark.parametrize("rows,chunks,commit", [(64, 2, False), (67, 3, False), (128, 4, True)])
+def test_chunked_request_equals_resident_attention(gpu, rows, chunks, commit):
+    """A request's batch in chunks of rows (``ChunkedForward``), each chunk's
+    recall overlapping the next chunk's indexer: every output equals, bit for
+    bit, sparse MLA over a fully resident fp8 cache of the same records on the
+    same selection, and the selections equal ``select`` over the whole batch.
+    Three users, two requests each, on a pool that holds two users' histories,
+    so later requests evict; uneven chunks (67 rows in 3); transient and
+    committed batches."""
+    from cxldsagr_amd.attention import pack_kv_fp8, sparse_mla_fp8_paged
+    from cxldsagr_amd.layer import OffloadDSALayer
+    from cxldsagr_amd.multi_user import ChunkedForward
+    from cxldsagr_amd.token_pool import TokenPool
+    from cxldsagr_amd.workloads import make_layer_inputs
+
+    history, topk, users, visits = 4096, 2048, 3, 2
+    grown = (history + visits * rows + 63) // 64 * 64   # whole 64-token host pages
+    slots = 2 * grown
+    pool = TokenPool(users * grown, slots, device=gpu, candidate_slots=rows,
+                     history_capacity=grown)
+    pipeline = ChunkedForward(pool, chunks)
+    pages = (grown + 63) // 64
+    identity = torch.arange(pages, dtype=torch.int32, device=gpu)
+    layers, caches = [], []
+    for u in range(users):
+        inputs = make_layer_inputs(history, rows, seed=71 + u)
+        layer = OffloadDSALayer(pool, pool.allocate_session(grown), grown + rows, topk=topk)
+        kv = inputs.kv[:history].to(gpu)
+        layer.write_history(inputs.index_k[:history].to(gpu), kv)
+        cache = torch.zeros(pages, 64, 656, dtype=torch.uint8, device=gpu)
+        pack_kv_fp8(kv, cache, identity)
+        layers.append(layer)
+        caches.append(cache)
+    for visit in range(visits):
+        for u in range(users):
+            layer, cache = layers[u], caches[u]
+            fresh = make_layer_inputs(0, rows, seed=5000 + 100 * visit + u)
+            index_q, index_k, weights, q, kv = (getattr(fresh, n).to(gpu) for n in
+                                                ("index_q", "index_k", "weights", "mla_q", "kv"))
+            position = layer.written
+            assert pipeline.overlaps(layer, rows, transient=not commit)
+            print(f"chunked request: user {u} visit {visit} rows {rows} chunks {chunks}", flush=True)
+            out, selection = pipeline.forward(layer, index_q, index_k, weights, q, kv,
+                                              transient=not commit)
+            torch.cuda.synchronize()
+            assert pool.check_status() == 0
+            assert layer.written == position + (rows if commit else 0)
+            expected_ids = layer.select(index_q, index_k, weights, position=position)
+            assert torch.equal(selection.token_ids, expected_ids), (visit, u)
+            pack_kv_fp8(kv, cache, identity, token_offset=position)
+            expected = sparse_mla_fp8_paged(q, cache, identity, expected_ids, 576**-0.5,
+                                            n_tokens=position + rows)
+            assert torch.equal(out.view(torch.int16), expected.view(torch.int16)), (visit, u)
+        live = _check_maps(pool)
+        assert 0 < live <= slots
+    assert pool.metrics()["evicted_records"] > 0
+
+
+def test_chunked_request_runs_sequentially_when_two_chunks_may_not_fit(gpu):
+    """With less than two histories of slots the pipeline would have to evict
+    the previous chunk's kept slots: it runs the batch as ``forward`` does."""
+    from cxldsagr_amd.layer import OffloadDSALayer
+    from cxldsagr_amd.multi_user import ChunkedForward
+    from cxldsagr_amd.token_pool import TokenPool
+    from cxldsagr_amd.workloads import make_layer_inputs
+
+    history, rows = 4096, 64
+    pool = TokenPool(history, history + 100, device=gpu, candidate_slots=rows,
+                     history_capacity=history)
+    inputs = make_layer_inputs(history, rows, seed=9)
+    layer = OffloadDSALayer(pool, pool.allocate_session(history), history + rows, topk=2048)
+    layer.write_history(inputs.index_k[:history].to(gpu), inputs.kv[:history].to(gpu))
+    pipeline = ChunkedForward(pool, 2)
+    assert not pipeline.overlaps(layer, rows, transient=True)
+    batch = [getattr(inputs, n)[-rows:].to(gpu) if n in ("index_k", "kv") else getattr(inputs, n).to(gpu)
+             for n in ("index_q", "index_k", "weights", "mla_q", "kv")]
+    out, selection = pipeline.forward(layer, *batch, transient=True)
+    again, second = layer.forward(*batch, transient=True)
+    torch.cuda.synchronize()
+    assert torch.equal(selection.token_ids, second.token_ids)
+    assert torch.equal(out.view(torch.int16), again.view(torch.int16))
+    with pytest.raises(ValueError, match="chunks"):
+        ChunkedForward(pool, 0)
