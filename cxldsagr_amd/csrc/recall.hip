@@ -57,18 +57,85 @@ __global__ void recall_mark(const int32_t* __restrict__ indices, int64_t n, int6
   if (id >= 0 && id < history_end) atomicOr(&sel_bits[id >> 5], 1u << (id & 31));
 }
 
+// recall_mark with the bitmap first built in LDS (a selection repeats ids
+// across its rows, so the global words would take ~n / words atomics each):
+// each work-group ORs its share of the ids into its own copy, then adds each
+// nonzero word to the global bitmap once. For bitmaps of at most
+// kMarkLdsWords words.
+constexpr int kMarkThreads = 1024;
+constexpr int kMarkLdsWords = 8192;    // 262,144 history ids, 32 KB of LDS
+constexpr int kMarkIdsPerThread = 8;
+constexpr int kMarkIdsPerBlock = kMarkThreads * kMarkIdsPerThread;
+__global__ __launch_bounds__(kMarkThreads) void recall_mark_lds(
+    const int32_t* __restrict__ indices, int64_t n, int64_t history_end, int64_t written,
+    uint32_t* __restrict__ sel_bits, int32_t* __restrict__ status) {
+  __shared__ uint32_t local[kMarkLdsWords];
+  const int64_t words = (history_end + 31) >> 5;
+  for (int64_t w = threadIdx.x; w < words; w += kMarkThreads) local[w] = 0u;
+  __syncthreads();
+  const int64_t begin = (int64_t)blockIdx.x * kMarkIdsPerBlock + threadIdx.x;
+  int64_t ids[kMarkIdsPerThread];
+#pragma unroll
+  for (int k = 0; k < kMarkIdsPerThread; ++k) {  // all loads first, then the LDS ORs
+    const int64_t i = begin + (int64_t)k * kMarkThreads;
+    ids[k] = i < n ? indices[i] : -1;
+  }
+  bool unwritten = false;
+#pragma unroll
+  for (int k = 0; k < kMarkIdsPerThread; ++k) {
+    const int64_t id = ids[k];
+    if (id >= written) unwritten = true;
+    else if (id >= 0 && id < history_end) atomicOr(&local[id >> 5], 1u << (id & 31));
+  }
+  if (unwritten && status) atomicOr(status, kUnwritten);
+  __syncthreads();
+  for (int64_t w = threadIdx.x; w < words; w += kMarkThreads) {
+    const uint32_t bits = local[w];
+    if (bits) atomicOr(&sel_bits[w], bits);
+  }
+}
+
 __device__ __forceinline__ int64_t to_global(const int32_t* page_table, int64_t t) {
   return (int64_t)page_table[t / kPage] * kPage + t % kPage;
 }
 
-// One work-group walks the selection bitmap in order. Thread t of a round
-// owns one 32-id word; hits are protected, misses are counted, and a block
-// scan places each thread's misses so the list is in ascending logical order.
-__global__ __launch_bounds__(kClassifyThreads) void recall_classify(
+// Hits and misses of the selection, one thread per history id: a selected
+// id's global host row through the page table, then h2d; a hit's slot is
+// protected (priority = protect_stamp, kept bit), a miss sets its bit in
+// miss_bits. The loads of all ids are independent, so they overlap. A wave
+// covers two 32-id words and writes them from its ballot.
+__global__ __launch_bounds__(256) void recall_lookup(
     const uint32_t* __restrict__ sel_bits, int64_t history_end,
     const int32_t* __restrict__ page_table, const int32_t* __restrict__ h2d,
     int64_t* __restrict__ priority, uint32_t* __restrict__ kept_bits, int64_t protect_stamp,
-    int64_t* __restrict__ misses, int64_t* __restrict__ counters, int64_t* __restrict__ stats) {
+    uint32_t* __restrict__ miss_bits) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const bool in = t < history_end;
+  const uint32_t word = in ? sel_bits[t >> 5] : 0u;
+  bool miss = false;
+  if ((word >> (t & 31)) & 1u) {
+    const int32_t d = h2d[to_global(page_table, t)];
+    if (d != kMissing) {
+      priority[d] = protect_stamp;
+      atomicOr(&kept_bits[d >> 5], 1u << (d & 31));
+    } else {
+      miss = true;
+    }
+  }
+  const uint64_t m = __builtin_amdgcn_ballot_w64(miss);
+  const int64_t words = (history_end + 31) >> 5;
+  const int64_t w = (t >> 5);  // lane 0: the wave's first word, lane 32: its second
+  if ((lane & 31) == 0 && w < words) miss_bits[w] = (uint32_t)(m >> lane);
+}
+
+// One work-group scans the miss bitmap in order: thread t of a round owns
+// one 32-id word, and a block scan gives each word the position of its first
+// miss in the list (ascending logical order). Also counts the union.
+__global__ __launch_bounds__(kClassifyThreads) void recall_classify(
+    const uint32_t* __restrict__ sel_bits, const uint32_t* __restrict__ miss_bits,
+    int64_t history_end, int32_t* __restrict__ word_offset, int64_t* __restrict__ counters,
+    int64_t* __restrict__ stats) {
   __shared__ uint32_t wave_sums[kClassifyThreads / 64];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -78,18 +145,7 @@ __global__ __launch_bounds__(kClassifyThreads) void recall_classify(
   for (int64_t base = 0; base < words; base += kClassifyThreads) {
     const int64_t w = base + tid;
     const uint32_t bits = w < words ? sel_bits[w] : 0u;
-    uint32_t miss_mask = 0;
-    for (uint32_t rest = bits; rest; rest &= rest - 1) {
-      const int b = __builtin_ctz(rest);
-      const int64_t t = w * 32 + b;
-      const int32_t d = h2d[to_global(page_table, t)];
-      if (d != kMissing) {
-        priority[d] = protect_stamp;
-        atomicOr(&kept_bits[d >> 5], 1u << (d & 31));
-      } else {
-        miss_mask |= 1u << b;
-      }
-    }
+    const uint32_t miss_mask = w < words ? miss_bits[w] : 0u;
     const uint32_t mine = __builtin_popcount(miss_mask);
     uint32_t incl = mine;
 #pragma unroll
@@ -106,11 +162,7 @@ __global__ __launch_bounds__(kClassifyThreads) void recall_classify(
       if (i < wave) before += s;
       total += s;
     }
-    int64_t slot = running + before + incl - mine;
-    for (uint32_t rest = miss_mask; rest; rest &= rest - 1) {
-      const int b = __builtin_ctz(rest);
-      misses[slot++] = to_global(page_table, w * 32 + b);
-    }
+    if (w < words) word_offset[w] = (int32_t)(running + before + incl - mine);
     running += total;
     // union count: reduce popcounts through the same scratch after a barrier
     __syncthreads();
@@ -128,6 +180,21 @@ __global__ __launch_bounds__(kClassifyThreads) void recall_classify(
     atomicAdd(reinterpret_cast<unsigned long long*>(&stats[0]), (unsigned long long)union_total);
     atomicAdd(reinterpret_cast<unsigned long long*>(&stats[1]), (unsigned long long)running);
   }
+}
+
+// The miss list, one thread per history id: a missed id's global host row
+// at its word's first position plus the misses before it in the word.
+__global__ __launch_bounds__(256) void recall_emit(const uint32_t* __restrict__ miss_bits,
+                                                   const int32_t* __restrict__ word_offset,
+                                                   int64_t history_end,
+                                                   const int32_t* __restrict__ page_table,
+                                                   int64_t* __restrict__ misses) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= history_end) return;
+  const uint32_t m = miss_bits[t >> 5];
+  const uint32_t bit = 1u << (t & 31);
+  if (!(m & bit)) return;
+  misses[word_offset[t >> 5] + __builtin_popcount(m & (bit - 1u))] = to_global(page_table, t);
 }
 
 // Sort keys of the victim order; kept slots (the sentinel, this selection's
@@ -157,25 +224,33 @@ __global__ void recall_assign(const uint64_t* __restrict__ sorted,
                               int64_t* __restrict__ stats, int32_t* __restrict__ status) {
   const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t m = counters[kMisses];
-  if (j >= m) return;
-  const uint64_t key = sorted[j];
-  if (key == ~0ull) {
-    if (status) atomicOr(status, kShortPool);
-    chosen[j] = -1;
-    return;
+  bool evicted = false;
+  if (j < m) {
+    const uint64_t key = sorted[j];
+    if (key == ~0ull) {
+      if (status) atomicOr(status, kShortPool);
+      chosen[j] = -1;
+    } else {
+      const int64_t s = (int64_t)(key & 0xFFFFFFFFull);
+      const int64_t old = d2h[s];
+      if (old != kMissing) {
+        h2d[old] = kMissing;
+        evicted = true;
+      }
+      const int64_t g = misses[j];
+      d2h[s] = g;
+      h2d[g] = (int32_t)s;
+      priority[s] = stamp;
+      chosen[j] = s;
+    }
   }
-  const int64_t s = (int64_t)(key & 0xFFFFFFFFull);
-  const int64_t old = d2h[s];
-  if (old != kMissing) {
-    h2d[old] = kMissing;
-    atomicAdd(reinterpret_cast<unsigned long long*>(&counters[kEvicted]), 1ull);
-    atomicAdd(reinterpret_cast<unsigned long long*>(&stats[2]), 1ull);
+  // One pair of counter atomics per wave (every lane reaches the ballot).
+  const uint64_t ev = __builtin_amdgcn_ballot_w64(evicted);
+  if (ev && (threadIdx.x & 63) == 0) {
+    const unsigned long long k = (unsigned long long)__builtin_popcountll(ev);
+    atomicAdd(reinterpret_cast<unsigned long long*>(&counters[kEvicted]), k);
+    atomicAdd(reinterpret_cast<unsigned long long*>(&stats[2]), k);
   }
-  const int64_t g = misses[j];
-  d2h[s] = g;
-  h2d[g] = (int32_t)s;
-  priority[s] = stamp;
-  chosen[j] = s;
 }
 
 // records[chosen[j]] = host[misses[j]] for j < m; one wave per record.
@@ -223,6 +298,8 @@ __global__ void recall_map(const int32_t* __restrict__ indices, int64_t n, int64
 struct Workspace {
   uint32_t* sel_bits;
   uint32_t* kept_bits;
+  uint32_t* miss_bits;
+  int32_t* word_offset;
   int64_t* misses;
   int64_t* chosen;
   uint64_t* keys;
@@ -259,6 +336,8 @@ int plan(int64_t slots, int64_t history_capacity, uint8_t* base, Workspace* ws) 
   };
   ws->sel_bits = reinterpret_cast<uint32_t*>(take(((history_capacity + 31) / 32) * 4));
   ws->kept_bits = reinterpret_cast<uint32_t*>(take(((slots + 1 + 31) / 32) * 4));
+  ws->miss_bits = reinterpret_cast<uint32_t*>(take(((history_capacity + 31) / 32) * 4));
+  ws->word_offset = reinterpret_cast<int32_t*>(take(((history_capacity + 31) / 32) * 4));
   ws->misses = reinterpret_cast<int64_t*>(take(history_capacity * 8));
   ws->chosen = reinterpret_cast<int64_t*>(take(history_capacity * 8));
   ws->keys = reinterpret_cast<uint64_t*>(take((slots + 1) * 8));
@@ -326,6 +405,7 @@ int recall_impl(const int32_t* indices, int64_t n, const int32_t* page_table,
   DSA_CHECK_ARG(n >= 0 && slots >= 1 && history_end >= 0 && written >= history_end,
                 "invalid recall shape");
   DSA_CHECK_ARG(history_end <= history_capacity, "history exceeds the planned workspace");
+  DSA_CHECK_ARG(history_end < 0x7FFFFFFF, "history ids must fit int32");
   DSA_CHECK_ARG(history_end <= slots || union_checked,
                 "recall without a host check needs history <= slots; otherwise the caller "
                 "must have checked that the selection's union fits the pool");
@@ -362,12 +442,22 @@ int recall_impl(const int32_t* indices, int64_t n, const int32_t* page_table,
   const int64_t clear_n = sel_words > kept_words ? sel_words : kept_words;
   hipLaunchKernelGGL(recall_clear, dim3((unsigned)((clear_n + 255) / 256 + 1)), dim3(256), 0,
                      stream, ws.sel_bits, sel_words, ws.kept_bits, kept_words, ws.counters);
-  if (n > 0)
+  if (n > 0 && (history_end + 31) / 32 <= kMarkLdsWords)
+    hipLaunchKernelGGL(recall_mark_lds, dim3((unsigned)((n + kMarkIdsPerBlock - 1) / kMarkIdsPerBlock)),
+                       dim3(kMarkThreads), 0, stream, indices, n, history_end, written, ws.sel_bits,
+                       status);
+  else if (n > 0)
     hipLaunchKernelGGL(recall_mark, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
                        indices, n, history_end, written, ws.sel_bits, status);
+  if (history_end > 0)
+    hipLaunchKernelGGL(recall_lookup, dim3((unsigned)((history_end + 255) / 256)), dim3(256), 0,
+                       stream, ws.sel_bits, history_end, page_table, h2d, priority, ws.kept_bits,
+                       protect_stamp, ws.miss_bits);
   hipLaunchKernelGGL(recall_classify, dim3(1), dim3(kClassifyThreads), 0, stream, ws.sel_bits,
-                     history_end, page_table, h2d, priority, ws.kept_bits, protect_stamp,
-                     ws.misses, ws.counters, stats);
+                     ws.miss_bits, history_end, ws.word_offset, ws.counters, stats);
+  if (history_end > 0)
+    hipLaunchKernelGGL(recall_emit, dim3((unsigned)((history_end + 255) / 256)), dim3(256), 0,
+                       stream, ws.miss_bits, ws.word_offset, history_end, page_table, ws.misses);
   hipLaunchKernelGGL(recall_victim_keys, dim3((unsigned)((slots + 1 + 255) / 256)), dim3(256), 0,
                      stream, d2h, priority, ws.kept_bits, slots, keep_floor, ws.keys);
   // The keys arrive in slot order and the radix sort is stable, so sorting
