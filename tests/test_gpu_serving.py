@@ -225,3 +225,48 @@ def test_failed_requests_discard_the_session_and_budget_errors_evict_nothing(gpu
         assert result.metrics["prefix_cache_hit"]
         for pool in pools:
             assert pool.check_status() == 0
+
+
+def test_chunked_requests_equal_resident_attention(gpu):
+    """``GRServingRunner(chunks=2)``: each layer's candidate batch runs as two
+    chunks of rows whose recalls overlap (``multi_user.ChunkedForward``); on
+    pools that hold two histories the pipeline is taken, and every output
+    still equals, bit for bit, sparse MLA over a fully resident cache of the
+    user's records on the same selection, through a miss, a committed append
+    and a hit on the extended history."""
+    from cxldsagr_amd.serving import GRServingRunner
+    from cxldsagr_amd.token_pool import TokenPool
+
+    grown = HISTORY + QUERIES
+    pools = [TokenPool(2 * grown, 2 * grown, device=gpu, candidate_slots=QUERIES,
+                       history_capacity=grown) for _ in range(LAYERS)]
+    users = Users(gpu)
+    with GRServingRunner(pools, topk=TOPK, chunks=2) as runner:
+        first = users.candidates(4, 0)
+        print("chunked serving: miss with commit", flush=True)
+        result = runner.execute({"user_id": 4, "signature": "h4", "history_tokens": HISTORY,
+                                 "history": users.history(4), "candidates": first,
+                                 "commit": True, "commit_signature": "h4+1"})
+        layers = runner.lru._entries[4].session
+        assert all(runner.pipelines[i].overlaps(layer, QUERIES, transient=True)
+                   for i, layer in enumerate(layers))
+        for layer in range(LAYERS):
+            kv = torch.cat((users.history_kv(4, layer), first[layer][4]))
+            ref = _resident_reference(gpu, kv, result.selections[layer], first[layer][3])
+            torch.cuda.synchronize()
+            assert torch.equal(result.outputs[layer].view(torch.int16), ref.view(torch.int16))
+        second = users.candidates(4, 1)
+        print("chunked serving: hit, transient", flush=True)
+        result = runner.execute({"user_id": 4, "signature": "h4+1", "history_tokens": grown,
+                                 "history": None, "candidates": second})
+        assert result.metrics["prefix_cache_hit"]
+        for layer in range(LAYERS):
+            kv = torch.cat((users.history_kv(4, layer), first[layer][4], second[layer][4]))
+            ref = _resident_reference(gpu, kv, result.selections[layer], second[layer][3])
+            torch.cuda.synchronize()
+            assert torch.equal(result.outputs[layer].view(torch.int16), ref.view(torch.int16))
+        for pool in pools:
+            assert pool.check_status() == 0
+            assert _check_maps(pool) > 0
+    with pytest.raises(ValueError, match="chunks"):
+        GRServingRunner(pools, chunks=0)
