@@ -256,7 +256,7 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported here "
-              "(the DSA layer is single-GPU; see DESIGN.md for how it would shard)",
+              "(the DSA layer step is measured on one GPU's share of the work)",
               file=sys.stderr)
         sys.exit(2)
     import torch

@@ -205,7 +205,7 @@ int dsa_indexer_topk_fp8(const void* q, const void* k, const float* weights, con
                          hipStream_t stream);
 
 /*
- * A4 + A6 fused without the score matrix (the SURVEY (f)1 indexer step that
+ * A4 + A6 fused without the score matrix (the fused indexer step that
  * writes only top-k candidates): the same values and indices as
  * dsa_indexer_logits_fp8 followed by dsa_topk_radix over its [rows, columns]
  * scores, bit for bit, for every input. Replaces the reference's logits()
