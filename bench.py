@@ -47,6 +47,8 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-config4", action="store_true",
                    help="skip the compact config-4 layer time of the default line")
+    p.add_argument("--no-config3", action="store_true",
+                   help="skip the compact config-3 layer times of the default line")
     p.add_argument("--only", choices=["layer", "logits", "topk", "mla", "producer"], default=None,
                    help="time only one stage (for profiler runs)")
     p.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -479,6 +481,18 @@ def main():
         # same way; the full config-4 report is `bench.py --config 4`.
         result["config4_fp8_paged_us"] = config4_layer(torch, args, ("fp8_paged",))[
             "formats"]["fp8_paged"]["layer_us"]
+    if not args.no_config3:
+        # BASELINE config 3 (16 users x 65,536 fp8 history records in pinned host
+        # memory, a 262,144-slot pool): one layer for all users, the second of two
+        # rounds with the users in sequence and with the overlapped multi-user
+        # step; the full report is `bench.py --config 3`.
+        rounds, _ = config3_rounds(args, ("sequential", "sequential", "overlapped", "overlapped"))
+        result["config3_layer_us"] = {
+            "users": args.users,
+            "sequential": rounds[1]["layer_us"],
+            "overlapped": rounds[3]["layer_us"],
+            "fetch_bytes_per_layer": rounds[3]["fetch_bytes_per_layer"],
+        }
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(inputs, args.cpu_rows, topk)
     print(json.dumps(result))
@@ -644,16 +658,30 @@ def pcie_reference(pool, records=262144, reps=5, seed=11):
 
 
 def bench_config3(args):
+    """The full config-3 report: every round mode, the PCIe reference and the
+    serving runner (``config3_rounds`` for the rounds)."""
+    rounds, reference = config3_rounds(
+        args, ("sequential", "sequential", "overlapped", "overlapped",
+               "chunked-2", "chunked-2", "chunked-4", "chunked-4"), reference=True)
+    history, queries, topk = 65536, 128, 2048
+    print(json.dumps({"config": 3, "users": args.users, "history": history, "queries": queries,
+                      "pool_slots": args.users * history // 4, "rounds": rounds,
+                      "pcie_reference": reference,
+                      "serving": bench_serving(args, args.users, history, queries, topk)}))
+
+
+def config3_rounds(args, modes, reference=False):
     """GR multi-user recall: `users` sessions of 65536 fp8 history records
     in a pinned host arena, a shared HBM pool of 25 % of all history (262,144 slots for 16
     users), resident indexer keys for every user, rounds of 128 fresh candidate tokens per
     user. Per user and layer: logits -> top-k -> exact recall (gather of the misses from pinned
-    host) -> sparse MLA over the pool. Rounds 1-2 run the users one after another, as the
-    reference's runner does; rounds 3-4 run them through ``MultiUserStep`` (each user's recall
-    on a second stream, overlapping its neighbours' indexer and sparse MLA); rounds 5-8 run the
-    users one after another again, each user's batch through ``ChunkedForward`` in 2 (rounds
-    5-6) or 4 (rounds 7-8) chunks of rows (each chunk's recall overlapping the next chunk's
-    indexer and the previous chunk's sparse MLA, within the one request)."""
+    host) -> sparse MLA over the pool. One round per entry of ``modes``: "sequential" runs the
+    users one after another, as the reference's runner does; "overlapped" runs them through
+    ``MultiUserStep`` (each user's recall on a second stream, overlapping its neighbours'
+    indexer and sparse MLA); "chunked-N" runs the users one after another, each user's batch
+    through ``ChunkedForward`` in N chunks of rows (each chunk's recall overlapping the next
+    chunk's indexer and the previous chunk's sparse MLA, within the one request). Returns the
+    rounds' reports and, with ``reference``, the box's PCIe reference rates."""
     import torch
 
     from cxldsagr_amd.layer import OffloadDSALayer
@@ -705,8 +733,6 @@ def bench_config3(args):
             chunked[chunks].forward(layer, *batch, transient=True)
 
     rounds = []
-    modes = ("sequential", "sequential", "overlapped", "overlapped",
-             "chunked-2", "chunked-2", "chunked-4", "chunked-4")
     for r, mode in enumerate(modes):
         batches = round_inputs(r + 1)
         before = pool.metrics()["recalled_records"]
@@ -741,12 +767,11 @@ def bench_config3(args):
         else:
             entry["pcie_GBps_over_layer"] = round(fetch_bytes / (entry["layer_us"] * 1e3), 2)
         rounds.append(entry)
-    reference = pcie_reference(pool)
-    del step, layers, pool
+    pcie = pcie_reference(pool) if reference else None
+    del step, chunked, layers, pool
     torch.cuda.synchronize()
-    print(json.dumps({"config": 3, "users": users, "history": history, "queries": queries,
-                      "pool_slots": slots, "rounds": rounds, "pcie_reference": reference,
-                      "serving": bench_serving(args, users, history, queries, topk)}))
+    torch.cuda.empty_cache()
+    return rounds, pcie
 
 
 def bench_serving(args, users, history, queries, topk):
