@@ -282,3 +282,35 @@ def test_contract_adapters_equal_layer_forward(gpu, kv_format):
     assert torch.equal(out.view(torch.int16), out_ref.view(torch.int16))
     with pytest.raises(ValueError, match="TokenSelection"):
         LayerAttention(layer)(x["mla_q"], None, layer, context)
+
+
+def test_layer_step_repeats_bit_exact_on_a_side_stream(gpu):
+    """64 layer steps in a row at configs 1+2 size on a non-default stream:
+    every output and selection is bit-equal to the first step's, so no stage
+    reads a workspace (the per-stream floors, split records and candidate
+    lists, the top-k's sort scratch, the pool of MLA records) that a later
+    launch has already overwritten (the reference's stage-reuse check repeats
+    its fused indexer 64 times, test_echo_indexer.py:227-245)."""
+    from cxldsagr_amd.layer import DSALayer
+    from cxldsagr_amd.workloads import make_layer_inputs
+
+    history, queries = 65536, 128
+    inputs = make_layer_inputs(history, queries, seed=4242)
+    layer = DSALayer(history + queries, device=gpu, kv_format="fp8_paged",
+                     page_table=inputs.page_table)
+    layer.write_history(inputs.index_k[:history].to(gpu), inputs.kv[:history].to(gpu))
+    args = tuple(x.to(gpu) for x in (inputs.index_q, inputs.index_k[history:], inputs.weights,
+                                     inputs.mla_q, inputs.kv[history:]))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    outs, ids = [], []
+    with torch.cuda.stream(side):
+        for _ in range(64):
+            layer.written = history
+            out, selection = layer.forward(*args)
+            outs.append(out)
+            ids.append(selection.token_ids)
+    side.synchronize()
+    for step in range(1, 64):
+        assert torch.equal(ids[step], ids[0]), step
+        assert torch.equal(outs[step].view(torch.int16), outs[0].view(torch.int16)), step
