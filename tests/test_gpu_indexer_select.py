@@ -253,3 +253,44 @@ def test_layer_prologue_floors(gpu):
     _, selection = layer.forward(index_q, index_k, weights, mla_q, kv)
     torch.cuda.synchronize()
     assert torch.equal(selection.token_ids, ids)
+
+
+@pytest.mark.parametrize("case", range(24))
+def test_select_random_shapes_bounds_caps_and_floors(gpu, case):
+    """Seeded random cases over every path of the candidate top-k at once:
+    row counts 1-300, rows of 1-70K columns, top-k 1-2048, causal or ragged
+    bounds, default or short candidate lists (spills), and floors estimated,
+    absent, or forced at a random rank of each row's scores (recompute when
+    above its count-th score, the raised floor when far below). Every case
+    equals the unfused logits -> exact_topk bit for bit."""
+    from cxldsagr_amd import indexer
+
+    rng = np.random.default_rng(9000 + case)
+    rows = int(rng.integers(1, 301))
+    columns = int(rng.integers(max(rows, 16), 70001))
+    topk = int(rng.choice([1, 7, 100, 1000, 2048]))
+    query_start = columns - rows
+    q, k, w, s = _inputs(rows, columns, gpu, seed=100 + case, heavy=float(rng.choice([0.0, 0.05, 0.3])))
+    bounds = None
+    if rng.random() < 0.4:
+        ends = rng.integers(1, columns + 1, rows)
+        starts = (ends * rng.random(rows) * 0.5).astype(np.int64)
+        bounds = (torch.from_numpy(starts.astype(np.int32)).to(gpu),
+                  torch.from_numpy(ends.astype(np.int32)).to(gpu))
+    scores, values, ids = _unfused(q, k, w, s, query_start, topk, bounds)
+    hooks = {}
+    if rng.random() < 0.3:
+        hooks["_list_cap"] = int(rng.choice([64, 128, 256, 512]))
+    mode = rng.choice(["estimated", "none", "forced"])
+    if mode != "estimated":
+        keys = _radix(scores[:, :columns])  # -inf columns have the lowest keys
+        if mode == "none":
+            floors = torch.zeros(rows, dtype=torch.int64, device=gpu)
+        else:
+            ranks = torch.from_numpy(rng.integers(1, min(columns, 20000) + 1, rows)).to(gpu)
+            floors = torch.sort(keys, dim=1, descending=True).values.gather(1, (ranks - 1)[:, None])[:, 0]
+        hooks["_floors"] = torch.where(floors >= 2**31, floors - 2**32, floors).to(torch.int32)
+    print(f"random select case {case}: rows {rows} columns {columns} topk {topk} bounds "
+          f"{bounds is not None} mode {mode} hooks {sorted(hooks)}", flush=True)
+    got = indexer.select_topk(q, k, w, s, query_start, topk, _bounds=bounds, **hooks)
+    _same(got, (values, ids))
