@@ -517,7 +517,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
       if constexpr (kS) s_prev = sa;
     } else {
       // ---- rows of block it + 1 (its buffer last held block it - 3) in
-      // eight rounds beside the PV MFMAs; the records of block it +
+      // 32 quarters beside the PV MFMAs; the records of block it +
       // kLookahead into the freed registers.
       const uint32_t rec = kS ? lane_base(buf_of(it + 1), (uint32_t)kk * kRowBytes + 32 * j) : 0;
       const v4u* st = pool + decltype(set)::value;
@@ -544,20 +544,45 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
           }
         }
       };
-      // Two rounds first (the checks' reads land meanwhile), then the PV
-      // MFMAs with the other rounds spread over them.
-      constexpr int kRounds = kS ? 8 : 0;
-      constexpr int kFirst = kRounds > 2 ? 2 : kRounds;
-#pragma unroll
-      for (int r = 0; r < kFirst; ++r) unpack_round(r);
+      // The rounds in quarters (two conversions each; the row's two 16-byte
+      // halves stored after quarters 1 and 3), one quarter after each PV
+      // MFMA: a 16-cycle MFMA hides about two VALU instructions, so whole
+      // rounds (eight conversions) after every sixth MFMA stalled its pipe.
+      v4u part_lo = v4u{0u, 0u, 0u, 0u}, part_hi = v4u{0u, 0u, 0u, 0u};
+      auto unpack_quarter = [&](int i, int u) __attribute__((always_inline)) {
+        if (kFp8) {
+          const float s_i = __builtin_bit_cast(v4f, st[8])[i >> 1];
+          const v4u w = st[i];
+          if (u == 0) {
+            part_lo.x = dequant_pair<false>(w.x, s_i);
+            part_lo.y = dequant_pair<true>(w.x, s_i);
+          } else if (u == 1) {
+            part_lo.z = dequant_pair<false>(w.y, s_i);
+            part_lo.w = dequant_pair<true>(w.y, s_i);
+            lds_store<v4u>(rec + 128 * i, part_lo);
+          } else if (u == 2) {
+            part_hi.x = dequant_pair<false>(w.z, s_i);
+            part_hi.y = dequant_pair<true>(w.z, s_i);
+          } else {
+            part_hi.z = dequant_pair<false>(w.w, s_i);
+            part_hi.w = dequant_pair<true>(w.w, s_i);
+            lds_store<v4u>(rec + 128 * i + 16, part_hi);
+            if (i == 7) {
+              lds_store<v4u>(rec + 2 * kVDim, st[9]);
+              lds_store<v4u>(rec + 2 * kVDim + 16, st[10]);
+            }
+          }
+        } else if (u == 3) {
+          unpack_round(i);  // bf16 records: stores only
+        }
+      };
       checks();
-      constexpr int kLeft = kRounds - kFirst;
-      constexpr int kSpread = kLeft > 0 && kPvMfmas / kLeft > 1 ? kPvMfmas / kLeft : 1;
-      constexpr int kSteps = kPvMfmas > kSpread * kLeft ? kPvMfmas : kSpread * kLeft;
+      constexpr int kQuarters = kS ? 32 : 0;
+      constexpr int kSteps = kPvMfmas > kQuarters ? kPvMfmas : kQuarters;
 #pragma unroll
       for (int k = 0; k < kSteps; ++k) {
         if (k < kPvMfmas) pv_mfma(k);
-        if (k % kSpread == 0 && k / kSpread < kLeft) unpack_round(kFirst + k / kSpread);
+        if (k < kQuarters) unpack_quarter(k / 4, k % 4);
         __builtin_amdgcn_sched_barrier(0);
       }
       if constexpr (kS) {
