@@ -307,11 +307,16 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
     const int32_t page = page_table[in ? id / kPageTokens : 0];
     return in ? page : -1;
   };
-  int32_t ring_id[2] = {-1, -1}, ring_page[2] = {-1, -1};
+  // Ring state per step parity: the id and page of the block whose row the
+  // step stores, and the id loaded for the block two steps after it.
+  int32_t ring_id[2] = {-1, -1}, ring_page[2] = {-1, -1}, id_keep[2] = {-1, -1};
   if (!scorer) {
-    ring_id[0] = id_load(kRingAhead);
-    ring_id[1] = id_load(kRingAhead + 1);
-    ring_page[1] = page_load(ring_id[0]);
+    id_keep[0] = id_load(kRingAhead);
+    id_keep[1] = id_load(kRingAhead + 1);
+    ring_page[0] = page_load(id_keep[0]);
+    ring_page[1] = page_load(id_keep[1]);
+    ring_id[0] = id_load(kRingAhead + 2);
+    ring_id[1] = id_load(kRingAhead + 3);
     // The records of blocks 0 and 1 from this lane's own id and page loads,
     // without waiting for the ring.
     const int32_t id0 = id_load(0), id1 = id_load(1);
@@ -587,17 +592,21 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
       }
       if constexpr (kS) {
         // Ring: row of block it + kRingAhead (its slot held block it - 2)
-        // from the id loaded two steps and the page loaded one step earlier;
-        // then the page of block it + 7 and the id of block it + 8. These
-        // loads go out before the record loads, so that waiting for them next
-        // step waits for nothing the step does not wait for anyway. Loaded
-        // values live in one register per step parity and are never copied
-        // (a copy would wait for the load); the four lanes of a key store the
+        // from its id and page, both landed two steps ago; then the page of
+        // block it + kRingAhead + 2 from its id (loaded two steps ago, kept
+        // for the row two steps from now) and the id of block it +
+        // kRingAhead + 4. Each link of the id -> page -> row chain thus has
+        // two steps to land (with one step each, the load waves waited
+        // ~640 ticks per step here). These loads go out before the record
+        // loads, so that waiting for them waits for nothing the step does not
+        // wait for anyway. Loaded values live in one register per step parity
+        // and are copied only once landed; the four lanes of a key store the
         // same value.
-        constexpr int kP = decltype(parity)::value, kQ = 1 - kP;
-        lds.ring[(it + kRingAhead) % kRing][kk] = phys_from(ring_id[kP], ring_page[kQ]);
-        ring_page[kP] = page_load(ring_id[kQ]);
-        ring_id[kP] = id_load(it + kRingAhead + 2);
+        constexpr int kP = decltype(parity)::value;
+        lds.ring[(it + kRingAhead) % kRing][kk] = phys_from(id_keep[kP], ring_page[kP]);
+        id_keep[kP] = ring_id[kP];
+        ring_page[kP] = page_load(ring_id[kP]);
+        ring_id[kP] = id_load(it + kRingAhead + 4);
         fetch(set, phys_next);
         phys_next = row_of(it + kLookahead + 1);
       }
