@@ -308,8 +308,9 @@ __global__ __launch_bounds__(256) void kv_pack_fp8(const uint16_t* __restrict__ 
 // the hardware conversion - the floor is an estimate, and the exact codes
 // are the Q blocks') and scores its samples with four MFMAs per 16 (each
 // wave a quarter of them, all 64 heads; the MFMAs of one group are issued
-// before the previous group's head sum). The query loads are issued first,
-// then the sample loads.
+// before the previous group's head sum). The query loads are issued first
+// and the sample loads after the quantisation: issued before it, they
+// delayed the query rows it waits for (~1.5k ticks per block).
 constexpr int kPrologueFloorSamples = 2048;  // per row (both halves)
 constexpr int kPrologueFloorBatch = 8;  // 16-sample groups per wave in flight together
 constexpr float kPrologueFloorSigmas = 3.5f;
@@ -387,15 +388,13 @@ __device__ void prologue_floor(int64_t i, int half, const uint16_t* __restrict__
       ks[j] = fa.key_scales[key];
     }
   };
-  // The query loads first (the quantisation waits for them alone), then the
-  // sample loads (the MFMAs wait for them after the quantisation).
+  // The query loads first; the sample loads after the quantisation.
   uint4 qraw[4];
   {
     const uint4* src = reinterpret_cast<const uint4*>(q + ((i * kHeads + (tid >> 2)) * kDim + 32 * (tid & 3)));
 #pragma unroll
     for (int c = 0; c < 4; ++c) qraw[c] = src[c];
   }
-  load_batch(wave);
   // Quantise the row's heads: thread t takes head t / 4, dims 32 (t % 4) ..
   // + 31 (the row amax over its four threads).
   {
@@ -467,6 +466,7 @@ __device__ void prologue_floor(int64_t i, int half, const uint16_t* __restrict__
       }
     }
   }
+  load_batch(wave);
 #pragma unroll
   for (int j = 0; j < 8; ++j) hist[8 * tid + j] = 0;
   if (tid < 4) result[tid] = 0;
