@@ -311,6 +311,12 @@ __global__ __launch_bounds__(256) void kv_pack_fp8(const uint16_t* __restrict__ 
 // before the previous group's head sum). The query loads are issued first
 // and the sample loads after the quantisation: issued before it, they
 // delayed the query rows it waits for (~1.5k ticks per block).
+// The prologue launches are bound by load latency (808 blocks at configs
+// 1+2, two thirds of them short): three resident blocks per CU (168
+// registers, no scratch) instead of the two that 190 registers allowed took
+// the launch from 10.2 to 9.1 us (4.2 us without floor blocks) and config
+// 4's from 41 to 35 us; four would spill.
+constexpr int kPrologueBlocksPerCu = 3;
 constexpr int kPrologueFloorSamples = 2048;  // per row (both halves)
 constexpr int kPrologueFloorBatch = 8;  // 16-sample groups per wave in flight together
 constexpr float kPrologueFloorSigmas = 3.5f;
@@ -521,7 +527,7 @@ __device__ void prologue_floor(int64_t i, int half, const uint16_t* __restrict__
 // cache, and nf more blocks (when floors are asked for; placed first)
 // compute the candidate top-k's per-row floors, two blocks per row. All are independent of
 // each other.
-__global__ __launch_bounds__(256) void layer_prologue(
+__global__ __launch_bounds__(256, kPrologueBlocksPerCu) void layer_prologue(
     const uint16_t* __restrict__ q, int64_t q_rows, const float* __restrict__ weights,
     uint8_t* __restrict__ q_codes, float* __restrict__ q_scales, float* __restrict__ w_folded,
     float* __restrict__ q_fold, const uint16_t* __restrict__ k, int64_t k_rows,
@@ -780,7 +786,7 @@ __device__ __forceinline__ QuantLane produce_rows_d128(
 // then [0, nq): index Q rows (RoPE, quantise, weight fold, partial folded
 // queries); [nq, nq + nk): index K rows (LayerNorm, RoPE, quantise into the
 // resident cache); the rest: new KV tokens into the fp8 paged cache.
-__global__ __launch_bounds__(256) void index_producer(
+__global__ __launch_bounds__(256, kPrologueBlocksPerCu) void index_producer(
     const uint16_t* __restrict__ q, int64_t q_rows, const float* __restrict__ head, float pre,
     float post, uint8_t* __restrict__ q_codes, float* __restrict__ q_scales,
     float* __restrict__ w_folded, float* __restrict__ q_fold, const uint16_t* __restrict__ k,
