@@ -314,3 +314,47 @@ def test_layer_step_repeats_bit_exact_on_a_side_stream(gpu):
     for step in range(1, 64):
         assert torch.equal(ids[step], ids[0]), step
         assert torch.equal(outs[step].view(torch.int16), outs[0].view(torch.int16)), step
+
+
+# Seeded layer shapes off the benchmark's: histories that are not multiples
+# of the 64-token page or the 128-key logits stage, query counts that are not
+# multiples of the 16-query logits work-group, rows that see fewer than 2048
+# keys (their selection ends in -1 ids), and histories below the floors'
+# 8192-column minimum (rows selected from their full scores) as well as above.
+RANDOM_LAYERS = [
+    # (history, queries, seed)
+    (1500, 600, 101),     # rows 0 .. 546 see fewer than 2048 keys
+    (5000, 9, 102),       # below the floor minimum: no floors
+    (8192 + 37, 5, 103),  # just above it
+    (12345, 17, 104),
+    (30001, 33, 105),
+    (65536 + 100, 3, 106),
+]
+
+
+@pytest.mark.parametrize(("history", "queries", "seed"), RANDOM_LAYERS)
+def test_layer_random_shapes_match_oracle(gpu, history, queries, seed):
+    """Logits, selection (with -1 past a row's visible keys) and sparse MLA
+    on every query row of seeded shapes, to the bars of the fixed configs."""
+    inputs, out, ids, scores = _run_layer(gpu, history, queries, seed=seed)
+    rows = np.arange(queries)
+    cache, ref_scores, ref_values, ref_ids = _oracle(inputs, rows)
+    tokens = history + queries
+    ref = ref_scores[:, :tokens]
+    gpu_scores = scores.cpu().numpy()[:, :tokens]
+    visible = np.isfinite(ref)
+    np.testing.assert_array_equal(np.isfinite(gpu_scores), visible)
+    np.testing.assert_allclose(gpu_scores[visible], ref[visible], atol=2e-3, rtol=1e-3)
+
+    gpu_ids = ids.cpu().numpy()
+    for i in range(queries):
+        seen = history + i + 1
+        live = min(seen, TOPK)
+        # Every slot past the row's visible keys is -1, and only those.
+        assert (gpu_ids[i, live:] == -1).all() and (gpu_ids[i, :live] >= 0).all(), i
+        assert (ref_ids[i, live:] == -1).all(), i
+        kth = float(ref_values[i, live - 1])
+        _check_selection(gpu_ids[i, :live], ref_ids[i, :live], ref[i], kth)
+
+    _, expected = omla.sparse_mla(inputs.mla_q.float().numpy(), cache.records, gpu_ids, SCALE)
+    _check_attention(out.float().cpu().numpy(), expected)
