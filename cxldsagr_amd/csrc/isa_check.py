@@ -15,7 +15,11 @@ condition ``__builtin_amdgcn_readfirstlane(wave) & 1`` turns it into a scalar
 branch.)
 
 This module compiles each source to gfx950 assembly with the library's flags
-and reports every MFMA that sits in a masked side with no EXEC-zero skip.
+and reports every MFMA that sits in a masked side with no EXEC-zero skip. It
+also reports every kernel that spills to scratch memory beyond the spills
+listed in KNOWN_SPILLS: the kernels' occupancy and speed are tuned to their
+register counts (the layer prologue to three work-groups per CU at 168
+registers), and a spill is the first sign that a change pushed one over.
 Usage: ``python -m cxldsagr_amd.csrc.isa_check`` (exit status 1 on a finding).
 """
 
@@ -29,6 +33,13 @@ from pathlib import Path
 from cxldsagr_amd.csrc import build
 
 _LABEL = re.compile(r"^(_Z[\w.$]+):")
+_KERNEL = re.compile(r"^\s*\.amdhsa_kernel\s+(\S+)")
+_SCRATCH = re.compile(r"^\s*\.amdhsa_private_segment_fixed_size\s+(\d+)")
+
+# Spills accepted as they are: (substring of the kernel symbol, bytes per lane).
+# topk_rows<17> keeps 68 scores per thread in registers for rows of up to
+# 69,632 columns (configs 1+2 of the unfused top-k) and spills 28 bytes.
+KNOWN_SPILLS = {"topk_rowsILi17E": 28}
 
 
 def unguarded_mfma(asm):
@@ -67,6 +78,27 @@ def unguarded_mfma(asm):
     return found
 
 
+def scratch_bytes(asm):
+    """``{kernel symbol: scratch bytes per lane}`` for each kernel of ``asm``
+    with a nonzero private segment."""
+    found, kernel = {}, None
+    for raw in asm.splitlines():
+        m = _KERNEL.match(raw)
+        if m:
+            kernel = m.group(1)
+            continue
+        m = _SCRATCH.match(raw)
+        if m and kernel and int(m.group(1)):
+            found[kernel] = int(m.group(1))
+    return found
+
+
+def unknown_spills(found):
+    """The entries of ``found`` (``scratch_bytes``) that KNOWN_SPILLS does not list."""
+    return {kernel: size for kernel, size in found.items()
+            if not any(key in kernel and size == known for key, known in KNOWN_SPILLS.items())}
+
+
 def device_asm(source, out_dir):
     """gfx950 assembly of one source with the library's compile flags."""
     out = Path(out_dir) / (Path(source).stem + ".s")
@@ -78,23 +110,39 @@ def device_asm(source, out_dir):
     return out.read_text()
 
 
-def check(sources=None):
-    """``{source name: findings}`` for every source with a finding."""
-    sources = list(sources or build.sources())
+def _texts(sources):
     with tempfile.TemporaryDirectory() as tmp, ThreadPoolExecutor(max_workers=8) as pool:
-        texts = list(pool.map(lambda s: device_asm(s, tmp), sources))
-    report = {}
-    for source, text in zip(sources, texts):
+        return list(pool.map(lambda s: device_asm(s, tmp), sources))
+
+
+def analyse(sources=None):
+    """``(mfma, spills)``: ``{source name: unguarded_mfma findings}`` and
+    ``{source name: {kernel: bytes}}`` of the spills KNOWN_SPILLS does not
+    list, each holding only the sources with a finding."""
+    sources = list(sources or build.sources())
+    mfma, spills = {}, {}
+    for source, text in zip(sources, _texts(sources)):
         findings = unguarded_mfma(text)
         if findings:
-            report[Path(source).name] = findings
-    return report
+            mfma[Path(source).name] = findings
+        extra = unknown_spills(scratch_bytes(text))
+        if extra:
+            spills[Path(source).name] = extra
+    return mfma, spills
+
+
+def check(sources=None):
+    """``{source name: findings}`` for every source with an unguarded MFMA."""
+    return analyse(sources)[0]
 
 
 if __name__ == "__main__":
-    problems = check()
+    problems, spills = analyse()
     for name, findings in problems.items():
         for function, line, start in findings[:5]:
             print(f"{name}: {function}: MFMA at assembly line {line} in the masked side "
                   f"opened at line {start}, with no s_cbranch_execz skip")
-    sys.exit(1 if problems else 0)
+    for name, kernels in spills.items():
+        for kernel, size in kernels.items():
+            print(f"{name}: {kernel}: {size} bytes of scratch per lane")
+    sys.exit(1 if problems or spills else 0)

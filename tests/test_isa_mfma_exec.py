@@ -1,6 +1,7 @@
 """Build check: no MFMA of the library sits in an EXEC-masked block that the
 GPU would run with EXEC = 0 (MFMAs ignore EXEC, so such a block overwrites
-its accumulator). The scanner is pinned on hand-written assembly first."""
+its accumulator), and no kernel spills to scratch beyond the listed spills.
+The scanners are pinned on hand-written assembly first."""
 
 import shutil
 
@@ -77,7 +78,31 @@ def test_scanner_flags_unskipped_sides():
     assert [line for _, line, _ in found] == [6]
 
 
+KERNEL_DESCRIPTORS = """
+.amdhsa_kernel _ZN3dsa12_GLOBAL__N_1fastE
+    .amdhsa_private_segment_fixed_size 0
+.end_amdhsa_kernel
+.amdhsa_kernel _ZN3dsa12_GLOBAL__N_19topk_rowsILi17EEEvPKf
+    .amdhsa_private_segment_fixed_size 28
+.end_amdhsa_kernel
+.amdhsa_kernel _ZN3dsa12_GLOBAL__N_114layer_prologueE
+    .amdhsa_private_segment_fixed_size 212
+.end_amdhsa_kernel
+"""
+
+
+def test_scratch_report_names_each_spilling_kernel():
+    found = isa_check.scratch_bytes(KERNEL_DESCRIPTORS)
+    assert found == {"_ZN3dsa12_GLOBAL__N_19topk_rowsILi17EEEvPKf": 28,
+                     "_ZN3dsa12_GLOBAL__N_114layer_prologueE": 212}
+    # The listed spill passes only at its listed size.
+    assert isa_check.unknown_spills(found) == {"_ZN3dsa12_GLOBAL__N_114layer_prologueE": 212}
+    assert isa_check.unknown_spills({"_ZN3dsa12_GLOBAL__N_19topk_rowsILi17EEEvPKf": 40}) != {}
+
+
 @pytest.mark.skipif(shutil.which("hipcc") is None and not isa_check.build.Path("/opt/rocm/bin/hipcc").exists(),
                     reason="needs hipcc")
-def test_library_has_no_mfma_in_unskipped_masked_blocks():
-    assert isa_check.check() == {}
+def test_library_has_no_mfma_in_unskipped_masked_blocks_and_no_new_spills():
+    mfma, spills = isa_check.analyse()
+    assert mfma == {}
+    assert spills == {}
