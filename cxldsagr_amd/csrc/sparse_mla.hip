@@ -13,7 +13,7 @@
 // in two roles:
 // * Score waves 0 and 1 compute S^T = K Q^T for all 32 keys and heads
 //   32 sw .. 32 sw + 31 with v_mfma_f32_32x32x16_bf16 (Q^T of their 32 heads
-//   stays in registers, 144 of them, as the B operand), and the online
+//   stays in 144 AGPRs, read by the MFMAs as the B operand), and the online
 //   softmax of their heads, writing P^T (bf16) and per-head rescale factors
 //   to LDS.
 // * Load waves 2 and 3 stage the records: lane (kk, j) (kk = 16 (w - 2) +
@@ -35,8 +35,8 @@
 // per step; four block buffers (S reads it, PV reads it - 2, it + 1 is
 // written); P and the rescale factors are double buffered by block parity.
 // The physical rows of the selection live in a ring of 8 blocks in LDS that
-// the load waves keep 6 blocks ahead (the id and page-table loads issued
-// two and one steps before use, ahead of the record loads).
+// the load waves keep 6 blocks ahead (the id and page-table loads each
+// land two steps before use, ahead of the record loads).
 //
 // Online softmax in log2 units with lazy rescaling (only when a block raises
 // a head's running max by more than 8, so p <= 2^8).
@@ -188,13 +188,18 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
   const int sw = wave & 1;           // score wave: heads 32 sw .. + 31
   const int n = lane & 31;           // score lane: head 32 sw + n
   const int h = lane >> 5;           // score lane: row half
-  // One register pool serves both roles, so that the allocator can give
-  // the two roles the same registers: Q^T operands on score waves (k-step
-  // ks: dims 16 ks + 8h), staged record bytes on load waves (fp8: two sets
-  // of kLoads at 0 and kLoads, bf16: one set).
-  constexpr int kPool = kQkDim / 16;
-  static_assert((kFp8 ? 2 : 1) * F::kLoads <= kPool, "staging does not fit the pool");
+  // Staged record bytes of the load waves (fp8: two sets of kLoads at 0 and
+  // kLoads, bf16: one set).
+  constexpr int kPool = (kFp8 ? 2 : 1) * F::kLoads;
   v4u pool[kPool];
+  // Q^T operands of the score waves (k-step ks: dims 16 ks + 8h), 144
+  // registers held in AGPRs: loaded straight into them, and read from
+  // there as the B operand of the S MFMAs, so that the score waves' VGPRs
+  // hold O^T, S, the softmax state and the operand read-ahead without
+  // spilling (in VGPRs, about ten of the 36 operands were reloaded from AGPR
+  // spill slots every step).
+  constexpr int kQOps = kQkDim / 16;
+  v4u q_ops[kQOps];
   float m_run = neg_inf;  // score lane: running max of its head (scaled)
   // Row sums of heads 16 wave + c (P^T against ones; every row alike).
   v4f l_acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
@@ -330,7 +335,10 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
   if (scorer) {
     const uint16_t* qrow = q + ((row * heads + head0 + 32 * sw + n) * kQkDim) + 8 * h;
 #pragma unroll
-    for (int ks = 0; ks < kPool; ++ks) pool[ks] = *reinterpret_cast<const v4u*>(qrow + 16 * ks);
+    for (int ks = 0; ks < kQOps; ++ks)
+      asm volatile("global_load_dwordx4 %0, %1, off" : "=a"(q_ops[ks]) : "v"(qrow + 16 * ks) : "memory");
+    // These loads are outside the compiler's load counting: wait here.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
   int32_t phys_next = -1;
   if (!scorer) {
@@ -506,7 +514,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
         if constexpr (kS) {
           const v8bf a = as_v8bf(ka[ks % kAheadK]);
           if (ks + kAheadK < kQkDim / 16) ka[ks % kAheadK] = lds_load<v4u>(kbase + 32 * (ks + kAheadK));
-          sa = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, as_v8bf(pool[ks]), sa, 0, 0, 0);
+          sa = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, as_v8bf(q_ops[ks]), sa, 0, 0, 0);
         }
         if (kHead > 0 && ks == kHead - 1) checks();
         const int kb = ks - kHead;
