@@ -391,10 +391,29 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
     if constexpr (kScore && kSoft)
       prow = lds_load<int32_t>(ring_base + 4 * (uint32_t)(((it - 1) % kRing) * kBlock + n));
     if constexpr (kPV) {
+      if constexpr (kScore) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
-        pb[t] = as_v8bf(lds_load<v4u>(p_base + par_pv * 4096 + (uint32_t)(t * 64 + lane) * 16));
-      p_own = as_v8bf(lds_load<v4u>(p_base + par_pv * 4096 + (uint32_t)(wave * 64 + lane) * 16));
+        for (int t = 0; t < 4; ++t)
+          pb[t] = as_v8bf(lds_load<v4u>(p_base + par_pv * 4096 + (uint32_t)(t * 64 + lane) * 16));
+        p_own = as_v8bf(lds_load<v4u>(p_base + par_pv * 4096 + (uint32_t)(wave * 64 + lane) * 16));
+      } else {
+        // Load waves: P^T straight into AGPRs (read from there as the MFMA
+        // B operand), which frees 20 VGPRs of the role that spills (its
+        // AGPR reloads per two steps 43 -> 27; layer -0.3 us). The reads go
+        // out before the V^T reads, so any wait that covers a V^T operand
+        // covers them too; the explicit wait below states it.
+        v4u t4[5];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const uint32_t addr = p_base + par_pv * 4096 + (uint32_t)(t * 64 + lane) * 16;
+          asm volatile("ds_read_b128 %0, %1" : "=a"(t4[t]) : "v"(addr) : "memory");
+        }
+        const uint32_t own = p_base + par_pv * 4096 + (uint32_t)(wave * 64 + lane) * 16;
+        asm volatile("ds_read_b128 %0, %1" : "=a"(t4[4]) : "v"(own) : "memory");
+#pragma unroll
+        for (int t = 0; t < 4; ++t) pb[t] = as_v8bf(t4[t]);
+        p_own = as_v8bf(t4[4]);
+      }
       vbase = lane_base(buf_of(it - 2), v_lane);
 #pragma unroll
       for (int d = 0; d < kAheadV; ++d) {
@@ -590,6 +609,8 @@ __global__ __launch_bounds__(kThreads, 1) void sparse_mla_fwd(
         }
       };
       checks();
+      // P^T of the load waves landed: 20 V^T reads follow them.
+      if constexpr (kPV) asm volatile("s_waitcnt lgkmcnt(15)" ::: "memory");
       constexpr int kQuarters = kS ? 32 : 0;
       constexpr int kSteps = kPvMfmas > kQuarters ? kPvMfmas : kQuarters;
 #pragma unroll
